@@ -1,0 +1,216 @@
+"""Benchmark of the matmul hot path on one MI355X; prints ONE JSON line.
+
+Metric (headline): SGEMM TFLOPS at 4096^3 fp32 + batch-1 GEMV GB/s (fraction of HBM peak)
++ decode tok/s.  `value` is the SGEMM figure: a step is one C = A*B, M = N = K = 4096, fp32
+row-major, A and B from the reference generator (srand(42), gpu_workload.c:81-82), computed
+by sgemm_opt through libswitchgpu.so.  W untimed warm-up steps, then exactly K timed steps
+between device synchronisations.  Inputs are resident in HBM before timing starts.
+
+Secondary figures measured in the same run (same JSON line):
+  gemv   -- fp16-weight GEMV on the Qwen2.5-0.5B lm_head shape [151936 x 896], rotating
+            four weight copies (1.09 GB) so every launch streams from HBM, not the MALL
+  decode -- random-init Qwen2.5-0.5B-architecture decode, 32-token prompt, 128 greedy tokens
+The CPU baseline is the oracle's serial-order SGEMM (row-parallel over the host cores) on a
+bounded sample of rows of the same 4096^3 problem.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "switch-l4t-gpu_amd"))
+
+import numpy as np  # noqa: E402
+
+import sgpu  # noqa: E402
+
+METRIC = "SGEMM TFLOPS @4096³ + GEMV GB/s (% of HBM peak); decode tok/s"
+PEAK_FP32_MATRIX_TFLOPS = 157.3      # MI355X dense fp32 matrix
+PEAK_HBM_GBPS = 8000.0               # MI355X HBM3E
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bench_sgemm(n, steps, warmup):
+    A, B = sgpu.gen_sgemm_inputs(n * n, 42)
+    dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((n, n))
+    run = lambda: sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, n, n, n, None)
+    for _ in range(max(warmup, 1)):
+        run()
+    sgpu.synchronize()
+    # correctness of what is timed: sampled rows against the oracle-free float64 product
+    C = dC.to_host()
+    rows = np.linspace(0, n - 1, 8).astype(int)
+    ref = A.reshape(n, n)[rows].astype(np.float64) @ B.reshape(n, n).astype(np.float64)
+    err = float(np.abs(C[rows] - ref).max() / np.abs(ref).max())
+    ev = sgpu.Events()
+    sgpu.synchronize()
+    t0 = time.perf_counter()
+    ev.record_start(None)
+    for _ in range(steps):
+        run()
+    ev.record_stop(None)
+    sgpu.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = ev.elapsed_ms() / steps
+    flops = 2.0 * n * n * n
+    return dict(wall_s=wall, kernel_ms=kernel_ms, flops=flops, err=err)
+
+
+def bench_gemv_lm_head(reps=20, copies=4):
+    N, K = 151936, 896
+    Wf, s = sgpu.gen_normal(N * K, 42, 0.0, 0.02)
+    W = sgpu.f32_to_f16(Wf)
+    del Wf
+    x, _ = sgpu.gen_normal(K, s, 0.0, 1.0)
+    dWs = [sgpu.DeviceArray.from_host(W) for _ in range(copies)]
+    dx, dy = sgpu.DeviceArray.from_host(x), sgpu.DeviceArray(N)
+    run = lambda i: sgpu.call("sgpu_gemv_h", dWs[i % copies].ptr, dx.ptr, None, dy.ptr, K, N, None)
+    for i in range(copies * 2):
+        run(i)
+    sgpu.synchronize()
+    y = dy.to_host()
+    rows = np.arange(0, N, 997)
+    Wd = W.reshape(N, K)[rows].view(np.float16).astype(np.float64)
+    Wd[np.abs(Wd) < 2.0 ** -14] = 0.0          # the h2f contract flushes fp16 subnormals
+    ref = Wd @ x.astype(np.float64)
+    err = float(np.abs(y[rows] - ref).max() / np.abs(ref).max())
+    ev = sgpu.Events()
+    ev.record_start(None)
+    for i in range(reps * copies):
+        run(i)
+    ev.record_stop(None)
+    us = ev.elapsed_ms() * 1e3 / (reps * copies)
+    algo_bytes = 2.0 * N * K + 4.0 * K + 4.0 * N
+    return dict(us=us, bytes=algo_bytes, gbps=algo_bytes / (us * 1e-6) / 1e9, err=err, copies=copies)
+
+
+def bench_decode(prompt_len=32, gen=128):
+    cfg = sgpu.qwen_default_cfg()
+    t = time.perf_counter()
+    blob = sgpu.qwen_random_blob(cfg, seed=2024, std=0.02)
+    eng = sgpu.QwenEngine(cfg, blob)
+    del blob
+    log(f"decode: weights built and uploaded in {time.perf_counter() - t:.1f} s")
+    ids = [int(v) for v in np.random.default_rng(32).integers(0, cfg.V, prompt_len)]
+    for p, tok in enumerate(ids):
+        logits = eng.forward(tok, p, p == prompt_len - 1)
+    nxt = int(np.argmax(logits))
+    sgpu.synchronize()
+    t0 = time.perf_counter()
+    for g in range(gen):
+        logits = eng.forward(nxt, prompt_len + g, True)
+        nxt = int(np.argmax(logits))
+    dt = time.perf_counter() - t0
+    eng.close()
+    per_layer = (cfg.C + (cfg.C + 2 * cfg.NKV * cfg.HD) * cfg.C + cfg.C * cfg.C + cfg.C
+                 + 2 * cfg.FC * cfg.C + cfg.C * cfg.FC) * 2 + (cfg.C + 2 * cfg.NKV * cfg.HD) * 4
+    bytes_tok = per_layer * cfg.NL + 2 * cfg.V * cfg.C + 2 * cfg.C
+    tps = gen / dt
+    return dict(tok_s=tps, ms_per_tok=dt / gen * 1e3, bytes_per_token=bytes_tok,
+                hbm_floor_frac=bytes_tok * tps / (PEAK_HBM_GBPS * 1e9), prompt=prompt_len, generated=gen)
+
+
+def cpu_baseline(n, target_s=1.5):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    A, B = sgpu.gen_sgemm_inputs(n * n, 42)
+    rows = threads
+    t = time.perf_counter()
+    oracle.sgemm_rows(A, B, n, n, n, 0, rows, threads)
+    dt = time.perf_counter() - t
+    rows = int(min(n, max(threads, rows * target_s / max(dt, 1e-3))))
+    rows -= rows % threads or 0
+    rows = max(rows, threads)
+    t = time.perf_counter()
+    oracle.sgemm_rows(A, B, n, n, n, 0, rows, threads)
+    dt = time.perf_counter() - t
+    tflops = 2.0 * rows * n * n / dt / 1e12
+    return dict(value=tflops, unit="TFLOP/s", cores=threads, kind="port",
+                sample=f"oracle og_sgemm_rows (serial k-order fp32, -O2 -ffp-contract=off), rows 0..{rows - 1} "
+                       f"of the {n}^3 SGEMM ({2.0 * rows * n * n / 1e9:.1f} GFLOP), {dt:.2f} s on {threads} threads")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
+              f"multi-GPU path; run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("--steps must be >= 1 and --warmup >= 0")
+
+    sgpu.init(0)
+    props = sgpu.device_props(0)
+    log(f"device: {props.name.decode()} ({props.arch.decode()}), {props.compute_units} CUs, "
+        f"{props.clock_khz / 1e3:.0f} MHz")
+    n = 4096
+    sg = bench_sgemm(n, args.steps, args.warmup)
+    tflops = sg["flops"] * args.steps / sg["wall_s"] / 1e12
+    achieved = sg["flops"] / (sg["kernel_ms"] * 1e-3) / 1e12
+    log(f"sgemm_opt {n}^3: {sg['kernel_ms']:.3f} ms/launch, {achieved:.1f} TFLOP/s kernel, "
+        f"{tflops:.1f} TFLOP/s wall, normwise err {sg['err']:.2e}")
+    gv = bench_gemv_lm_head()
+    log(f"gemv_h lm_head: {gv['us']:.1f} us, {gv['gbps']:.0f} GB/s ({gv['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), "
+        f"err {gv['err']:.2e}")
+    dec = None
+    if not args.no_decode:
+        dec = bench_decode()
+        log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['ms_per_tok']:.3f} ms/token, "
+            f"{dec['hbm_floor_frac']:.1%} of the HBM floor)")
+    cpu = None if args.no_cpu else cpu_baseline(n)
+    traffic = {}
+    if os.path.exists(PROFILE_TRAFFIC):
+        traffic = json.load(open(PROFILE_TRAFFIC))
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sg["wall_s"] / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "SGEMM C=A*B M=N=K=4096 fp32 row-major, A,B from srand(42) "
+                               "(rand()%2000-1000)/1000, alpha=1 beta=0, kernel sgemm_opt",
+                   "M": n, "N": n, "K": n, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MATRIX_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),
+                     "traffic": traffic.get("sgemm_opt_4096")},
+        "cpu_baseline": cpu,
+        "gemv": {"kernel": "gemv_h (fp16 weights, fp32 x/y)", "shape": [151936, 896],
+                 "us_per_call": round(gv["us"], 3), "gbps": round(gv["gbps"], 1),
+                 "roofline": {"bound": "hbm", "achieved": round(gv["gbps"], 1), "peak": PEAK_HBM_GBPS,
+                              "unit": "GB/s", "frac": round(gv["gbps"] / PEAK_HBM_GBPS, 4),
+                              "traffic": traffic.get("gemv_h_lm_head")},
+                 "weight_copies_rotated": gv["copies"], "normwise_err": gv["err"]},
+        "decode": None if dec is None else {
+            "model": "Qwen2.5-0.5B architecture, random-init N(0,0.02) fp16 weights",
+            "tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4),
+            "prompt": dec["prompt"], "generated": dec["generated"],
+            "bytes_per_token": dec["bytes_per_token"], "hbm_floor_frac": round(dec["hbm_floor_frac"], 4)},
+        "sgemm_normwise_err": sg["err"],
+        "device": props.name.decode(),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,202 @@
+/* switch_gpu.h -- C ABI of libswitchgpu.so, the MI355X (gfx950) matmul hot path.
+ *
+ * Drop-in for the reference's driver-API path: the SGEMM family of switch_gpu.cu, the
+ * fp32 / fp16-weight batch-1 GEMV kernels of gpu-llm/kernels, and the host calls that
+ * load and launch them (cuda_drv.h:14-32 and the per-file copies of those prototypes,
+ * e.g. gpu_workload.c:19-31, qwen_engine.c:27-39).
+ *
+ * Conventions (kept from the reference, cuda_drv.h:9-40):
+ *  - Every call returns an int status, 0 on success.  Positive values are hipError_t
+ *    codes from the HIP runtime; negative values are this library's own (SGPU_ERR_*).
+ *    sgpu_error_string() names both (cuGetErrorString role).
+ *  - All buffer arguments are device pointers unless stated otherwise; sizes are element
+ *    counts as in the reference kernels (ints, K before N in GEMV calls).  Sub-buffers
+ *    are plain byte offsets from a device pointer.
+ *  - The caller owns all memory; nothing here allocates except sgpu_malloc and the engine
+ *    object (sgpu_qwen_*).  Outputs are fully overwritten (no accumulate-into-y/C).
+ *  - `stream` is a hipStream_t passed as void*; NULL is the default stream, as the
+ *    reference's cuLaunchKernel(..., NULL, ...) calls use.  Launchers are asynchronous.
+ *  - bias pointers are nullable wherever the reference kernel reads `bias ? bias[n] : 0`.
+ *
+ * Launchers pick their own wave64 launch geometry; the code objects they use can also be
+ * loaded by callers that resolve kernels by name (sgpu_code_object + hipModuleLoadData).
+ */
+#ifndef SWITCH_GPU_H
+#define SWITCH_GPU_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define SGPU_OK 0
+#define SGPU_ERR_INVALID_ARG (-1)    /* a size, pointer or shape the call cannot accept */
+#define SGPU_ERR_NOT_INITIALIZED (-2) /* sgpu_init has not succeeded on the current device */
+#define SGPU_ERR_NO_KERNEL (-3)      /* a code object lacks a kernel the call needs */
+#define SGPU_ERR_NO_DEVICE (-4)      /* no usable HIP device */
+#define SGPU_ERR_HOST_ALLOC (-5)     /* host memory exhausted */
+
+/* Replaces cuGetErrorString (cuda_drv.h:31).  Never NULL. */
+const char *sgpu_error_string(int status);
+
+/* ---- runtime: device, memory, synchronisation (cuda_drv.h:14-30) ---- */
+
+/* Replaces cuInit + cuDeviceGet + cuCtxCreate_v2 + cuModuleLoadData + cuModuleGetFunction
+ * (gpu_workload.c:65-74, qwen_engine.c:144-155): makes `device` current and loads every
+ * embedded gfx950 code object on it, resolving all kernels.  Idempotent per device. */
+int sgpu_init(int device);
+/* cuDeviceGetCount (cuda_drv.h:16). */
+int sgpu_device_count(int *count);
+
+typedef struct {
+    char name[256];           /* marketing name, e.g. "AMD Instinct MI355X" */
+    char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int compute_units;        /* CU count (cuDeviceGetAttribute SM_COUNT role) */
+    int clock_khz;            /* peak shader clock (CU_ATTR_CLOCK_KHZ role) */
+    int memory_clock_khz;
+    int memory_bus_width;     /* bits */
+    size_t total_mem;         /* bytes (cuDeviceTotalMem_v2 role) */
+    size_t lds_per_block;     /* bytes */
+    int l2_bytes;
+    int warp_size;            /* 64 on CDNA */
+} sgpu_device_props;
+/* cuDeviceGetName / cuDeviceTotalMem_v2 / cuDeviceGetAttribute (cuda_drv.h:17-19). */
+int sgpu_get_device_props(int device, sgpu_device_props *props);
+
+int sgpu_malloc(void **dptr, size_t bytes);                          /* cuMemAlloc_v2 */
+int sgpu_free(void *dptr);                                           /* cuMemFree_v2 */
+int sgpu_memcpy_htod(void *dst, const void *src, size_t bytes);      /* cuMemcpyHtoD_v2 */
+int sgpu_memcpy_dtoh(void *dst, const void *src, size_t bytes);      /* cuMemcpyDtoH_v2 */
+int sgpu_memcpy_dtod(void *dst, const void *src, size_t bytes);      /* cuMemcpyDtoD_v2 (qwen_engine.c:229-230) */
+int sgpu_memcpy_dtod_async(void *dst, const void *src, size_t bytes, void *stream);
+int sgpu_memset_d8(void *dst, int value, size_t bytes);              /* synchronous byte fill */
+int sgpu_synchronize(void);                                          /* cuCtxSynchronize */
+int sgpu_stream_synchronize(void *stream);
+
+/* Timing with HIP events on a stream (the reference times with CLOCK_MONOTONIC around a
+ * synchronised batch, gpu_workload.c:133-139; events time the stream itself). */
+int sgpu_event_create(void **event);
+int sgpu_event_destroy(void *event);
+int sgpu_event_record(void *event, void *stream);
+int sgpu_event_elapsed_ms(float *ms, void *start, void *stop);
+
+/* ---- code objects (the PTX modules' role: switch_gpu.ptx, gemv.ptx, gpt2.ptx, qwen.ptx) ----
+ * Returns the embedded gfx950 ELF code object named "switch_gpu", "gemv", "gpt2_kernels",
+ * "qwen_kernels" or "sgpu_tuned" (and its size), ready for hipModuleLoadData; NULL if the
+ * name is unknown.  The first four export the reference's kernel names and arguments. */
+const void *sgpu_code_object(const char *name, size_t *size);
+
+/* Launch geometry the launchers use for a reference-named kernel at a given shape
+ * (SGEMM: M, N, K; GEMV family: N rows, K columns, M unused).  Lets a host that keeps its
+ * own hipModuleLaunchKernel calls (the gpu_workload flow) launch the code objects with the
+ * kernels' intended wave64 geometry.  Returns SGPU_ERR_NO_KERNEL for an unknown name. */
+int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[3], unsigned block[3]);
+
+/* ---- SGEMM family: C = A*B, fp32 row-major, alpha 1, beta 0 ----
+ * A: MxK (stride K), B: KxN (stride N), C: MxN (stride N).  Any M, N, K >= 0 (the
+ * reference kernels require multiples of 32/64, switch_gpu.cu:58,98).
+ * Replaces cuLaunchKernel(sgemm_*, ...) at gpu_workload.c:90,117,142,168; kernel
+ * signatures switch_gpu.cu:5-8 (sgemm_tiled), :59-62 (sgemm_tiled4), :99-102 (sgemm_opt),
+ * :140-143 (sgemm_naive). */
+int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+
+/* Read-bandwidth probe, membw_read4 (switch_gpu.cu:41-54; launched gpu_workload.c:210-213):
+ * every thread sums its grid-stride float4 sweep `iters` times into out[first index].
+ * buf: n4 float4 (16-byte aligned); out: one float per launched thread with index < n4.
+ * `threads` returns the launched thread count (may be NULL). */
+int sgpu_membw_read4(const void *buf, float *out, int n4, int iters, int *threads, void *stream);
+
+/* ---- batch-1 GEMV, fp32 weights: y[n] = sum_k W[n*K+k] x[k] (+ bias[n]) ----
+ * W: NxK row-major.  Any K (the reference float4 kernels need K % 4 == 0).
+ * gemv / gemv4 / gemv_warp: gemv.cu:3-6,18-21,51-54 and gpt2_kernels.cu:38-41, launched
+ * gemv_test.c:109 and gpt2_engine.c:188,214,230,243,260.  gemv_warp_b: gpt2_kernels.cu:75-79,
+ * launched gpt2_engine.c:185,211,227,240 (bias nullable here). */
+int sgpu_gemv(const float *W, const float *x, float *y, int K, int N, void *stream);
+int sgpu_gemv4(const float *W, const float *x, float *y, int K, int N, void *stream);
+int sgpu_gemv_warp(const float *W, const float *x, float *y, int K, int N, void *stream);
+int sgpu_gemv_warp_b(const float *W, const float *x, const float *bias, float *y, int K, int N,
+                     void *stream);
+
+/* Weight-stationary batched GEMV, gemv_multi (gpt2_kernels.cu:110-155, launched
+ * gpt2_engine.c:280,295,304,311): Y[t*N+n] = W[n,:].X[t,:] + (bias ? bias[n] : 0), X: TxK. */
+int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N, int T,
+                    void *stream);
+
+/* fp16-weight GEMV, gemv_h (qwen_kernels.cu:34-38, launched qwen_engine.c:219,242,249,256,265):
+ * W holds fp16 bit patterns decoded with the reference h2f (qwen_kernels.cu:6-14), x and
+ * bias are fp32, bias nullable.  Any K (the reference needs K % 4 == 0). */
+int sgpu_gemv_h(const uint16_t *W, const float *x, const float *bias, float *y, int K, int N,
+                void *stream);
+
+/* ---- Qwen2.5 decode support kernels (qwen_kernels.cu:72-189), launched per layer by
+ * gpu_forward (qwen_engine.c:216-264). ---- */
+/* rows independent rows of n; w fp16 bits (qwen_kernels.cu:74-93, grid = rows). */
+int sgpu_rmsnorm(const float *x, const uint16_t *w, float *y, int n, float eps, int rows, void *stream);
+/* qwen_kernels.cu:97-116, launched qwen_engine.c:222-226. */
+int sgpu_rope(float *x, const float *cosT, const float *sinT, int T, int H, int HD, int pos0, void *stream);
+/* qwen_kernels.cu:119-126, launched qwen_engine.c:253-254. */
+int sgpu_swiglu(const float *g, const float *u, float *y, int n, void *stream);
+/* qwen_kernels.cu:130-144, launched qwen_engine.c:231-232. */
+int sgpu_attn_scores_gqa(const float *q, const float *kc, float *scores, int T, float scale, int NH, int KV,
+                         int HD, void *stream);
+/* qwen_kernels.cu:147-164, launched qwen_engine.c:233-234. */
+int sgpu_attn_softmax(const float *scores, float *probs, int T, int NH, void *stream);
+/* qwen_kernels.cu:167-180, launched qwen_engine.c:235-236. */
+int sgpu_attn_mix_gqa(const float *probs, const float *vc, float *out, int T, int NH, int KV, int HD,
+                      void *stream);
+/* qwen_kernels.cu:183-189, launched qwen_engine.c:244,258. */
+int sgpu_add2(const float *a, const float *b, float *out, int n, void *stream);
+
+/* ---- Qwen2.5 decode engine (qwen_engine.c:105-269): weights resident on the device,
+ * fp32 KV cache, the reference's per-layer launch sequence per position. ---- */
+typedef struct {
+    int V, C, NL, NH, NKV, HD, FC, CTX;
+    float eps;       /* RMSNorm eps (qwen_engine.c:55: 1e-6) */
+    float theta;     /* RoPE base used by the weight writer (conv_qwen.py:27: 1e6) */
+} sgpu_qwen_cfg;
+/* The Qwen2.5-0.5B dims of qwen_engine.c:43-55 (V 151936, C 896, 24 layers, 14/2 heads,
+ * HD 64, FC 4864, CTX 8192). */
+void sgpu_qwen_default_cfg(sgpu_qwen_cfg *cfg);
+/* Byte size of the flat weight file (qwen_engine.c:61-67 layout). */
+size_t sgpu_qwen_file_bytes(const sgpu_qwen_cfg *cfg);
+/* Fill a host blob of sgpu_qwen_file_bytes() with a random-init model in that layout:
+ * every fp16 tensor N(0, std) from the seeded LCG + Box-Muller (cast to fp16 RNE), RoPE
+ * tables from conv_qwen.py:75-80 (float64 angles, stored fp32). */
+int sgpu_qwen_fill_random(void *blob, const sgpu_qwen_cfg *cfg, uint64_t seed, float std);
+
+typedef struct sgpu_qwen sgpu_qwen;
+/* gpu_setup (qwen_engine.c:137-189): uploads the host blob, allocates KV caches and
+ * activation buffers on the current device. */
+int sgpu_qwen_create(sgpu_qwen **engine, const sgpu_qwen_cfg *cfg, const void *blob);
+void sgpu_qwen_destroy(sgpu_qwen *engine);
+/* gpu_forward (qwen_engine.c:205-269): token at `pos` (cache holds 0..pos-1 and gains pos).
+ * If want_logits, the V logits are copied to host `logits_host` (may be NULL to leave them on
+ * the device).  Synchronous when logits are requested, asynchronous otherwise. */
+int sgpu_qwen_forward(sgpu_qwen *engine, int token, int pos, int want_logits, float *logits_host);
+/* Device pointer to the last logits (V floats). */
+const float *sgpu_qwen_device_logits(const sgpu_qwen *engine);
+
+/* ---- seeded input generators (host only; no device needed) ----
+ * gpu_workload.c:81-82: srand(seed); A[i], B[i] interleaved = (rand()%2000 - 1000)/1000.0f. */
+void sgpu_gen_sgemm_inputs(float *A, float *B, size_t count, unsigned seed);
+/* gemv_test.c:46-50 LCG: s = s*6364136223846793005 + 1442695040888963407,
+ * value ((s >> 40) & 0xFFFFFF) / 2^24 in [0, 1). */
+float sgpu_frand(uint64_t *state);
+/* n values frand() + offset (gemv_test.c:80-81 uses offset -0.5). */
+void sgpu_gen_uniform(float *out, size_t n, uint64_t *state, float offset);
+/* n values mean + std * N(0,1), Box-Muller on two frand() draws (cosine branch). */
+void sgpu_gen_normal(float *out, size_t n, uint64_t *state, float mean, float std);
+/* fp32 -> fp16 bits, round to nearest even (overflow to inf, subnormals kept). */
+void sgpu_f32_to_f16(const float *in, uint16_t *out, size_t n);
+/* fp16 bits -> fp32 with the reference h2f contract (qwen_engine.c:90-98). */
+float sgpu_h2f_host(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SWITCH_GPU_H */

@@ -1,0 +1,251 @@
+// gemv_core.h -- batch-1 GEMV kernels for gfx950, fp32 and fp16-bit weights.
+//
+//   y[n] = sum_k W[n*K + k] * x[k] + (bias ? bias[n] : 0)      W: N x K row-major
+//
+// This is HBM streaming work (one flop per weight byte for fp16): the kernels are built to
+// keep enough 128-bit weight loads in flight per CU, not to reach the matrix cores.
+//
+// Two shapes of kernel:
+//  * gemv_generic: a wave per row, lanes striding the row in 16-byte segments, x read
+//    through the vector L1.  Any K, any pointer alignment (scalar path when a row is not
+//    16-byte aligned), any grid (wave-granular grid-stride).  Backs the reference-named
+//    symbols so hosts that keep the reference's own launch geometry stay correct.
+//  * gemv_xreg<LPR, S>: a team of LPR lanes per row (16, 64 or 256 = four waves split-K),
+//    each lane owning up to S fixed 16-byte segments of every row.  The lane's slice of x
+//    (S*VEC floats) is loaded once into VGPRs and reused for every row of a persistent
+//    grid-stride loop; all S weight loads of a row are issued before the first FMA.
+//    Lane partials are combined with DPP row shifts/broadcasts (no LDS, no barrier) and,
+//    for 256-lane teams, one LDS exchange across the four waves.
+// Weights are read with the nontemporal hint: each byte is used exactly once per call.
+#pragma once
+#include "sgpu_device.h"
+
+namespace sgpu {
+
+// Weight element traits: 16 bytes = 4 fp32 or 8 fp16.
+struct WF32 {
+    typedef float elem;
+    typedef sgpu_f32x4 vec;
+    static constexpr int VEC = 4;
+    __device__ static __forceinline__ float dot(const vec& w, const float* xv, float acc) {
+        acc = __builtin_fmaf(w[0], xv[0], acc);
+        acc = __builtin_fmaf(w[1], xv[1], acc);
+        acc = __builtin_fmaf(w[2], xv[2], acc);
+        acc = __builtin_fmaf(w[3], xv[3], acc);
+        return acc;
+    }
+    __device__ static __forceinline__ float one(elem w) { return w; }
+};
+struct WF16 {
+    typedef uint16_t elem;
+    typedef sgpu_u32x4 vec;
+    static constexpr int VEC = 8;
+    __device__ static __forceinline__ float dot(const vec& w, const float* xv, float acc) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc = __builtin_fmaf(sgpu_h2f_lo(w[i]), xv[2 * i], acc);
+            acc = __builtin_fmaf(sgpu_h2f_hi(w[i]), xv[2 * i + 1], acc);
+        }
+        return acc;
+    }
+    __device__ static __forceinline__ float one(elem w) { return sgpu_h2f(w); }
+};
+
+// ---------------------------------------------------------------------------------------
+// Generic: wave per row.
+template <class WT>
+__device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict__ W,
+                                             const float* __restrict__ x,
+                                             const float* __restrict__ bias,
+                                             float* __restrict__ y, int K, int N) {
+    typedef typename WT::vec vec;
+    constexpr int VEC = WT::VEC;
+    const int lane = sgpu_tid() & 63;
+    const int wave = (sgpu_bid() * sgpu_nthreads() + sgpu_tid()) >> 6;
+    const int nwaves = (sgpu_nblocks() * sgpu_nthreads()) >> 6;
+    if (((sgpu_nthreads()) & 63) != 0) {
+        // Partial waves cannot run the DPP reduction: fall back to one thread per row.
+        const int t = sgpu_bid() * sgpu_nthreads() + sgpu_tid();
+        const int nt = sgpu_nblocks() * sgpu_nthreads();
+        for (int n = t; n < N; n += nt) {
+            const typename WT::elem* row = W + (size_t)n * K;
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
+            y[n] = acc + (bias ? bias[n] : 0.0f);
+        }
+        return;
+    }
+    const bool vec_ok = (K % VEC == 0) && ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0;
+    const int nseg = K / VEC;
+    for (int n = wave; n < N; n += nwaves) {          // wave-uniform loop: no barriers inside
+        const typename WT::elem* row = W + (size_t)n * K;
+        float acc = 0.0f;
+        if (vec_ok) {
+            const vec* rv = reinterpret_cast<const vec*>(row);
+            const sgpu_f32x4* xv4 = reinterpret_cast<const sgpu_f32x4*>(x);
+            int s = lane;
+            for (; s + 64 < nseg; s += 128) {         // two segments in flight per lane
+                const vec w0 = sgpu_ldnt(rv + s), w1 = sgpu_ldnt(rv + s + 64);
+                float xa[VEC], xb[VEC];
+#pragma unroll
+                for (int q = 0; q < VEC / 4; q++) {
+                    const sgpu_f32x4 a = xv4[s * (VEC / 4) + q], b = xv4[(s + 64) * (VEC / 4) + q];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) { xa[4 * q + e] = a[e]; xb[4 * q + e] = b[e]; }
+                }
+                acc = WT::dot(w0, xa, acc);
+                acc = WT::dot(w1, xb, acc);
+            }
+            for (; s < nseg; s += 64) {
+                const vec w0 = sgpu_ldnt(rv + s);
+                float xa[VEC];
+#pragma unroll
+                for (int q = 0; q < VEC / 4; q++) {
+                    const sgpu_f32x4 a = xv4[s * (VEC / 4) + q];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) xa[4 * q + e] = a[e];
+                }
+                acc = WT::dot(w0, xa, acc);
+            }
+        } else {
+            for (int k = lane; k < K; k += 64) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
+        }
+        acc = sgpu_group_sum<64>(acc);
+        if (lane == 63) y[n] = acc + (bias ? bias[n] : 0.0f);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Tuned: team of LPR lanes per row, x slice in VGPRs, persistent over rows.
+// Preconditions (checked by the launcher): blockDim == 256, K % VEC == 0, W and x 16-byte
+// aligned, K/VEC <= S*LPR.
+template <class WT, int LPR, int S>
+__device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ W,
+                                          const float* __restrict__ x,
+                                          const float* __restrict__ bias,
+                                          float* __restrict__ y, int K, int N) {
+    static_assert(LPR == 16 || LPR == 32 || LPR == 64 || LPR == 128 || LPR == 256, "team size");
+    typedef typename WT::vec vec;
+    constexpr int VEC = WT::VEC;
+    constexpr int NT = 256;
+    constexpr int TEAMS = NT / LPR;                   // rows per block iteration
+    constexpr int WAVES_PER_TEAM = LPR > 64 ? LPR / 64 : 1;
+    __shared__ float red[NT / 64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int team = tid / LPR, sub = tid % LPR;
+    const int nseg = K / VEC;
+
+    // This lane's x slice: segments sub, sub+LPR, ..., kept for every row.
+    float xr[S][VEC];
+    bool has[S];
+#pragma unroll
+    for (int j = 0; j < S; j++) {
+        const int seg = sub + LPR * j;
+        has[j] = seg < nseg;
+        const sgpu_f32x4* xv4 = reinterpret_cast<const sgpu_f32x4*>(x) + (size_t)seg * (VEC / 4);
+#pragma unroll
+        for (int q = 0; q < VEC / 4; q++) {
+            const sgpu_f32x4 a = has[j] ? xv4[q] : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) xr[j][4 * q + e] = a[e];
+        }
+    }
+
+    for (int rb = blockIdx.x; rb * TEAMS < N; rb += gridDim.x) {   // block-uniform loop
+        const int n = rb * TEAMS + team;
+        float acc = 0.0f;
+        if (n < N) {
+            const vec* rv = reinterpret_cast<const vec*>(W + (size_t)n * K) + sub;
+            vec w[S];
+#pragma unroll
+            for (int j = 0; j < S; j++)
+                if (has[j]) w[j] = sgpu_ldnt(rv + LPR * j);
+#pragma unroll
+            for (int j = 0; j < S; j++)
+                if (has[j]) acc = WT::dot(w[j], xr[j], acc);
+        }
+        if constexpr (LPR <= 64) {
+            acc = sgpu_group_sum<LPR>(acc);
+            if (sub == LPR - 1 && n < N) y[n] = acc + (bias ? bias[n] : 0.0f);
+        } else {
+            acc = sgpu_group_sum<64>(acc);
+            if (lane == 63) red[wave] = acc;
+            __syncthreads();
+            if (sub == 0 && n < N) {
+                float s = 0.0f;
+#pragma unroll
+                for (int i = 0; i < WAVES_PER_TEAM; i++) s += red[team * WAVES_PER_TEAM + i];
+                y[n] = s + (bias ? bias[n] : 0.0f);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Weight-stationary batched GEMV (gemv_multi role): Y[t*N+n] = W[n,:].X[t,:] + bias?[n].
+// A wave owns one row and a chunk of up to TW tokens: the row is streamed once per chunk
+// while TW register accumulators collect the chunk's dot products.
+template <int TW>
+__device__ __forceinline__ void gemv_multi_f32(const float* __restrict__ W, const float* __restrict__ X,
+                                               const float* __restrict__ bias, float* __restrict__ Y,
+                                               int K, int N, int T) {
+    if ((sgpu_nthreads() & 63) != 0) {
+        // Partial waves: one thread per (row, token), serial dot product.
+        const int t0 = sgpu_bid() * sgpu_nthreads() + sgpu_tid();
+        const int nt = sgpu_nblocks() * sgpu_nthreads();
+        for (long long i = t0; i < (long long)N * T; i += nt) {
+            const int n = (int)(i % N), t = (int)(i / N);
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc = __builtin_fmaf(W[(size_t)n * K + k], X[(size_t)t * K + k], acc);
+            Y[(size_t)t * N + n] = acc + (bias ? bias[n] : 0.0f);
+        }
+        return;
+    }
+    const int lane = sgpu_tid() & 63;
+    const int wave = (blockIdx.x * sgpu_nthreads() + sgpu_tid()) >> 6;
+    const int nwaves = (gridDim.x * sgpu_nthreads()) >> 6;
+    const bool vec_ok = (K % 4 == 0) && ((((uintptr_t)W) | ((uintptr_t)X)) & 15) == 0;
+    const int nseg = K / 4;
+    for (int c = blockIdx.y; c * TW < T; c += gridDim.y) {
+        const int t0 = c * TW;
+        const int tn = min(TW, T - t0);
+        for (int n = wave; n < N; n += nwaves) {
+            float acc[TW];
+#pragma unroll
+            for (int j = 0; j < TW; j++) acc[j] = 0.0f;
+            if (vec_ok) {
+                const sgpu_f32x4* wr = reinterpret_cast<const sgpu_f32x4*>(W + (size_t)n * K);
+                for (int s = lane; s < nseg; s += 64) {
+                    const sgpu_f32x4 w = sgpu_ldnt(wr + s);
+#pragma unroll
+                    for (int j = 0; j < TW; j++)
+                        if (j < tn) {
+                            const sgpu_f32x4 v = *reinterpret_cast<const sgpu_f32x4*>(X + (size_t)(t0 + j) * K + 4 * s);
+                            acc[j] = __builtin_fmaf(w[0], v[0], acc[j]);
+                            acc[j] = __builtin_fmaf(w[1], v[1], acc[j]);
+                            acc[j] = __builtin_fmaf(w[2], v[2], acc[j]);
+                            acc[j] = __builtin_fmaf(w[3], v[3], acc[j]);
+                        }
+                }
+            } else {
+                for (int k = lane; k < K; k += 64) {
+                    const float w = W[(size_t)n * K + k];
+#pragma unroll
+                    for (int j = 0; j < TW; j++)
+                        if (j < tn) acc[j] = __builtin_fmaf(w, X[(size_t)(t0 + j) * K + k], acc[j]);
+                }
+            }
+            const float b = bias ? bias[n] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < TW; j++) {
+                const float s = sgpu_group_sum<64>(acc[j]);
+                if (j < tn && lane == 63) Y[(size_t)(t0 + j) * N + n] = s + b;
+            }
+        }
+    }
+}
+
+}  // namespace sgpu

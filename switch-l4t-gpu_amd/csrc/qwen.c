@@ -1,0 +1,250 @@
+/* qwen.c -- Qwen2.5 decode engine over the C-ABI launchers (part of libswitchgpu.so).
+ *
+ * The device side of qwen_engine.c: weight upload and buffers (gpu_setup, :137-189) and
+ * the per-position forward (gpu_forward, :205-269) with the reference's per-layer launch
+ * sequence -- rmsnorm, gemv_h qkv (+bias), rope q, rope k, K/V cache writes, attention
+ * scores / softmax / mix, gemv_h o, residual add, rmsnorm, gemv_h gate|up, swiglu, gemv_h
+ * down, residual add -- then final rmsnorm and the tied lm_head gemv_h.
+ * Layout of the flat weight file: qwen_engine.c:8-16,61-75 (writer conv_qwen.py:63-99).
+ */
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "sgpu_internal.h"
+#include "switch_gpu.h"
+
+typedef struct {
+    size_t off_emb, off_cos, off_sin, l_base, lstride, off_lnfw, bytes;      /* bytes */
+    size_t li_inln, li_qkvw, li_qkvb, li_ow, li_postln, li_gateup, li_down;  /* halves */
+    int kvd, qkvd;
+} qlayout;
+
+static void q_layout(const sgpu_qwen_cfg *c, qlayout *L) {
+    L->kvd = c->NKV * c->HD;
+    L->qkvd = c->C + 2 * L->kvd;
+    L->off_emb = 0;
+    L->off_cos = (size_t)c->V * c->C * 2;
+    L->off_sin = L->off_cos + (size_t)c->CTX * (c->HD / 2) * 4;
+    L->l_base = L->off_sin + (size_t)c->CTX * (c->HD / 2) * 4;
+    L->lstride = ((size_t)c->C + (size_t)L->qkvd * c->C + L->qkvd + (size_t)c->C * c->C + c->C +
+                  (size_t)2 * c->FC * c->C + (size_t)c->C * c->FC) * 2;
+    L->off_lnfw = L->l_base + (size_t)c->NL * L->lstride;
+    L->bytes = L->off_lnfw + (size_t)c->C * 2;
+    L->li_inln = 0;
+    L->li_qkvw = (size_t)c->C;
+    L->li_qkvb = (size_t)c->C + (size_t)L->qkvd * c->C;
+    L->li_ow = L->li_qkvb + L->qkvd;
+    L->li_postln = L->li_ow + (size_t)c->C * c->C;
+    L->li_gateup = L->li_postln + c->C;
+    L->li_down = L->li_gateup + (size_t)2 * c->FC * c->C;
+}
+
+static int cfg_ok(const sgpu_qwen_cfg *c) {
+    return c && c->V > 0 && c->C > 0 && c->NL > 0 && c->NH > 0 && c->NKV > 0 && c->HD > 0 &&
+           c->HD % 2 == 0 && c->NH % c->NKV == 0 && c->FC > 0 && c->CTX > 0 &&
+           (long long)c->CTX * c->NH < 0x7fffffffLL;
+}
+
+void sgpu_qwen_default_cfg(sgpu_qwen_cfg *c) {
+    /* qwen_engine.c:43-55, conv_qwen.py:23-27 */
+    c->V = 151936; c->C = 896; c->NL = 24; c->NH = 14; c->NKV = 2; c->HD = 64; c->FC = 4864;
+    c->CTX = 8192; c->eps = 1e-6f; c->theta = 1e6f;
+}
+
+size_t sgpu_qwen_file_bytes(const sgpu_qwen_cfg *cfg) {
+    if (!cfg_ok(cfg)) return 0;
+    qlayout L;
+    q_layout(cfg, &L);
+    return L.bytes;
+}
+
+/* N(0, std) fp16 for n halves at dst, continuing the LCG stream. */
+static int fill_h(uint16_t *dst, size_t n, uint64_t *state, float std, float *tmp, size_t tmp_n) {
+    for (size_t done = 0; done < n;) {
+        size_t c = n - done < tmp_n ? n - done : tmp_n;
+        sgpu_gen_normal(tmp, c, state, 0.0f, std);
+        sgpu_f32_to_f16(tmp, dst + done, c);
+        done += c;
+    }
+    return 0;
+}
+
+int sgpu_qwen_fill_random(void *blob, const sgpu_qwen_cfg *c, uint64_t seed, float std) {
+    if (!blob || !cfg_ok(c)) return SGPU_ERR_INVALID_ARG;
+    qlayout L;
+    q_layout(c, &L);
+    const size_t tmp_n = (size_t)1 << 22;   /* even: chunks continue the pair stream exactly */
+    float *tmp = malloc(tmp_n * sizeof(float));
+    if (!tmp) return SGPU_ERR_HOST_ALLOC;
+    unsigned char *b = (unsigned char *)blob;
+    uint64_t s = seed;
+    fill_h((uint16_t *)(b + L.off_emb), (size_t)c->V * c->C, &s, std, tmp, tmp_n);
+    /* RoPE tables, conv_qwen.py:75-80: freq_d = theta^(-2d/HD), angle = pos*freq_d (float64). */
+    float *cosT = (float *)(b + L.off_cos), *sinT = (float *)(b + L.off_sin);
+    const int h2 = c->HD / 2;
+    for (int p = 0; p < c->CTX; p++)
+        for (int d = 0; d < h2; d++) {
+            double ang = (double)p * pow((double)c->theta, -2.0 * (double)d / (double)c->HD);
+            cosT[(size_t)p * h2 + d] = (float)cos(ang);
+            sinT[(size_t)p * h2 + d] = (float)sin(ang);
+        }
+    for (int l = 0; l < c->NL; l++)
+        fill_h((uint16_t *)(b + L.l_base + (size_t)l * L.lstride), L.lstride / 2, &s, std, tmp, tmp_n);
+    fill_h((uint16_t *)(b + L.off_lnfw), (size_t)c->C, &s, std, tmp, tmp_n);
+    free(tmp);
+    return SGPU_OK;
+}
+
+struct sgpu_qwen {
+    sgpu_qwen_cfg cfg;
+    qlayout L;
+    hipStream_t stream;
+    uint16_t *d_emb, *d_lnfw;
+    float *d_cos, *d_sin;
+    uint16_t **d_ln1w, **d_qkvw, **d_ow, **d_ln2w, **d_gateupw, **d_downw;
+    float **d_qkvb, **d_kc, **d_vc;
+    float *d_x, *d_ln1, *d_qkv, *d_att, *d_y, *d_ln2, *d_gate, *d_down, *d_scores, *d_probs, *d_logits, *d_x2;
+};
+
+static int dalloc(void **p, size_t bytes, const void *src) {
+    int rc = sgpu_malloc(p, bytes);
+    if (rc) return rc;
+    if (src) return sgpu_memcpy_htod(*p, src, bytes);
+    return sgpu_memset_d8(*p, 0, bytes);
+}
+
+void sgpu_qwen_destroy(sgpu_qwen *e) {
+    if (!e) return;
+    const int NL = e->cfg.NL;
+    void **single[] = {(void **)&e->d_emb, (void **)&e->d_lnfw, (void **)&e->d_cos, (void **)&e->d_sin,
+                       (void **)&e->d_x, (void **)&e->d_ln1, (void **)&e->d_qkv, (void **)&e->d_att,
+                       (void **)&e->d_y, (void **)&e->d_ln2, (void **)&e->d_gate, (void **)&e->d_down,
+                       (void **)&e->d_scores, (void **)&e->d_probs, (void **)&e->d_logits, (void **)&e->d_x2};
+    for (size_t i = 0; i < sizeof single / sizeof single[0]; i++) sgpu_free(*single[i]);
+    void ***arrs[] = {(void ***)&e->d_ln1w, (void ***)&e->d_qkvw, (void ***)&e->d_ow, (void ***)&e->d_ln2w,
+                      (void ***)&e->d_gateupw, (void ***)&e->d_downw, (void ***)&e->d_qkvb,
+                      (void ***)&e->d_kc, (void ***)&e->d_vc};
+    for (size_t a = 0; a < sizeof arrs / sizeof arrs[0]; a++) {
+        void **arr = *arrs[a];
+        if (!arr) continue;
+        for (int l = 0; l < NL; l++) sgpu_free(arr[l]);
+        free(arr);
+    }
+    if (e->stream) hipStreamDestroy(e->stream);
+    free(e);
+}
+
+int sgpu_qwen_create(sgpu_qwen **out, const sgpu_qwen_cfg *c, const void *blob) {
+    if (!out || !blob || !cfg_ok(c)) return SGPU_ERR_INVALID_ARG;
+    *out = NULL;
+    int rc;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return SGPU_ERR_NO_DEVICE;
+    if ((rc = sgpu_init(dev))) return rc;
+    sgpu_qwen *e = calloc(1, sizeof *e);
+    if (!e) return SGPU_ERR_HOST_ALLOC;
+    e->cfg = *c;
+    q_layout(c, &e->L);
+    const qlayout *L = &e->L;
+    const int NL = c->NL, C = c->C, FC = c->FC, QKVD = L->qkvd, KVD = L->kvd;
+    const unsigned char *b = (const unsigned char *)blob;
+#define TRY(x) do { if ((rc = (x))) goto fail; } while (0)
+    if (hipStreamCreate(&e->stream) != hipSuccess) { rc = SGPU_ERR_NO_DEVICE; goto fail; }
+    e->d_ln1w = calloc(NL, sizeof(void *)); e->d_qkvw = calloc(NL, sizeof(void *));
+    e->d_ow = calloc(NL, sizeof(void *)); e->d_ln2w = calloc(NL, sizeof(void *));
+    e->d_gateupw = calloc(NL, sizeof(void *)); e->d_downw = calloc(NL, sizeof(void *));
+    e->d_qkvb = calloc(NL, sizeof(void *)); e->d_kc = calloc(NL, sizeof(void *));
+    e->d_vc = calloc(NL, sizeof(void *));
+    if (!e->d_ln1w || !e->d_qkvw || !e->d_ow || !e->d_ln2w || !e->d_gateupw || !e->d_downw || !e->d_qkvb ||
+        !e->d_kc || !e->d_vc) { rc = SGPU_ERR_HOST_ALLOC; goto fail; }
+    TRY(dalloc((void **)&e->d_emb, (size_t)c->V * C * 2, b + L->off_emb));
+    TRY(dalloc((void **)&e->d_cos, (size_t)c->CTX * (c->HD / 2) * 4, b + L->off_cos));
+    TRY(dalloc((void **)&e->d_sin, (size_t)c->CTX * (c->HD / 2) * 4, b + L->off_sin));
+    TRY(dalloc((void **)&e->d_lnfw, (size_t)C * 2, b + L->off_lnfw));
+    {
+        float *tmp = malloc(sizeof(float) * QKVD);
+        if (!tmp) { rc = SGPU_ERR_HOST_ALLOC; goto fail; }
+        for (int l = 0; l < NL && !rc; l++) {
+            const uint16_t *lb = (const uint16_t *)(b + L->l_base + (size_t)l * L->lstride);
+            if ((rc = dalloc((void **)&e->d_ln1w[l], (size_t)C * 2, lb + L->li_inln))) break;
+            if ((rc = dalloc((void **)&e->d_qkvw[l], (size_t)QKVD * C * 2, lb + L->li_qkvw))) break;
+            /* q/k/v bias decoded to fp32 on the host, as qwen_engine.c:170-175 */
+            for (int i = 0; i < QKVD; i++) tmp[i] = sgpu_h2f_host(lb[L->li_qkvb + i]);
+            if ((rc = dalloc((void **)&e->d_qkvb[l], (size_t)QKVD * 4, tmp))) break;
+            if ((rc = dalloc((void **)&e->d_ow[l], (size_t)C * C * 2, lb + L->li_ow))) break;
+            if ((rc = dalloc((void **)&e->d_ln2w[l], (size_t)C * 2, lb + L->li_postln))) break;
+            if ((rc = dalloc((void **)&e->d_gateupw[l], (size_t)2 * FC * C * 2, lb + L->li_gateup))) break;
+            if ((rc = dalloc((void **)&e->d_downw[l], (size_t)C * FC * 2, lb + L->li_down))) break;
+            if ((rc = dalloc((void **)&e->d_kc[l], (size_t)c->CTX * KVD * 4, NULL))) break;
+            if ((rc = dalloc((void **)&e->d_vc[l], (size_t)c->CTX * KVD * 4, NULL))) break;
+        }
+        free(tmp);
+        if (rc) goto fail;
+    }
+    TRY(dalloc((void **)&e->d_x, (size_t)C * 4, NULL));
+    TRY(dalloc((void **)&e->d_ln1, (size_t)C * 4, NULL));
+    TRY(dalloc((void **)&e->d_qkv, (size_t)QKVD * 4, NULL));
+    TRY(dalloc((void **)&e->d_att, (size_t)C * 4, NULL));
+    TRY(dalloc((void **)&e->d_y, (size_t)C * 4, NULL));
+    TRY(dalloc((void **)&e->d_ln2, (size_t)C * 4, NULL));
+    TRY(dalloc((void **)&e->d_gate, (size_t)2 * FC * 4, NULL));
+    TRY(dalloc((void **)&e->d_down, (size_t)FC * 4, NULL));
+    TRY(dalloc((void **)&e->d_scores, (size_t)c->CTX * c->NH * 4, NULL));
+    TRY(dalloc((void **)&e->d_probs, (size_t)c->CTX * c->NH * 4, NULL));
+    TRY(dalloc((void **)&e->d_logits, (size_t)c->V * 4, NULL));
+    TRY(dalloc((void **)&e->d_x2, (size_t)C * 4, NULL));
+#undef TRY
+    *out = e;
+    return SGPU_OK;
+fail:
+    sgpu_qwen_destroy(e);
+    return rc;
+}
+
+const float *sgpu_qwen_device_logits(const sgpu_qwen *e) { return e ? e->d_logits : NULL; }
+
+int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host) {
+    if (!e) return SGPU_ERR_INVALID_ARG;
+    const sgpu_qwen_cfg *c = &e->cfg;
+    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
+    const int C = c->C, NH = c->NH, NKV = c->NKV, HD = c->HD, FC = c->FC;
+    const int KVD = e->L.kvd, QKVD = e->L.qkvd, Tp = pos + 1;
+    const float eps = c->eps, scale = (float)(1.0 / sqrt((double)HD));
+    void *s = (void *)e->stream;
+    int rc;
+#define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+    TRY(sgpu_internal_embed_h(e->d_emb, token, e->d_x, C, s));
+    for (int l = 0; l < c->NL; l++) {
+        TRY(sgpu_rmsnorm(e->d_x, e->d_ln1w[l], e->d_ln1, C, eps, 1, s));
+        TRY(sgpu_gemv_h(e->d_qkvw[l], e->d_ln1, e->d_qkvb[l], e->d_qkv, C, QKVD, s));
+        TRY(sgpu_rope(e->d_qkv, e->d_cos, e->d_sin, 1, NH, HD, pos, s));
+        TRY(sgpu_rope(e->d_qkv + (size_t)NH * HD, e->d_cos, e->d_sin, 1, NKV, HD, pos, s));
+        TRY(sgpu_memcpy_dtod_async(e->d_kc[l] + (size_t)pos * KVD, e->d_qkv + (size_t)NH * HD, (size_t)KVD * 4, s));
+        TRY(sgpu_memcpy_dtod_async(e->d_vc[l] + (size_t)pos * KVD, e->d_qkv + (size_t)NH * HD + KVD,
+                                   (size_t)KVD * 4, s));
+        TRY(sgpu_attn_scores_gqa(e->d_qkv, e->d_kc[l], e->d_scores, Tp, scale, NH, KVD, HD, s));
+        TRY(sgpu_attn_softmax(e->d_scores, e->d_probs, Tp, NH, s));
+        TRY(sgpu_attn_mix_gqa(e->d_probs, e->d_vc[l], e->d_att, Tp, NH, KVD, HD, s));
+        TRY(sgpu_gemv_h(e->d_ow[l], e->d_att, NULL, e->d_y, C, C, s));
+        TRY(sgpu_add2(e->d_x, e->d_y, e->d_x, C, s));
+        TRY(sgpu_rmsnorm(e->d_x, e->d_ln2w[l], e->d_ln2, C, eps, 1, s));
+        TRY(sgpu_gemv_h(e->d_gateupw[l], e->d_ln2, NULL, e->d_gate, C, 2 * FC, s));
+        TRY(sgpu_swiglu(e->d_gate, e->d_gate + FC, e->d_down, FC, s));
+        TRY(sgpu_gemv_h(e->d_downw[l], e->d_down, NULL, e->d_y, FC, C, s));
+        TRY(sgpu_add2(e->d_x, e->d_y, e->d_x, C, s));
+    }
+    if (!want_logits) return SGPU_OK;
+    TRY(sgpu_rmsnorm(e->d_x, e->d_lnfw, e->d_x2, C, eps, 1, s));
+    TRY(sgpu_gemv_h(e->d_emb, e->d_x2, NULL, e->d_logits, C, c->V, s));
+    if (logits_host) {
+        hipError_t he = hipMemcpyAsync(logits_host, e->d_logits, (size_t)c->V * 4, hipMemcpyDeviceToHost, e->stream);
+        if (he != hipSuccess) return (int)he;
+        TRY(sgpu_stream_synchronize(s));
+    }
+#undef TRY
+    return SGPU_OK;
+}

@@ -1,0 +1,658 @@
+/* sgpu.c -- libswitchgpu.so: the C-ABI host side of the gfx950 matmul hot path.
+ *
+ * Plain C over the HIP module API: the gfx950 code objects are embedded in this library
+ * (code_objects.S) and loaded with hipModuleLoadData, kernels are resolved by name with
+ * hipModuleGetFunction and launched with hipModuleLaunchKernel -- the HIP counterparts of
+ * the reference's cuModuleLoadData / cuModuleGetFunction / cuLaunchKernel flow
+ * (gpu_workload.c:68-74,90; qwen_engine.c:147-155,216-266).  The launchers own the launch
+ * geometry (wave64 blocks), so callers pass only the reference kernels' own arguments.
+ */
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+
+#include <math.h>
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "sgpu_internal.h"
+#include "switch_gpu.h"
+
+#define SGPU_MAX_DEVICES 16
+
+/* ---- embedded code objects (code_objects.S) ---- */
+extern const unsigned char sgpu_co_switch_gpu[], sgpu_co_switch_gpu_end[];
+extern const unsigned char sgpu_co_gemv[], sgpu_co_gemv_end[];
+extern const unsigned char sgpu_co_gpt2_kernels[], sgpu_co_gpt2_kernels_end[];
+extern const unsigned char sgpu_co_qwen_kernels[], sgpu_co_qwen_kernels_end[];
+extern const unsigned char sgpu_co_sgpu_tuned[], sgpu_co_sgpu_tuned_end[];
+
+enum { MOD_SWITCH, MOD_GEMV, MOD_GPT2, MOD_QWEN, MOD_TUNED, NMOD };
+static const struct {
+    const char *name;
+    const unsigned char *start, *end;
+} g_cos[NMOD] = {
+    {"switch_gpu", sgpu_co_switch_gpu, sgpu_co_switch_gpu_end},
+    {"gemv", sgpu_co_gemv, sgpu_co_gemv_end},
+    {"gpt2_kernels", sgpu_co_gpt2_kernels, sgpu_co_gpt2_kernels_end},
+    {"qwen_kernels", sgpu_co_qwen_kernels, sgpu_co_qwen_kernels_end},
+    {"sgpu_tuned", sgpu_co_sgpu_tuned, sgpu_co_sgpu_tuned_end},
+};
+
+/* Every kernel the launchers use: (module, symbol). */
+enum {
+    K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_NAIVE, K_MEMBW,
+    K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI,
+    K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
+    K_EMBED_H,
+    NKERN
+};
+static const struct {
+    int mod;
+    const char *sym;
+} g_kern[NKERN] = {
+    {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
+    {MOD_SWITCH, "sgemm_naive"}, {MOD_SWITCH, "membw_read4"},
+    {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
+    {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"},
+    {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
+    {MOD_QWEN, "attn_scores_gqa"}, {MOD_QWEN, "attn_softmax"}, {MOD_QWEN, "attn_mix_gqa"},
+    {MOD_QWEN, "add2"},
+    {MOD_TUNED, "sgpu_embed_h"},
+};
+
+/* Tuned GEMV table: team sizes x segments-per-lane instantiated in sgpu_tuned.hip. */
+static const int g_lpr[3] = {16, 64, 256};
+static const int g_segs[10] = {1, 2, 3, 4, 6, 7, 8, 10, 12, 16};
+#define NLPR 3
+#define NSEG 10
+
+typedef struct {
+    int ready;
+    int cus;
+    hipModule_t mod[NMOD];
+    hipFunction_t fn[NKERN];
+    hipFunction_t gemv_f32[NLPR][NSEG], gemv_h[NLPR][NSEG];
+} devstate;
+
+static devstate g_dev[SGPU_MAX_DEVICES];
+static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
+
+const char *sgpu_error_string(int status) {
+    switch (status) {
+    case SGPU_OK: return "success";
+    case SGPU_ERR_INVALID_ARG: return "invalid argument (size, shape or pointer)";
+    case SGPU_ERR_NOT_INITIALIZED: return "sgpu_init has not succeeded on the current device";
+    case SGPU_ERR_NO_KERNEL: return "kernel not found in the code object";
+    case SGPU_ERR_NO_DEVICE: return "no usable HIP device";
+    case SGPU_ERR_HOST_ALLOC: return "host allocation failed";
+    default: break;
+    }
+    if (status > 0) return hipGetErrorString((hipError_t)status);
+    return "unknown sgpu error";
+}
+
+#define HIPCHK(x)                                \
+    do {                                         \
+        hipError_t e_ = (x);                     \
+        if (e_ != hipSuccess) return (int)e_;    \
+    } while (0)
+
+static int load_device(int dev) {
+    devstate *d = &g_dev[dev];
+    if (d->ready) return SGPU_OK;
+    int rc = SGPU_OK;
+    pthread_mutex_lock(&g_lock);
+    if (d->ready) goto out;
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) { rc = (int)e; goto out; }
+    d->cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 1;
+    for (int m = 0; m < NMOD; m++) {
+        e = hipModuleLoadData(&d->mod[m], g_cos[m].start);
+        if (e != hipSuccess) { rc = (int)e; goto out; }
+    }
+    for (int k = 0; k < NKERN; k++) {
+        e = hipModuleGetFunction(&d->fn[k], d->mod[g_kern[k].mod], g_kern[k].sym);
+        if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+    }
+    for (int i = 0; i < NLPR; i++)
+        for (int j = 0; j < NSEG; j++) {
+            char name[64];
+            snprintf(name, sizeof name, "sgpu_gemv_f32_l%d_s%d", g_lpr[i], g_segs[j]);
+            e = hipModuleGetFunction(&d->gemv_f32[i][j], d->mod[MOD_TUNED], name);
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+            snprintf(name, sizeof name, "sgpu_gemv_h_l%d_s%d", g_lpr[i], g_segs[j]);
+            e = hipModuleGetFunction(&d->gemv_h[i][j], d->mod[MOD_TUNED], name);
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+        }
+    d->ready = 1;
+out:
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+int sgpu_init(int device) {
+    hipError_t e = hipInit(0);
+    if (e != hipSuccess) return (int)e;
+    int n = 0;
+    e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return (int)e;
+    if (n <= 0) return SGPU_ERR_NO_DEVICE;
+    if (device < 0 || device >= n || device >= SGPU_MAX_DEVICES) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipSetDevice(device));
+    return load_device(device);
+}
+
+/* State of the current device, loading it on first use. */
+static devstate *cur(int *rc) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { *rc = (int)e; return NULL; }
+    if (dev < 0 || dev >= SGPU_MAX_DEVICES) { *rc = SGPU_ERR_NO_DEVICE; return NULL; }
+    if (!g_dev[dev].ready) {
+        *rc = load_device(dev);
+        if (*rc) return NULL;
+    }
+    *rc = SGPU_OK;
+    return &g_dev[dev];
+}
+
+int sgpu_device_count(int *count) {
+    if (!count) return SGPU_ERR_INVALID_ARG;
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    return e == hipSuccess ? SGPU_OK : (int)e;
+}
+
+int sgpu_get_device_props(int device, sgpu_device_props *props) {
+    if (!props) return SGPU_ERR_INVALID_ARG;
+    hipDeviceProp_t p;
+    HIPCHK(hipGetDeviceProperties(&p, device));
+    memset(props, 0, sizeof *props);
+    snprintf(props->name, sizeof props->name, "%s", p.name);
+    snprintf(props->arch, sizeof props->arch, "%.63s", p.gcnArchName);
+    props->compute_units = p.multiProcessorCount;
+    props->clock_khz = p.clockRate;
+    props->memory_clock_khz = p.memoryClockRate;
+    props->memory_bus_width = p.memoryBusWidth;
+    props->total_mem = p.totalGlobalMem;
+    props->lds_per_block = p.sharedMemPerBlock;
+    props->l2_bytes = p.l2CacheSize;
+    props->warp_size = p.warpSize;
+    return SGPU_OK;
+}
+
+int sgpu_malloc(void **dptr, size_t bytes) {
+    if (!dptr) return SGPU_ERR_INVALID_ARG;
+    *dptr = NULL;
+    if (bytes == 0) return SGPU_OK;
+    HIPCHK(hipMalloc(dptr, bytes));
+    return SGPU_OK;
+}
+int sgpu_free(void *dptr) {
+    if (!dptr) return SGPU_OK;
+    HIPCHK(hipFree(dptr));
+    return SGPU_OK;
+}
+int sgpu_memcpy_htod(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return SGPU_OK;
+    if (!dst || !src) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return SGPU_OK;
+}
+int sgpu_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return SGPU_OK;
+    if (!dst || !src) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return SGPU_OK;
+}
+int sgpu_memcpy_dtod(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return SGPU_OK;
+    if (!dst || !src) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return SGPU_OK;
+}
+int sgpu_memcpy_dtod_async(void *dst, const void *src, size_t bytes, void *stream) {
+    if (!bytes) return SGPU_OK;
+    if (!dst || !src) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return SGPU_OK;
+}
+int sgpu_memset_d8(void *dst, int value, size_t bytes) {
+    if (!bytes) return SGPU_OK;
+    if (!dst) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipMemset(dst, value, bytes));
+    return SGPU_OK;
+}
+int sgpu_synchronize(void) {
+    HIPCHK(hipDeviceSynchronize());
+    return SGPU_OK;
+}
+int sgpu_stream_synchronize(void *stream) {
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    return SGPU_OK;
+}
+
+int sgpu_event_create(void **event) {
+    if (!event) return SGPU_ERR_INVALID_ARG;
+    hipEvent_t e;
+    HIPCHK(hipEventCreate(&e));
+    *event = (void *)e;
+    return SGPU_OK;
+}
+int sgpu_event_destroy(void *event) {
+    if (!event) return SGPU_OK;
+    HIPCHK(hipEventDestroy((hipEvent_t)event));
+    return SGPU_OK;
+}
+int sgpu_event_record(void *event, void *stream) {
+    if (!event) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return SGPU_OK;
+}
+int sgpu_event_elapsed_ms(float *ms, void *start, void *stop) {
+    if (!ms || !start || !stop) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipEventSynchronize((hipEvent_t)stop));
+    HIPCHK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return SGPU_OK;
+}
+
+const void *sgpu_code_object(const char *name, size_t *size) {
+    if (!name) return NULL;
+    for (int m = 0; m < NMOD; m++)
+        if (!strcmp(name, g_cos[m].name)) {
+            if (size) *size = (size_t)(g_cos[m].end - g_cos[m].start);
+            return g_cos[m].start;
+        }
+    return NULL;
+}
+
+/* ---- geometry ---- */
+static unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
+static unsigned umin(unsigned a, unsigned b) { return a < b ? a : b; }
+
+static int sgemm_tile(const char *k) {
+    if (!strcmp(k, "sgemm_tiled")) return 64;
+    if (!strcmp(k, "sgemm_tiled4") || !strcmp(k, "sgemm_opt")) return 128;
+    return 0;
+}
+
+static int geometry(const devstate *d, const char *kernel, int M, int N, int K, unsigned g[3], unsigned b[3]) {
+    (void)K;
+    const unsigned cus = d ? (unsigned)d->cus : 256u;
+    g[0] = g[1] = g[2] = 1;
+    b[0] = b[1] = b[2] = 1;
+    int tile = sgemm_tile(kernel);
+    if (tile) {
+        long long nt = (long long)cdiv(M, tile) * cdiv(N, tile);
+        g[0] = (unsigned)(nt > 0 ? nt : 1);
+        b[0] = 256;
+        return SGPU_OK;
+    }
+    if (!strcmp(kernel, "sgemm_naive")) {
+        g[0] = umin(cdiv(N > 0 ? N : 1, 16), 65535u);
+        g[1] = umin(cdiv(M > 0 ? M : 1, 16), 65535u);
+        b[0] = b[1] = 16;
+        return SGPU_OK;
+    }
+    if (!strcmp(kernel, "membw_read4")) {
+        g[0] = cus * 8;
+        b[0] = 256;
+        return SGPU_OK;
+    }
+    if (!strcmp(kernel, "gemv") || !strcmp(kernel, "gemv4") || !strcmp(kernel, "gemv_warp") ||
+        !strcmp(kernel, "gemv_warp_b") || !strcmp(kernel, "gemv_h")) {
+        g[0] = umin(cdiv(N > 0 ? N : 1, 4), cus * 16);   /* a wave per row, 4 waves per block */
+        b[0] = 256;
+        return SGPU_OK;
+    }
+    if (!strcmp(kernel, "gemv_multi")) {   /* M carries T for this kernel */
+        g[0] = umin(cdiv(N > 0 ? N : 1, 4), cus * 16);
+        g[1] = umin(cdiv(M > 0 ? M : 1, 16), 65535u);
+        b[0] = 256;
+        return SGPU_OK;
+    }
+    return SGPU_ERR_NO_KERNEL;
+}
+
+int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[3], unsigned block[3]) {
+    if (!kernel || !grid || !block || M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    int dev = 0;
+    const devstate *d = NULL;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < SGPU_MAX_DEVICES && g_dev[dev].ready)
+        d = &g_dev[dev];
+    return geometry(d, kernel, M, N, K, grid, block);
+}
+
+static int launch(hipFunction_t f, const unsigned g[3], const unsigned b[3], void *stream, void **args) {
+    hipError_t e = hipModuleLaunchKernel(f, g[0], g[1], g[2], b[0], b[1], b[2], 0, (hipStream_t)stream, args, NULL);
+    return (int)e;
+}
+
+/* ---- SGEMM ---- */
+static int sgemm_common(int kid, const char *name, const float *A, const float *B, float *C, int M, int N,
+                        int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    if (!C || (K > 0 && (!A || !B))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3], b[3];
+    if ((rc = geometry(d, name, M, N, K, g, b))) return rc;
+    void *args[] = {&A, &B, &C, &M, &N, &K};
+    return launch(d->fn[kid], g, b, stream, args);
+}
+int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    return sgemm_common(K_SGEMM_TILED, "sgemm_tiled", A, B, C, M, N, K, stream);
+}
+int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
+}
+int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    return sgemm_common(K_SGEMM_OPT, "sgemm_opt", A, B, C, M, N, K, stream);
+}
+int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    return sgemm_common(K_SGEMM_NAIVE, "sgemm_naive", A, B, C, M, N, K, stream);
+}
+
+int sgpu_membw_read4(const void *buf, float *out, int n4, int iters, int *threads, void *stream) {
+    if (n4 < 0 || iters < 0) return SGPU_ERR_INVALID_ARG;
+    if (n4 > 0 && (!buf || !out || ((uintptr_t)buf & 15))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3], b[3];
+    geometry(d, "membw_read4", 0, 0, 0, g, b);
+    if (threads) *threads = (int)(g[0] * b[0]);
+    if (n4 == 0) return SGPU_OK;
+    void *args[] = {&buf, &out, &n4, &iters};
+    return launch(d->fn[K_MEMBW], g, b, stream, args);
+}
+
+/* ---- GEMV ---- */
+/* Pick the tuned instantiation for a K x N GEMV (VEC elements per 16 bytes), or -1/-1 for
+ * the generic kernel.  Smallest team that still gives >= 8 waves per CU, else the largest
+ * that fits in 16 segments per lane. */
+static void pick_tuned(const devstate *d, int K, int N, int vec, int *li, int *si) {
+    *li = *si = -1;
+    if (K <= 0 || N <= 0 || K % vec) return;
+    const long long nseg = K / vec;
+    const long long want_waves = 8LL * d->cus;
+    int best_l = -1;
+    for (int i = 0; i < NLPR; i++) {
+        long long s = (nseg + g_lpr[i] - 1) / g_lpr[i];
+        if (s > g_segs[NSEG - 1]) continue;
+        best_l = i;
+        if ((long long)N * g_lpr[i] / 64 >= want_waves) break;
+    }
+    if (best_l < 0) return;
+    long long s = (nseg + g_lpr[best_l] - 1) / g_lpr[best_l];
+    for (int j = 0; j < NSEG; j++)
+        if (g_segs[j] >= s) { *li = best_l; *si = j; return; }
+}
+
+static int gemv_launch(int generic_kid, int is_h, const void *W, const float *x, const float *bias, float *y,
+                       int K, int N, void *stream) {
+    if (K < 0 || N < 0) return SGPU_ERR_INVALID_ARG;
+    if (N == 0) return SGPU_OK;
+    if (!y || (K > 0 && (!W || !x))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    void *args[] = {(void *)&W, (void *)&x, (void *)&bias, (void *)&y, &K, &N};
+    const int vec = is_h ? 8 : 4;
+    int li, si;
+    pick_tuned(d, K, N, vec, &li, &si);
+    const int aligned = ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0;
+    if (li >= 0 && aligned) {
+        const int teams = 256 / g_lpr[li];
+        unsigned g[3] = {umin(cdiv(N, teams), (unsigned)d->cus * 8u), 1, 1}, b[3] = {256, 1, 1};
+        return launch(is_h ? d->gemv_h[li][si] : d->gemv_f32[li][si], g, b, stream, args);
+    }
+    unsigned g[3], b[3];
+    geometry(d, "gemv_h", 0, N, K, g, b);
+    if (generic_kid == K_GEMV || generic_kid == K_GEMV4 || generic_kid == K_GEMV_WARP) {
+        void *args5[] = {(void *)&W, (void *)&x, (void *)&y, &K, &N};   /* no bias slot */
+        return launch(d->fn[generic_kid], g, b, stream, args5);
+    }
+    return launch(d->fn[generic_kid], g, b, stream, args);
+}
+
+int sgpu_gemv(const float *W, const float *x, float *y, int K, int N, void *stream) {
+    return gemv_launch(K_GEMV, 0, W, x, NULL, y, K, N, stream);
+}
+int sgpu_gemv4(const float *W, const float *x, float *y, int K, int N, void *stream) {
+    return gemv_launch(K_GEMV4, 0, W, x, NULL, y, K, N, stream);
+}
+int sgpu_gemv_warp(const float *W, const float *x, float *y, int K, int N, void *stream) {
+    return gemv_launch(K_GEMV_WARP, 0, W, x, NULL, y, K, N, stream);
+}
+int sgpu_gemv_warp_b(const float *W, const float *x, const float *bias, float *y, int K, int N, void *stream) {
+    return gemv_launch(K_GEMV_WARP_B, 0, W, x, bias, y, K, N, stream);
+}
+int sgpu_gemv_h(const uint16_t *W, const float *x, const float *bias, float *y, int K, int N, void *stream) {
+    return gemv_launch(K_GEMV_H, 1, W, x, bias, y, K, N, stream);
+}
+
+int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N, int T,
+                    void *stream) {
+    if (K < 0 || N < 0 || T < 0) return SGPU_ERR_INVALID_ARG;
+    if (N == 0 || T == 0) return SGPU_OK;
+    if (!Y || (K > 0 && (!W || !X))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3], b[3];
+    geometry(d, "gemv_multi", T, N, K, g, b);
+    void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T};
+    return launch(d->fn[K_GEMV_MULTI], g, b, stream, args);
+}
+
+/* ---- Qwen support kernels ---- */
+static int elem_grid(int n) { return (int)umin(cdiv(n > 0 ? n : 1, 256), 65535u); }
+
+int sgpu_rmsnorm(const float *x, const uint16_t *w, float *y, int n, float eps, int rows, void *stream) {
+    if (n < 0 || rows < 0) return SGPU_ERR_INVALID_ARG;
+    if (n == 0 || rows == 0) return SGPU_OK;
+    if (!x || !w || !y || rows > 65535 * 1024) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)rows, 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&x, (void *)&w, (void *)&y, &n, &eps};
+    return launch(d->fn[K_RMSNORM], g, b, stream, args);
+}
+
+int sgpu_rope(float *x, const float *cosT, const float *sinT, int T, int H, int HD, int pos0, void *stream) {
+    if (T < 0 || H < 0 || HD < 0 || HD % 2 || pos0 < 0) return SGPU_ERR_INVALID_ARG;
+    long long total = (long long)T * H * (HD / 2);
+    if (total == 0) return SGPU_OK;
+    if (!x || !cosT || !sinT || total > 0x7fffffffLL) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid((int)total), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&x, (void *)&cosT, (void *)&sinT, &T, &H, &HD, &pos0};
+    return launch(d->fn[K_ROPE], g, b, stream, args);
+}
+
+int sgpu_swiglu(const float *gt, const float *u, float *y, int n, void *stream) {
+    if (n < 0) return SGPU_ERR_INVALID_ARG;
+    if (n == 0) return SGPU_OK;
+    if (!gt || !u || !y) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(n), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&gt, (void *)&u, (void *)&y, &n};
+    return launch(d->fn[K_SWIGLU], g, b, stream, args);
+}
+
+static int gqa_ok(int NH, int KV, int HD) {
+    return NH > 0 && HD > 0 && KV > 0 && KV % HD == 0 && NH % (KV / HD) == 0;
+}
+
+int sgpu_attn_scores_gqa(const float *q, const float *kc, float *scores, int T, float scale, int NH, int KV,
+                         int HD, void *stream) {
+    if (T < 0 || !gqa_ok(NH, KV, HD)) return SGPU_ERR_INVALID_ARG;
+    if (T == 0) return SGPU_OK;
+    if (!q || !kc || !scores || (long long)T * NH > 0x7fffffffLL) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(T * NH), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&q, (void *)&kc, (void *)&scores, &T, &scale, &NH, &KV, &HD};
+    return launch(d->fn[K_ASCORES], g, b, stream, args);
+}
+
+int sgpu_attn_softmax(const float *scores, float *probs, int T, int NH, void *stream) {
+    if (T < 0 || NH < 0) return SGPU_ERR_INVALID_ARG;
+    if (T == 0 || NH == 0) return SGPU_OK;
+    if (!scores || !probs) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {umin(cdiv(NH, 4), 65535u), 1, 1}, b[3] = {256, 1, 1};   /* a wave per head */
+    void *args[] = {(void *)&scores, (void *)&probs, &T, &NH};
+    return launch(d->fn[K_ASOFTMAX], g, b, stream, args);
+}
+
+int sgpu_attn_mix_gqa(const float *probs, const float *vc, float *out, int T, int NH, int KV, int HD,
+                      void *stream) {
+    if (T < 0 || !gqa_ok(NH, KV, HD)) return SGPU_ERR_INVALID_ARG;
+    if (!probs || !vc || !out) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(NH * HD), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&probs, (void *)&vc, (void *)&out, &T, &NH, &KV, &HD};
+    return launch(d->fn[K_AMIX], g, b, stream, args);
+}
+
+int sgpu_add2(const float *a, const float *bb, float *out, int n, void *stream) {
+    if (n < 0) return SGPU_ERR_INVALID_ARG;
+    if (n == 0) return SGPU_OK;
+    if (!a || !bb || !out) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(n), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&a, (void *)&bb, (void *)&out, &n};
+    return launch(d->fn[K_ADD2], g, b, stream, args);
+}
+
+/* ---- seeded generators ---- */
+void sgpu_gen_sgemm_inputs(float *A, float *B, size_t count, unsigned seed) {
+    srand(seed);
+    for (size_t i = 0; i < count; i++) {
+        A[i] = (rand() % 2000 - 1000) / 1000.0f;
+        B[i] = (rand() % 2000 - 1000) / 1000.0f;
+    }
+}
+
+#define LCG_A 6364136223846793005ULL
+#define LCG_C 1442695040888963407ULL
+
+float sgpu_frand(uint64_t *state) {
+    *state = *state * LCG_A + LCG_C;
+    return (float)((*state >> 40) & 0xFFFFFF) / (float)0x1000000;
+}
+
+/* Advance the LCG by n steps in O(log n) (affine map composition), so a long stream can be
+ * produced in parallel chunks that equal the serial stream. */
+static uint64_t lcg_skip(uint64_t s, uint64_t n) {
+    uint64_t acc_a = 1, acc_c = 0, a = LCG_A, c = LCG_C;
+    while (n) {
+        if (n & 1) { acc_a *= a; acc_c = acc_c * a + c; }
+        c = c * (a + 1);
+        a = a * a;
+        n >>= 1;
+    }
+    return s * acc_a + acc_c;
+}
+
+void sgpu_gen_uniform(float *out, size_t n, uint64_t *state, float offset) {
+    const uint64_t s0 = *state;
+#pragma omp parallel for schedule(static)
+    for (long long c = 0; c < (long long)((n + 65535) / 65536); c++) {
+        uint64_t s = lcg_skip(s0, (uint64_t)c * 65536);
+        size_t end = (size_t)(c + 1) * 65536 < n ? (size_t)(c + 1) * 65536 : n;
+        for (size_t i = (size_t)c * 65536; i < end; i++) out[i] = sgpu_frand(&s) + offset;
+    }
+    *state = lcg_skip(s0, n);
+}
+
+static void normal_pair(uint64_t *s, float mean, float std, float *z0, float *z1) {
+    double u1 = sgpu_frand(s), u2 = sgpu_frand(s);
+    if (u1 <= 0.0) u1 = 1.0 / 16777216.0;
+    double r = sqrt(-2.0 * log(u1)), th = 6.283185307179586 * u2;
+    *z0 = (float)(mean + std * (r * cos(th)));
+    *z1 = (float)(mean + std * (r * sin(th)));
+}
+
+void sgpu_gen_normal(float *out, size_t n, uint64_t *state, float mean, float std) {
+    const uint64_t s0 = *state;
+    const size_t pairs = (n + 1) / 2;
+#pragma omp parallel for schedule(static)
+    for (long long c = 0; c < (long long)((pairs + 32767) / 32768); c++) {
+        uint64_t s = lcg_skip(s0, (uint64_t)c * 65536);
+        size_t p_end = (size_t)(c + 1) * 32768 < pairs ? (size_t)(c + 1) * 32768 : pairs;
+        for (size_t p = (size_t)c * 32768; p < p_end; p++) {
+            float z0, z1;
+            normal_pair(&s, mean, std, &z0, &z1);
+            out[2 * p] = z0;
+            if (2 * p + 1 < n) out[2 * p + 1] = z1;
+        }
+    }
+    *state = lcg_skip(s0, 2 * pairs);
+}
+
+static uint16_t f32_to_f16_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t absu = u & 0x7fffffffu;
+    if (absu >= 0x7f800000u) return (uint16_t)(sign | (absu > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (absu >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);        /* rounds to >= 65520 */
+    if (absu < 0x38800000u) {                                          /* below 2^-14: subnormal */
+        if (absu < 0x33000000u) return (uint16_t)sign;                   /* < 2^-25 rounds to 0 */
+        uint32_t e = absu >> 23, m = (absu & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126 - e;                                      /* 14 + (127-e) - 1 ... */
+        /* value = m * 2^(e-150); fp16 subnormal unit = 2^-24 -> q = m * 2^(e-126) */
+        uint32_t q = m >> (shift), rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((absu - 0x38000000u) >> 13);                          /* rebias 127 -> 15 */
+    uint32_t rem = absu & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) h++;
+    return (uint16_t)(sign | h);
+}
+
+void sgpu_f32_to_f16(const float *in, uint16_t *out, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)n; i++) out[i] = f32_to_f16_rne(in[i]);
+}
+
+float sgpu_h2f_host(uint16_t h) {
+    uint32_t e = (h >> 10) & 0x1fu;
+    if (e == 0) return 0.0f;
+    uint32_t u = ((uint32_t)(h & 0x8000u) << 16) | ((e + 112u) << 23) | ((uint32_t)(h & 0x3ffu) << 13);
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* ---- library-internal launches ---- */
+int sgpu_internal_embed_h(const uint16_t *emb, int token, float *x, int C, void *stream) {
+    if (C <= 0 || token < 0 || !emb || !x) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(C), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&emb, &token, (void *)&x, &C};
+    return launch(d->fn[K_EMBED_H], g, b, stream, args);
+}

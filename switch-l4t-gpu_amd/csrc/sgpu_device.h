@@ -1,0 +1,80 @@
+// sgpu_device.h -- device helpers shared by the gfx950 code objects.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, DPP row
+// operations (a "row" is 16 lanes), AGPR-backed MFMA accumulators.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SGPU_WAVE 64
+
+typedef float sgpu_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sgpu_u32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming loads (global_load_dwordx4 with the nontemporal hint): data read once.
+__device__ __forceinline__ sgpu_f32x4 sgpu_ldnt(const sgpu_f32x4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ sgpu_u32x4 sgpu_ldnt(const sgpu_u32x4* p) { return __builtin_nontemporal_load(p); }
+
+// fp16 bits -> fp32 with the reference contract (qwen_kernels.cu:6-14): exponent 0 gives
+// +0.0 (subnormals and -0 flushed, sign dropped), exponent 31 gives the finite value
+// +-2^16 * (1 + m/1024), every other code converts exactly.  Pure integer arithmetic, so
+// it does not depend on the wave's denormal mode.  0x38000000 = 112 << 23 re-biases the
+// exponent from 15 to 127.
+__device__ __forceinline__ float sgpu_h2f_lo(uint32_t w) {
+    uint32_t t = (((w & 0x7fffu) << 13) + 0x38000000u) | ((w & 0x8000u) << 16);
+    return __uint_as_float((w & 0x7c00u) ? t : 0u);
+}
+__device__ __forceinline__ float sgpu_h2f_hi(uint32_t w) {
+    uint32_t t = ((((w >> 16) & 0x7fffu) << 13) + 0x38000000u) | (w & 0x80000000u);
+    return __uint_as_float((w & 0x7c000000u) ? t : 0u);
+}
+__device__ __forceinline__ float sgpu_h2f(uint16_t h) { return sgpu_h2f_lo((uint32_t)h); }
+
+// DPP controls (GFX9 encoding).
+#define SGPU_DPP_ROW_SHR(n) (0x110 + (n))
+#define SGPU_DPP_ROW_BCAST15 0x142
+#define SGPU_DPP_ROW_BCAST31 0x143
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float sgpu_dpp(float v) {
+    // Lanes whose source is outside the row (or masked off) read 0.
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
+}
+
+// Sum over groups of LANES consecutive lanes (16, 32 or 64).  The total of each group ends
+// up in the group's LAST lane (lane % LANES == LANES-1); other lanes hold partial sums.
+// Must run with the whole wave active.
+template <int LANES>
+__device__ __forceinline__ float sgpu_group_sum(float v) {
+    static_assert(LANES == 16 || LANES == 32 || LANES == 64, "group of 16/32/64 lanes");
+    v += sgpu_dpp<SGPU_DPP_ROW_SHR(1)>(v);
+    v += sgpu_dpp<SGPU_DPP_ROW_SHR(2)>(v);
+    v += sgpu_dpp<SGPU_DPP_ROW_SHR(4)>(v);
+    v += sgpu_dpp<SGPU_DPP_ROW_SHR(8)>(v);
+    if (LANES >= 32) v += sgpu_dpp<SGPU_DPP_ROW_BCAST15, 0xa>(v);
+    if (LANES >= 64) v += sgpu_dpp<SGPU_DPP_ROW_BCAST31, 0xc>(v);
+    return v;
+}
+
+// Whole-wave reductions returning the result in every lane (via lane 63 / readlane).
+__device__ __forceinline__ float sgpu_wave_sum(float v) {
+    v = sgpu_group_sum<64>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float sgpu_wave_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), SGPU_DPP_ROW_SHR(1), 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), SGPU_DPP_ROW_SHR(2), 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), SGPU_DPP_ROW_SHR(4), 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), SGPU_DPP_ROW_SHR(8), 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), SGPU_DPP_ROW_BCAST15, 0xa, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), SGPU_DPP_ROW_BCAST31, 0xc, 0xf, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Linear thread index / block size for kernels that accept 1-D or 2-D blocks.
+__device__ __forceinline__ int sgpu_tid() { return threadIdx.x + threadIdx.y * blockDim.x; }
+__device__ __forceinline__ int sgpu_nthreads() { return blockDim.x * blockDim.y * blockDim.z; }
+__device__ __forceinline__ int sgpu_bid() {
+    return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+}
+__device__ __forceinline__ int sgpu_nblocks() { return gridDim.x * gridDim.y * gridDim.z; }

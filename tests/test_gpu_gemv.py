@@ -1,0 +1,153 @@
+"""Batch-1 GEMV family and the read-bandwidth probe on the GPU through the C ABI, against
+the oracle (og_gemv: gemv_test.c:85-90 / gpt2_engine.c:342-349; og_gemv_h: qwen_engine.c:276-284;
+og_gemv_multi: gpt2_kernels.cu:110-155 semantics) and exact integer arithmetic.
+
+Bars: fp32 weights, per element |y - y_ref| <= 1e-4 |y_ref| + 1e-4 (gemv_test.c:119);
+fp16 weights (fp32 accumulate) max|y - y_ref| / max|y_ref| <= 1e-3 and per element
+1e-3 |y_ref| + 1e-3 max|y_ref|; integer-valued inputs bit-exact at every shape."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+NT = min(16, os.cpu_count() or 1)
+F32_KERNELS = ["sgpu_gemv", "sgpu_gemv4", "sgpu_gemv_warp"]
+GPT2_SHAPES = [(2304, 768), (768, 768), (3072, 768), (768, 3072), (50257, 768)]      # [N x K]
+QWEN_SHAPES = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896), (1152, 896), (9728, 896)]
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def gemv_dev(gpu, fn, W, x, bias, K, N, x_off=0):
+    dW = gpu.DeviceArray.from_host(W)
+    dx = gpu.DeviceArray(K + x_off + 1)
+    gpu.call("sgpu_memcpy_htod", dx.offset(x_off), np.ascontiguousarray(x, np.float32).ctypes.data, K * 4)
+    dy = gpu.DeviceArray(N)
+    dy.fill_bytes(0xFF)
+    db = gpu.DeviceArray.from_host(np.asarray(bias, np.float32)) if bias is not None else None
+    if fn in F32_KERNELS:
+        gpu.call(fn, dW.ptr, dx.offset(x_off), dy.ptr, K, N, None)
+    else:
+        gpu.call(fn, dW.ptr, dx.offset(x_off), db.ptr if db is not None else None, dy.ptr, K, N, None)
+    gpu.synchronize()
+    return dy.to_host()
+
+
+@pytest.mark.parametrize("N,K", GPT2_SHAPES)
+@pytest.mark.parametrize("fn", F32_KERNELS + ["sgpu_gemv_warp_b"])
+def test_gpt2_shapes_fp32(gpu, og, fn, N, K):
+    say(f"gemv {fn} {N}x{K}")
+    W, s = gpu.gen_normal(N * K, 42 + N, 0.0, 0.02)
+    x, s = gpu.gen_normal(K, s, 0.0, 1.0)
+    bias = gpu.gen_normal(N, s, 0.0, 0.1)[0] if fn == "sgpu_gemv_warp_b" else None
+    y = gemv_dev(gpu, fn, W, x, bias, K, N)
+    ref = og.gemv(W, x, bias, K, N, NT)
+    assert np.all(np.abs(y - ref) <= 1e-4 * np.abs(ref) + 1e-4), np.abs(y - ref).max()
+
+
+@pytest.mark.parametrize("N,K", QWEN_SHAPES)
+def test_qwen_shapes_fp16(gpu, og, N, K):
+    say(f"gemv_h {N}x{K}")
+    Wf, s = gpu.gen_normal(N * K, 7 + N, 0.0, 0.02)
+    W = gpu.f32_to_f16(Wf)
+    x, s = gpu.gen_normal(K, s, 0.0, 1.0)
+    bias = gpu.gen_normal(N, s, 0.0, 0.02)[0] if N == 1152 else None      # fused qkv carries a bias
+    y = gemv_dev(gpu, "sgpu_gemv_h", W, x, bias, K, N)
+    ref = og.gemv_h_fbias(W, x, bias, K, N, NT)
+    m = np.abs(ref).max()
+    assert np.abs(y - ref).max() / m <= 1e-3
+    assert np.all(np.abs(y - ref) <= 1e-3 * np.abs(ref) + 1e-3 * m)
+
+
+EDGE = [(1, 1), (5, 3), (64, 4), (63, 8), (1000, 63), (7, 896), (300, 4864), (33, 5000), (4, 8200), (2, 40000)]
+
+
+@pytest.mark.parametrize("N,K", EDGE)
+@pytest.mark.parametrize("fn", ["sgpu_gemv", "sgpu_gemv_warp_b", "sgpu_gemv_h"])
+def test_integer_exact_edges(gpu, fn, N, K):
+    say(f"gemv {fn} integer {N}x{K}")
+    rng = np.random.default_rng(N * 13 + K)
+    Wi = rng.integers(-3, 4, (N, K))
+    xi = rng.integers(-3, 4, K)
+    bi = rng.integers(-5, 6, N) if fn != "sgpu_gemv" else None
+    W = Wi.astype(np.float16).view(np.uint16) if fn == "sgpu_gemv_h" else Wi.astype(np.float32)
+    want = Wi @ xi + (bi if bi is not None else 0)
+    for x_off in (0, 1):                                  # aligned and unaligned x
+        y = gemv_dev(gpu, fn, W, xi.astype(np.float32), bi, K, N, x_off=x_off)
+        assert np.array_equal(y, want.astype(np.float32))
+
+
+def test_gemv_h_special_codes(gpu, og):
+    """Subnormal and -0 codes read as +0, exponent-31 codes as 2^16 (1 + m/1024): the
+    reference h2f contract (qwen_kernels.cu:6-14), exact with integer x."""
+    rng = np.random.default_rng(3)
+    N, K = 40, 896
+    codes = np.concatenate([np.arange(0, 1024), np.arange(0x8000, 0x8400), np.arange(0x7c00, 0x8000),
+                            np.arange(0xfc00, 0x10000), np.arange(0x3c00, 0x3c40)]).astype(np.uint16)
+    W = rng.choice(codes, (N, K)).astype(np.uint16)
+    x = rng.integers(-2, 3, K).astype(np.float32)
+    y = gemv_dev(gpu, "sgpu_gemv_h", W, x, None, K, N)
+    assert np.array_equal(y, og.gemv_h(W, x, None, K, N))    # all terms are integers: order-free
+
+
+@pytest.mark.parametrize("T", [1, 7, 16, 17, 128])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemv_multi(gpu, og, T, with_bias):
+    say(f"gemv_multi T={T} bias={with_bias}")
+    K, N = 768, 2304
+    W, s = gpu.gen_normal(N * K, 5, 0.0, 0.02)
+    X, s = gpu.gen_normal(T * K, s, 0.0, 1.0)
+    bias = gpu.gen_normal(N, s, 0.0, 0.1)[0] if with_bias else None
+    dW, dX = gpu.DeviceArray.from_host(W), gpu.DeviceArray.from_host(X)
+    db = gpu.DeviceArray.from_host(bias) if with_bias else None
+    dY = gpu.DeviceArray((T, N))
+    dY.fill_bytes(0xFF)
+    gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, db.ptr if db else None, dY.ptr, K, N, T, None)
+    gpu.synchronize()
+    ref = og.gemv_multi(W, X, bias, K, N, T, NT)
+    Y = dY.to_host()
+    assert np.all(np.abs(Y - ref) <= 1e-4 * np.abs(ref) + 1e-4)
+
+
+def test_gemv_multi_integer_ragged(gpu):
+    rng = np.random.default_rng(6)
+    K, N, T = 37, 29, 21
+    W = rng.integers(-3, 4, (N, K))
+    X = rng.integers(-3, 4, (T, K))
+    dW, dX = gpu.DeviceArray.from_host(W.astype(np.float32)), gpu.DeviceArray.from_host(X.astype(np.float32))
+    dY = gpu.DeviceArray((T, N))
+    gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, None, dY.ptr, K, N, T, None)
+    gpu.synchronize()
+    assert np.array_equal(dY.to_host(), (X @ W.T).astype(np.float32))
+
+
+def test_membw_read4_sums(gpu):
+    """Every thread's grid-stride sum, repeated `iters` times, lands in out[first index]
+    (switch_gpu.cu:41-54); integer-valued data makes the sums exact."""
+    import ctypes as ct
+
+    threads = ct.c_int()
+    gpu.call("sgpu_membw_read4", None, None, 0, 1, ct.byref(threads), None)
+    nthr = threads.value
+    n4 = 3 * nthr + 17
+    rng = np.random.default_rng(8)
+    buf = rng.integers(-8, 9, (n4, 4)).astype(np.float32)
+    dbuf = gpu.DeviceArray.from_host(buf)
+    dout = gpu.DeviceArray(nthr)
+    dout.fill_bytes(0xFF)
+    iters = 3
+    gpu.call("sgpu_membw_read4", dbuf.ptr, dout.ptr, n4, iters, ct.byref(threads), None)
+    gpu.synchronize()
+    out = dout.to_host()
+    row = buf.sum(axis=1)
+    want = np.zeros(nthr)
+    for j in range(0, n4, nthr):
+        seg = row[j:j + nthr]
+        want[:seg.size] += seg
+    assert np.array_equal(out, (iters * want).astype(np.float32))

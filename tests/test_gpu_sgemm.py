@@ -1,0 +1,164 @@
+"""SGEMM family on the GPU through the C ABI, against the oracle (og_sgemm, restating
+gpu_workload.c:97-98) and exact integer arithmetic.
+
+Bars: reference-generator inputs (srand(42), gpu_workload.c:81-82) at every size
+max|C - C_ref| / max|C_ref| <= 1e-4 and the reference verdict (5% + 1e-3) clean; small-integer
+inputs (|a|, |b| <= 2, every partial sum an exact fp32 integer) bit-exact against float64
+BLAS at every shape, including ragged edges and the full 4096^3."""
+import functools
+import json
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin")
+VARIANTS = ["sgpu_sgemm_tiled", "sgpu_sgemm_tiled4", "sgpu_sgemm_opt", "sgpu_sgemm_naive"]
+NORMWISE_TOL = 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def run_sgemm(gpu, fn, A, B, M, N, K, a_off=0, b_off=0):
+    """C = A B through launcher `fn`; a_off/b_off shift the operands by whole floats to
+    exercise unaligned base pointers.  C is pre-filled with NaN so unwritten cells show."""
+    dA = gpu.DeviceArray(M * K + a_off + 1)
+    dB = gpu.DeviceArray(K * N + b_off + 1)
+    if A.size:
+        gpu.call("sgpu_memcpy_htod", dA.offset(a_off), np.ascontiguousarray(A, np.float32).ctypes.data, A.size * 4)
+    if B.size:
+        gpu.call("sgpu_memcpy_htod", dB.offset(b_off), np.ascontiguousarray(B, np.float32).ctypes.data, B.size * 4)
+    dC = gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    gpu.call(fn, dA.offset(a_off), dB.offset(b_off), dC.ptr, M, N, K, None)
+    gpu.synchronize()
+    return dC.to_host()
+
+
+@functools.lru_cache(maxsize=None)
+def ref_inputs(M, N, K):
+    from sgpu import gen_sgemm_inputs
+
+    n = max(M * K, K * N)
+    A, B = gen_sgemm_inputs(n, 42)
+    return A[:M * K].reshape(M, K), B[:K * N].reshape(K, N)
+
+
+@functools.lru_cache(maxsize=None)
+def ref_golden(M, N, K):
+    import oracle
+
+    A, B = ref_inputs(M, N, K)
+    return oracle.sgemm_rows(A, B, M, N, K, 0, M, nthreads=min(16, os.cpu_count() or 1))
+
+
+@pytest.mark.parametrize("n", [256, 512, 1024])
+@pytest.mark.parametrize("fn", VARIANTS)
+def test_reference_generator(gpu, og, fn, n):
+    say(f"sgemm {fn} n={n} reference inputs")
+    A, B = ref_inputs(n, n, n)
+    C = run_sgemm(gpu, fn, A, B, n, n, n)
+    ref = ref_golden(n, n, n)
+    err = np.abs(C.astype(np.float64) - ref).max() / np.abs(ref).max()
+    assert err <= NORMWISE_TOL, err
+    assert og.sgemm_verdict_bad(C, ref, n, n) == 0
+
+
+@pytest.mark.parametrize("fn", VARIANTS[:3])
+def test_ragged_reference_generator(gpu, og, fn):
+    M, N, K = 1023, 1025, 997
+    say(f"sgemm {fn} ragged {M}x{N}x{K}")
+    A, B = ref_inputs(M, N, K)
+    C = run_sgemm(gpu, fn, A, B, M, N, K)
+    ref = ref_golden(M, N, K)
+    assert np.abs(C.astype(np.float64) - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    assert og.sgemm_verdict_bad(C, ref, M, N) == 0
+
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 16), (65, 33, 17), (127, 129, 131), (128, 128, 1), (256, 256, 256),
+          (300, 200, 64), (1023, 1025, 997), (257, 511, 1030)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("fn", VARIANTS)
+def test_integer_exact(gpu, fn, M, N, K):
+    say(f"sgemm {fn} integer {M}x{N}x{K}")
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    C = run_sgemm(gpu, fn, A, B, M, N, K)
+    assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("fn", VARIANTS[:3])
+def test_unaligned_pointers(gpu, fn):
+    M, N, K = 200, 136, 72
+    rng = np.random.default_rng(4)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    C = run_sgemm(gpu, fn, A, B, M, N, K, a_off=1, b_off=3)
+    assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("fn", VARIANTS)
+def test_k_zero_writes_zeros_and_empty_is_noop(gpu, fn):
+    C = run_sgemm(gpu, fn, np.zeros((5, 0), np.float32), np.zeros((0, 7), np.float32), 5, 7, 0)
+    assert np.array_equal(C, np.zeros((5, 7), np.float32))
+    assert getattr(gpu.lib(), fn)(None, None, None, 0, 7, 3, None) == 0
+
+
+@pytest.mark.parametrize("n", [2048, 4096])
+@pytest.mark.parametrize("fn", ["sgpu_sgemm_tiled4", "sgpu_sgemm_opt"])
+def test_full_size_integer_exact(gpu, fn, n):
+    say(f"sgemm {fn} integer {n}^3")
+    rng = np.random.default_rng(n)
+    A = rng.integers(-2, 3, (n, n)).astype(np.float32)
+    B = rng.integers(-2, 3, (n, n)).astype(np.float32)
+    C = run_sgemm(gpu, fn, A, B, n, n, n)
+    want = A.astype(np.float64) @ B.astype(np.float64)      # exact: |C| <= 4n < 2^24
+    assert np.array_equal(C, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("fn", ["sgpu_sgemm_tiled", "sgpu_sgemm_opt"])
+def test_4096_reference_generator_sampled_rows(gpu, og, fn):
+    n = 4096
+    say(f"sgemm {fn} 4096 reference inputs, sampled rows")
+    A, B = ref_inputs(n, n, n)
+    C = run_sgemm(gpu, fn, A, B, n, n, n)
+    rows = np.linspace(0, n - 1, 24).astype(int)
+    ref = np.stack([og.sgemm_rows(A, B, n, n, n, r, r + 1, 1)[r] for r in rows])
+    got = C[rows]
+    assert np.abs(got.astype(np.float64) - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    assert og.sgemm_verdict_bad(got, ref, len(rows), n) == 0
+
+
+@pytest.mark.parametrize("extra", [[], ["--ref-geometry"]])
+def test_gpu_workload_harness_json(gpu, extra):
+    """The harness flow end to end (module loaded from the .co file by path, kernels resolved
+    by name): the --json object passes the task-queue consumer's checks
+    (deploy/cluster/gpu_task_example.py:57-78) apart from its Tegra-sized GFLOPS bounds."""
+    co = os.path.join(ROOT, "switch-l4t-gpu_amd", "build", "switch_gpu.co")
+    cmd = [os.path.join(BIN, "gpu_workload"), "--json", "--membw-mb", "512", "--membw-iters", "2"] + extra
+    if not extra:
+        cmd += ["--extra", "2048", "--ragged"]
+    say("run", " ".join(cmd))
+    out = subprocess.run(cmd + [co], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    d = json.loads(out.stdout)
+    assert d["done"] is True
+    assert d["kernels"] == {"sgemm": "CORRECT", "sgemm_naive": "CORRECT", "sgemm_tiled4": "CORRECT",
+                            "sgemm_opt": "CORRECT"}
+    for key in ("sgemm", "sgemm4", "sgemm_opt"):
+        assert [r["n"] for r in d[key]] == [256, 512, 1024]
+        assert all(r["gflops"] > 1.0 for r in d[key])
+    assert d["membw_gbps"] > 100.0
+    for r in d.get("sgemm_extra", []):
+        assert r["verdict"] == "CORRECT"
