@@ -88,8 +88,11 @@ def test_gemv_h_special_codes(gpu, og):
     reference h2f contract (qwen_kernels.cu:6-14), exact with integer x."""
     rng = np.random.default_rng(3)
     N, K = 40, 896
+    # subnormals, -0/negative subnormals, exponent 31 (values 65536 + 64m: integers), and
+    # integer-valued normal codes 1, 2, 3, -1, -2 so every partial sum stays an exact fp32 integer
     codes = np.concatenate([np.arange(0, 1024), np.arange(0x8000, 0x8400), np.arange(0x7c00, 0x8000),
-                            np.arange(0xfc00, 0x10000), np.arange(0x3c00, 0x3c40)]).astype(np.uint16)
+                            np.arange(0xfc00, 0x10000),
+                            np.array([0x3c00, 0x4000, 0x4200, 0xbc00, 0xc000] * 40)]).astype(np.uint16)
     W = rng.choice(codes, (N, K)).astype(np.uint16)
     x = rng.integers(-2, 3, K).astype(np.float32)
     y = gemv_dev(gpu, "sgpu_gemv_h", W, x, None, K, N)
