@@ -138,6 +138,40 @@ def cpu_baseline(n, target_s=1.5):
                        f"of the {n}^3 SGEMM ({2.0 * rows * n * n / 1e9:.1f} GFLOP), {dt:.2f} s on {threads} threads")
 
 
+def pmc_probe():
+    """One launch each of: add2 over 64 Mi floats (a plain elementwise kernel whose HBM
+    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), sgemm_opt
+    4096^3 and the lm_head gemv_h.  Run under `rocprofv3 --pmc FETCH_SIZE` and again with
+    WRITE_SIZE; prints the algorithmic bytes of each launch as one JSON line."""
+    n = 64 << 20
+    a = sgpu.DeviceArray(n)
+    b = sgpu.DeviceArray(n)
+    c = sgpu.DeviceArray(n)
+    for d in (a, b, c):
+        d.fill_bytes(0)
+    sgpu.synchronize()
+    sgpu.call("sgpu_add2", a.ptr, b.ptr, c.ptr, n, None)
+    sgpu.synchronize()
+    del a, b, c
+    N4 = 4096
+    A, B = sgpu.gen_sgemm_inputs(N4 * N4, 42)
+    dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((N4, N4))
+    sgpu.synchronize()
+    sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, N4, N4, N4, None)
+    sgpu.synchronize()
+    del dA, dB, dC
+    N, K = 151936, 896
+    W = sgpu.f32_to_f16(sgpu.gen_normal(N * K, 42, 0.0, 0.02)[0])
+    dW, dx, dy = sgpu.DeviceArray.from_host(W), sgpu.DeviceArray(K), sgpu.DeviceArray(N)
+    dx.fill_bytes(0)
+    sgpu.synchronize()
+    sgpu.call("sgpu_gemv_h", dW.ptr, dx.ptr, None, dy.ptr, K, N, None)
+    sgpu.synchronize()
+    print(json.dumps({"add2_read": 2 * 4 * n, "add2_write": 4 * n,
+                      "sgemm_opt_read_min": 2 * 4 * N4 * N4, "sgemm_opt_write": 4 * N4 * N4,
+                      "gemv_h_read": 2 * N * K + 4 * K, "gemv_h_write": 4 * N}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,7 +179,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--pmc-probe", action="store_true", help="one launch per measured kernel, for rocprofv3 --pmc")
     args = ap.parse_args()
+    if args.pmc_probe:
+        sgpu.init(0)
+        pmc_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
               f"multi-GPU path; run with --gpus 1)", file=sys.stderr)

@@ -27,6 +27,7 @@ struct WF32 {
     typedef float elem;
     typedef sgpu_f32x4 vec;
     static constexpr int VEC = 4;
+    static constexpr bool NEEDS_RECHECK = false;
     __device__ static __forceinline__ float dot(const vec& w, const float* xv, float acc) {
         acc = __builtin_fmaf(w[0], xv[0], acc);
         acc = __builtin_fmaf(w[1], xv[1], acc);
@@ -36,20 +37,41 @@ struct WF32 {
     }
     __device__ static __forceinline__ float one(elem w) { return w; }
 };
+// fp16 weights.  The hot loop converts with the hardware (one v_fma_mix_f32 or
+// v_cvt_f32_f16 + FMA per weight).  The code objects holding these kernels are built with
+// the fp16 denormal mode set to flush, so an fp16 subnormal reads as +-0 -- which sums to
+// exactly what the reference's +0 gives (a running sum that starts at +0 never becomes -0).
+// The one code class the hardware converts differently is exponent 31 (inf/NaN in IEEE, the
+// finite 2^16 (1 + m/1024) in the reference); any such weight makes the row's sum
+// non-finite, and those rows are recomputed with the exact integer decode (recompute_row).
 struct WF16 {
     typedef uint16_t elem;
     typedef sgpu_u32x4 vec;
     static constexpr int VEC = 8;
+    static constexpr bool NEEDS_RECHECK = true;
+    __device__ static __forceinline__ float cvt(uint32_t bits16) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+    }
     __device__ static __forceinline__ float dot(const vec& w, const float* xv, float acc) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            acc = __builtin_fmaf(sgpu_h2f_lo(w[i]), xv[2 * i], acc);
-            acc = __builtin_fmaf(sgpu_h2f_hi(w[i]), xv[2 * i + 1], acc);
+            acc = __builtin_fmaf(cvt(w[i] & 0xffffu), xv[2 * i], acc);
+            acc = __builtin_fmaf(cvt(w[i] >> 16), xv[2 * i + 1], acc);
         }
         return acc;
     }
     __device__ static __forceinline__ float one(elem w) { return sgpu_h2f(w); }
 };
+
+// Serial k-ascending dot product of one row with the exact reference decode; used for the
+// rare rows whose fast sum is not finite.
+template <class WT>
+__device__ __noinline__ float recompute_row(const typename WT::elem* __restrict__ row, const float* __restrict__ x,
+                                            int K) {
+    float acc = 0.0f;
+    for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
+    return acc;
+}
 
 // ---------------------------------------------------------------------------------------
 // Generic: wave per row.
@@ -111,7 +133,10 @@ __device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict
             for (int k = lane; k < K; k += 64) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
         }
         acc = sgpu_group_sum<64>(acc);
-        if (lane == 63) y[n] = acc + (bias ? bias[n] : 0.0f);
+        if (lane == 63) {
+            if (WT::NEEDS_RECHECK && !__builtin_isfinite(acc)) acc = recompute_row<WT>(row, x, K);
+            y[n] = acc + (bias ? bias[n] : 0.0f);
+        }
     }
 }
 
@@ -168,7 +193,10 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
         }
         if constexpr (LPR <= 64) {
             acc = sgpu_group_sum<LPR>(acc);
-            if (sub == LPR - 1 && n < N) y[n] = acc + (bias ? bias[n] : 0.0f);
+            if (sub == LPR - 1 && n < N) {
+                if (WT::NEEDS_RECHECK && !__builtin_isfinite(acc)) acc = recompute_row<WT>(W + (size_t)n * K, x, K);
+                y[n] = acc + (bias ? bias[n] : 0.0f);
+            }
         } else {
             acc = sgpu_group_sum<64>(acc);
             if (lane == 63) red[wave] = acc;
@@ -177,6 +205,7 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
                 float s = 0.0f;
 #pragma unroll
                 for (int i = 0; i < WAVES_PER_TEAM; i++) s += red[team * WAVES_PER_TEAM + i];
+                if (WT::NEEDS_RECHECK && !__builtin_isfinite(s)) s = recompute_row<WT>(W + (size_t)n * K, x, K);
                 y[n] = s + (bias ? bias[n] : 0.0f);
             }
             __syncthreads();
