@@ -152,6 +152,50 @@ int sgpu_attn_mix_gqa(const float *probs, const float *vc, float *out, int T, in
 /* qwen_kernels.cu:183-189, launched qwen_engine.c:244,258. */
 int sgpu_add2(const float *a, const float *b, float *out, int n, void *stream);
 
+/* ---- GPT-2 124M decode support kernels (gpt2_kernels.cu:157-268), launched per layer by
+ * gpt2_engine.c gpu_forward (:174-264) and gpu_prefill (:269-326).  The attention kernels keep
+ * the reference's fixed layout: 12 heads of 64, K/V cache rows of 768 floats. ---- */
+/* rows independent rows of n: (x - mean)/sqrt(var + eps) * w + b (gpt2_kernels.cu:160-196). */
+int sgpu_layernorm(const float *x, const float *w, const float *b, float *y, int n, float eps, int rows,
+                   void *stream);
+/* tanh-form GELU, y may alias x (gpt2_kernels.cu:199-206, launched gpt2_engine.c:236). */
+int sgpu_gelu(const float *x, float *y, int n, void *stream);
+/* y += bias (gpt2_kernels.cu:209-212, launched gpt2_engine.c:190,216,232,245). */
+int sgpu_add_bias(float *y, const float *bias, int n, void *stream);
+/* attn_scores (gpt2_kernels.cu:221-234, launched gpt2_engine.c:199-200). */
+int sgpu_gpt2_attn_scores(const float *q, const float *kcache, float *scores, int T, float scale, void *stream);
+/* attn_softmax (gpt2_kernels.cu:238-253, launched gpt2_engine.c:201-202). */
+int sgpu_gpt2_attn_softmax(const float *scores, float *probs, int T, void *stream);
+/* attn_mix (gpt2_kernels.cu:258-268, launched gpt2_engine.c:203-204). */
+int sgpu_gpt2_attn_mix(const float *probs, const float *vcache, float *out, int T, void *stream);
+
+/* ---- GPT-2 124M fp32 decode engine (gpt2_engine.c:88-326) ---- */
+typedef struct {
+    int V, C, NL, NH, HD, FC, CTX;
+    float eps;       /* LayerNorm eps (gpt2_engine.c:77: 1e-5) */
+} sgpu_gpt2_cfg;
+/* gpt2_engine.c:40-48: V 50257, C 768, 12 heads of 64, 12 layers, FC 3072, CTX 1024.  The
+ * attention kernels fix C = 768, NH = 12, HD = 64; V, NL, CTX and FC may differ. */
+void sgpu_gpt2_default_cfg(sgpu_gpt2_cfg *cfg);
+/* Float count of the flat fp32 weight file (gpt2_engine.c:50-70 layout; conv_gpt2.py writer):
+ * 124,439,808 at the default dims. */
+size_t sgpu_gpt2_file_floats(const sgpu_gpt2_cfg *cfg);
+/* Random-init weights in that layout (make_random_bin.py role): every float
+ * (frand() - 0.5) * 2 * amp from the seeded LCG. */
+int sgpu_gpt2_fill_random(float *blob, const sgpu_gpt2_cfg *cfg, uint64_t seed, float amp);
+
+typedef struct sgpu_gpt2 sgpu_gpt2;
+/* gpu_setup (gpt2_engine.c:108-166): uploads the host weights, allocates fp32 KV caches and
+ * the batched-prefill buffers. */
+int sgpu_gpt2_create(sgpu_gpt2 **engine, const sgpu_gpt2_cfg *cfg, const float *blob);
+void sgpu_gpt2_destroy(sgpu_gpt2 *engine);
+/* gpu_forward (gpt2_engine.c:174-264): fused != 0 takes the --fused path (gemv_warp_b),
+ * otherwise gemv_warp + add_bias.  Logits (V floats) copied to logits_host if want_logits. */
+int sgpu_gpt2_forward(sgpu_gpt2 *engine, int token, int pos, int want_logits, float *logits_host, int fused);
+/* gpu_prefill (gpt2_engine.c:269-326): all T prompt positions through the layers with the
+ * weight-stationary gemv_multi; fills cache positions 0..T-1; logits of the last row. */
+int sgpu_gpt2_prefill(sgpu_gpt2 *engine, const int *ids, int T, float *logits_host);
+
 /* ---- Qwen2.5 decode engine (qwen_engine.c:105-269): weights resident on the device,
  * fp32 KV cache, the reference's per-layer launch sequence per position. ---- */
 typedef struct {

@@ -258,3 +258,108 @@ int og_qwen_forward(const og_qwen_cfg *c, const void *blob, float *kc, float *vc
     free(r_gate); free(r_down); free(sc);
     return 0;
 }
+
+/* ---- GPT-2 ---- */
+typedef struct {
+    size_t wte, wpe, l_base, lstride, lnfw, lnfb, total;
+    size_t ln1w, ln1b, qkvw, qkvb, aow, aob, ln2w, ln2b, fcw, fcb, projw, projb;
+} g2layout;
+
+/* gpt2_engine.c:50-70 */
+static void g2_layout(const og_gpt2_cfg *c, g2layout *L) {
+    const size_t C = (size_t)c->C, FC = (size_t)c->FC;
+    L->wte = 0;
+    L->wpe = (size_t)c->V * C;
+    L->l_base = L->wpe + (size_t)c->CTX * C;
+    L->lstride = 2 * C + 3 * C * C + 3 * C + C * C + C + 2 * C + FC * C + FC + FC * C + C;
+    L->lnfw = L->l_base + (size_t)c->NL * L->lstride;
+    L->lnfb = L->lnfw + C;
+    L->total = L->lnfb + C;
+    L->ln1w = 0; L->ln1b = C; L->qkvw = 2 * C; L->qkvb = L->qkvw + 3 * C * C; L->aow = L->qkvb + 3 * C;
+    L->aob = L->aow + C * C; L->ln2w = L->aob + C; L->ln2b = L->ln2w + C; L->fcw = L->ln2b + C;
+    L->fcb = L->fcw + FC * C; L->projw = L->fcb + FC; L->projb = L->projw + FC * C;
+}
+
+size_t og_gpt2_file_floats(const og_gpt2_cfg *cfg) {
+    g2layout L;
+    g2_layout(cfg, &L);
+    return L.total;
+}
+
+/* cpu_ln, gpt2_engine.c:333-341 */
+void og_layernorm(const float *x, const float *w, const float *b, float *y, int n, float eps) {
+    float mean = 0.0f, var = 0.0f;
+    for (int i = 0; i < n; i++) mean += x[i];
+    mean /= n;
+    for (int i = 0; i < n; i++) {
+        float d = x[i] - mean;
+        var += d * d;
+    }
+    var /= n;
+    float inv = 1.0f / sqrtf(var + eps);
+    for (int i = 0; i < n; i++) y[i] = (x[i] - mean) * inv * w[i] + b[i];
+}
+
+/* cpu_forward, gpt2_engine.c:363-421 (attention scale 0.125 = 1/sqrt(HD), gelu tanh form) */
+int og_gpt2_forward(const og_gpt2_cfg *c, const float *w, float *kc, float *vc, int token, int pos,
+                    int want_logits, float *logits, float *trace, int nthreads) {
+    if (!c || !w || !kc || !vc || token < 0 || token >= c->V || pos < 0 || pos >= c->CTX || c->NH * c->HD != c->C)
+        return -1;
+    g2layout L;
+    g2_layout(c, &L);
+    const int C = c->C, NH = c->NH, HD = c->HD, FC = c->FC, CTX = c->CTX;
+    const float scale = (float)(1.0 / sqrt((double)HD));
+    float *r_x = malloc(sizeof(float) * C), *r_ln = malloc(sizeof(float) * C);
+    float *r_qkv = malloc(sizeof(float) * 3 * C), *r_att = malloc(sizeof(float) * C);
+    float *r_y = malloc(sizeof(float) * C), *r_fc = malloc(sizeof(float) * FC);
+    float *sc = malloc(sizeof(float) * (pos + 1));
+    if (!r_x || !r_ln || !r_qkv || !r_att || !r_y || !r_fc || !sc) {
+        free(r_x); free(r_ln); free(r_qkv); free(r_att); free(r_y); free(r_fc); free(sc);
+        return -1;
+    }
+    for (int i = 0; i < C; i++) r_x[i] = w[L.wte + (size_t)token * C + i] + w[L.wpe + (size_t)pos * C + i];
+    for (int l = 0; l < c->NL; l++) {
+        const float *b = w + L.l_base + (size_t)l * L.lstride;
+        og_layernorm(r_x, b + L.ln1w, b + L.ln1b, r_ln, C, c->eps);
+        og_gemv(b + L.qkvw, r_ln, b + L.qkvb, r_qkv, C, 3 * C, nthreads);
+        for (int i = 0; i < C; i++) {
+            kc[((size_t)l * CTX + pos) * C + i] = r_qkv[C + i];
+            vc[((size_t)l * CTX + pos) * C + i] = r_qkv[2 * C + i];
+        }
+        for (int h = 0; h < NH; h++) {
+            float maxv = -1e30f, sum = 0.0f;
+            for (int t = 0; t <= pos; t++) {
+                const float *kh = kc + ((size_t)l * CTX + t) * C + h * HD;
+                const float *qh = r_qkv + h * HD;
+                float acc = 0.0f;
+                for (int d = 0; d < HD; d++) acc += qh[d] * kh[d];
+                sc[t] = acc * scale;
+                if (sc[t] > maxv) maxv = sc[t];
+            }
+            for (int t = 0; t <= pos; t++) { sc[t] = expf(sc[t] - maxv); sum += sc[t]; }
+            for (int d = 0; d < HD; d++) {
+                float acc = 0.0f;
+                for (int t = 0; t <= pos; t++) acc += sc[t] * vc[((size_t)l * CTX + t) * C + h * HD + d];
+                r_att[h * HD + d] = acc / sum;
+            }
+        }
+        og_gemv(b + L.aow, r_att, b + L.aob, r_y, C, C, nthreads);
+        for (int i = 0; i < C; i++) r_x[i] += r_y[i];
+        og_layernorm(r_x, b + L.ln2w, b + L.ln2b, r_ln, C, c->eps);
+        og_gemv(b + L.fcw, r_ln, b + L.fcb, r_fc, C, FC, nthreads);
+        for (int i = 0; i < FC; i++) {
+            float v = r_fc[i];
+            float t = 0.7978845608f * (v + 0.044715f * v * v * v);
+            r_fc[i] = 0.5f * v * (1.0f + tanhf(t));
+        }
+        og_gemv(b + L.projw, r_fc, b + L.projb, r_y, FC, C, nthreads);
+        for (int i = 0; i < C; i++) r_x[i] += r_y[i];
+        if (trace) memcpy(trace + (size_t)l * C, r_x, sizeof(float) * C);
+    }
+    if (want_logits && logits) {
+        og_layernorm(r_x, w + L.lnfw, w + L.lnfb, r_ln, C, c->eps);
+        og_gemv(w + L.wte, r_ln, NULL, logits, C, c->V, nthreads);   /* tied lm_head, no bias */
+    }
+    free(r_x); free(r_ln); free(r_qkv); free(r_att); free(r_y); free(r_fc); free(sc);
+    return 0;
+}

@@ -87,6 +87,20 @@ int og_qwen_forward(const og_qwen_cfg *cfg, const void *blob, float *kc, float *
                     int token, int pos, int want_logits, float *logits, float *trace,
                     int nthreads);
 
+/* ---- GPT-2 124M fp32 decode (gpt2_engine.c:40-70 dims/layout, :333-349 cpu_ln/cpu_gemv,
+ * :363-421 cpu_forward) ---- */
+typedef struct {
+    int V, C, NL, NH, HD, FC, CTX;
+    float eps;     /* LayerNorm eps, 1e-5 (gpt2_engine.c:339) */
+} og_gpt2_cfg;
+/* Float count of the flat fp32 weight file (gpt2_engine.c:50-58). */
+size_t og_gpt2_file_floats(const og_gpt2_cfg *cfg);
+/* LayerNorm with two-pass mean/variance, cpu_ln (gpt2_engine.c:333-341). */
+void og_layernorm(const float *x, const float *w, const float *b, float *y, int n, float eps);
+/* One decode position (cpu_forward).  kc/vc: NL*CTX*C fp32 caches.  Returns 0 or -1. */
+int og_gpt2_forward(const og_gpt2_cfg *cfg, const float *w, float *kc, float *vc, int token, int pos,
+                    int want_logits, float *logits, float *trace, int nthreads);
+
 /* First-max argmax (qwen_engine.c:360-364). */
 int og_argmax(const float *v, int n);
 

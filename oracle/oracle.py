@@ -21,6 +21,11 @@ class QwenCfg(ct.Structure):
                 ("HD", ct.c_int), ("FC", ct.c_int), ("CTX", ct.c_int), ("eps", ct.c_float), ("theta", ct.c_float)]
 
 
+class Gpt2Cfg(ct.Structure):
+    _fields_ = [("V", ct.c_int), ("C", ct.c_int), ("NL", ct.c_int), ("NH", ct.c_int), ("HD", ct.c_int),
+                ("FC", ct.c_int), ("CTX", ct.c_int), ("eps", ct.c_float)]
+
+
 _P, _I, _F, _S = ct.c_void_p, ct.c_int, ct.c_float, ct.c_size_t
 _SIGS = {
     "og_h2f": (_F, [ct.c_uint16]),
@@ -36,6 +41,9 @@ _SIGS = {
     "og_rope_tables": (None, [_I, _I, ct.c_double, _P, _P]),
     "og_qwen_forward": (_I, [ct.POINTER(QwenCfg), _P, _P, _P, _I, _I, _I, _P, _P, _I]),
     "og_argmax": (_I, [_P, _I]),
+    "og_gpt2_file_floats": (_S, [ct.POINTER(Gpt2Cfg)]),
+    "og_layernorm": (None, [_P, _P, _P, _P, _I, _F]),
+    "og_gpt2_forward": (_I, [ct.POINTER(Gpt2Cfg), _P, _P, _P, _I, _I, _I, _P, _P, _I]),
 }
 
 _lib = None
@@ -171,4 +179,38 @@ class QwenGolden:
                                    self.logits.ctypes.data if want_logits else None, tr, self.nthreads)
         if rc != 0:
             raise ValueError("og_qwen_forward rejected its arguments")
+        return self.logits.copy() if want_logits else None
+
+
+def layernorm(x, w, b, eps=1e-5):
+    x, w, b = _f32(x), _f32(w), _f32(b)
+    y = np.empty_like(x)
+    lib().og_layernorm(x.ctypes.data, w.ctypes.data, b.ctypes.data, y.ctypes.data, x.size, eps)
+    return y
+
+
+def gpt2_cfg(V=50257, C=768, NL=12, NH=12, HD=64, FC=3072, CTX=1024, eps=1e-5) -> Gpt2Cfg:
+    return Gpt2Cfg(V, C, NL, NH, HD, FC, CTX, eps)
+
+
+def gpt2_file_floats(cfg: Gpt2Cfg) -> int:
+    return lib().og_gpt2_file_floats(ct.byref(cfg))
+
+
+class Gpt2Golden:
+    """GPT-2 cpu_forward with its own fp32 KV cache."""
+
+    def __init__(self, cfg: Gpt2Cfg, weights: np.ndarray, nthreads: int = 1):
+        self.cfg, self.w, self.nthreads = cfg, _f32(weights), nthreads
+        self.kc = np.zeros(cfg.NL * cfg.CTX * cfg.C, np.float32)
+        self.vc = np.zeros_like(self.kc)
+        self.logits = np.empty(cfg.V, np.float32)
+
+    def forward(self, token, pos, want_logits=True, trace=None):
+        tr = trace.ctypes.data if trace is not None else None
+        rc = lib().og_gpt2_forward(ct.byref(self.cfg), self.w.ctypes.data, self.kc.ctypes.data, self.vc.ctypes.data,
+                                   token, pos, int(want_logits), self.logits.ctypes.data if want_logits else None,
+                                   tr, self.nthreads)
+        if rc != 0:
+            raise ValueError("og_gpt2_forward rejected its arguments")
         return self.logits.copy() if want_logits else None

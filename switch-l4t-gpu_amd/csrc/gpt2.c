@@ -1,0 +1,223 @@
+/* gpt2.c -- GPT-2 124M fp32 decode engine over the C-ABI launchers (part of libswitchgpu.so).
+ *
+ * The device side of gpt2_engine.c: weight upload and buffers (gpu_setup, :108-166), the
+ * per-position forward (gpu_forward, :174-264) with its --fused variant (gemv_warp_b instead
+ * of gemv_warp + add_bias), and the batched prompt prefill (gpu_prefill, :269-326) that runs
+ * every projection through the weight-stationary gemv_multi.
+ * Weight layout (gpt2_engine.c:10-13,50-70; writer conv_gpt2.py:37-52), fp32:
+ *   wte[V*C] wpe[CTX*C] { ln1_w ln1_b qkv_w[3C*C] qkv_b[3C] ao_w[C*C] ao_b ln2_w ln2_b
+ *   fc_w[FC*C] fc_b[FC] proj_w[C*FC] proj_b } x NL, ln_f_w[C] ln_f_b[C]
+ */
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+
+#include <stdlib.h>
+#include <string.h>
+
+#include "switch_gpu.h"
+
+typedef struct {
+    size_t wte, wpe, l_base, lstride, lnfw, lnfb, total;                       /* floats */
+    size_t ln1w, ln1b, qkvw, qkvb, aow, aob, ln2w, ln2b, fcw, fcb, projw, projb;  /* in-layer */
+} g2layout;
+
+static void g2_layout(const sgpu_gpt2_cfg *c, g2layout *L) {
+    const size_t C = (size_t)c->C, FC = (size_t)c->FC;
+    L->wte = 0;
+    L->wpe = (size_t)c->V * C;
+    L->l_base = L->wpe + (size_t)c->CTX * C;
+    L->lstride = 2 * C + 3 * C * C + 3 * C + C * C + C + 2 * C + FC * C + FC + FC * C + C;
+    L->lnfw = L->l_base + (size_t)c->NL * L->lstride;
+    L->lnfb = L->lnfw + C;
+    L->total = L->lnfb + C;
+    L->ln1w = 0; L->ln1b = C; L->qkvw = 2 * C; L->qkvb = L->qkvw + 3 * C * C; L->aow = L->qkvb + 3 * C;
+    L->aob = L->aow + C * C; L->ln2w = L->aob + C; L->ln2b = L->ln2w + C; L->fcw = L->ln2b + C;
+    L->fcb = L->fcw + FC * C; L->projw = L->fcb + FC; L->projb = L->projw + FC * C;
+}
+
+static int cfg_ok(const sgpu_gpt2_cfg *c) {
+    /* the attention kernels fix 12 heads of 64 in rows of 768 (gpt2_kernels.cu:5) */
+    return c && c->C == 768 && c->NH == 12 && c->HD == 64 && c->V > 0 && c->NL > 0 && c->FC > 0 &&
+           c->CTX > 0 && (long long)c->CTX * c->FC < 0x7fffffffLL;
+}
+
+void sgpu_gpt2_default_cfg(sgpu_gpt2_cfg *c) {
+    c->V = 50257; c->C = 768; c->NL = 12; c->NH = 12; c->HD = 64; c->FC = 3072; c->CTX = 1024; c->eps = 1e-5f;
+}
+
+size_t sgpu_gpt2_file_floats(const sgpu_gpt2_cfg *c) {
+    if (!cfg_ok(c)) return 0;
+    g2layout L;
+    g2_layout(c, &L);
+    return L.total;
+}
+
+int sgpu_gpt2_fill_random(float *blob, const sgpu_gpt2_cfg *c, uint64_t seed, float amp) {
+    if (!blob || !cfg_ok(c)) return SGPU_ERR_INVALID_ARG;
+    g2layout L;
+    g2_layout(c, &L);
+    uint64_t s = seed;
+    sgpu_gen_uniform(blob, L.total, &s, -0.5f);
+    for (size_t i = 0; i < L.total; i++) blob[i] *= 2.0f * amp;
+    return SGPU_OK;
+}
+
+struct sgpu_gpt2 {
+    sgpu_gpt2_cfg cfg;
+    g2layout L;
+    hipStream_t stream;
+    float *w;                                       /* the whole weight file on the device */
+    float **kc, **vc;
+    float *x, *ln1, *qkv, *att, *y, *ln2, *fc, *scores, *probs, *logits, *x2;
+    float *xT, *ln1T, *qkvT, *attT, *yT, *ln2T, *fcT;     /* batched prefill */
+};
+
+void sgpu_gpt2_destroy(sgpu_gpt2 *e) {
+    if (!e) return;
+    float *bufs[] = {e->w, e->x, e->ln1, e->qkv, e->att, e->y, e->ln2, e->fc, e->scores, e->probs, e->logits,
+                     e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) sgpu_free(bufs[i]);
+    for (int l = 0; l < e->cfg.NL; l++) {
+        if (e->kc) sgpu_free(e->kc[l]);
+        if (e->vc) sgpu_free(e->vc[l]);
+    }
+    free(e->kc);
+    free(e->vc);
+    if (e->stream) hipStreamDestroy(e->stream);
+    free(e);
+}
+
+static int zalloc(float **p, size_t floats) {
+    int rc = sgpu_malloc((void **)p, floats * 4);
+    if (rc) return rc;
+    return sgpu_memset_d8(*p, 0, floats * 4);
+}
+
+int sgpu_gpt2_create(sgpu_gpt2 **out, const sgpu_gpt2_cfg *c, const float *blob) {
+    if (!out || !blob || !cfg_ok(c)) return SGPU_ERR_INVALID_ARG;
+    *out = NULL;
+    int dev = 0, rc;
+    if (hipGetDevice(&dev) != hipSuccess) return SGPU_ERR_NO_DEVICE;
+    if ((rc = sgpu_init(dev))) return rc;
+    sgpu_gpt2 *e = calloc(1, sizeof *e);
+    if (!e) return SGPU_ERR_HOST_ALLOC;
+    e->cfg = *c;
+    g2_layout(c, &e->L);
+    const size_t C = (size_t)c->C, FC = (size_t)c->FC, CTX = (size_t)c->CTX;
+#define TRY(x) do { if ((rc = (x))) goto fail; } while (0)
+    if (hipStreamCreate(&e->stream) != hipSuccess) { rc = SGPU_ERR_NO_DEVICE; goto fail; }
+    e->kc = calloc((size_t)c->NL, sizeof(float *));
+    e->vc = calloc((size_t)c->NL, sizeof(float *));
+    if (!e->kc || !e->vc) { rc = SGPU_ERR_HOST_ALLOC; goto fail; }
+    TRY(sgpu_malloc((void **)&e->w, e->L.total * 4));
+    TRY(sgpu_memcpy_htod(e->w, blob, e->L.total * 4));
+    for (int l = 0; l < c->NL; l++) {
+        TRY(zalloc(&e->kc[l], CTX * C));
+        TRY(zalloc(&e->vc[l], CTX * C));
+    }
+    TRY(zalloc(&e->x, C)); TRY(zalloc(&e->ln1, C)); TRY(zalloc(&e->qkv, 3 * C)); TRY(zalloc(&e->att, C));
+    TRY(zalloc(&e->y, C)); TRY(zalloc(&e->ln2, C)); TRY(zalloc(&e->fc, FC)); TRY(zalloc(&e->x2, C));
+    TRY(zalloc(&e->scores, CTX * 12)); TRY(zalloc(&e->probs, CTX * 12)); TRY(zalloc(&e->logits, (size_t)c->V));
+    TRY(zalloc(&e->xT, CTX * C)); TRY(zalloc(&e->ln1T, CTX * C)); TRY(zalloc(&e->qkvT, CTX * 3 * C));
+    TRY(zalloc(&e->attT, CTX * C)); TRY(zalloc(&e->yT, CTX * C)); TRY(zalloc(&e->ln2T, CTX * C));
+    TRY(zalloc(&e->fcT, CTX * FC));
+#undef TRY
+    *out = e;
+    return SGPU_OK;
+fail:
+    sgpu_gpt2_destroy(e);
+    return rc;
+}
+
+static int logits_out(sgpu_gpt2 *e, const float *xrow, float *logits_host) {
+    const int C = e->cfg.C;
+    void *s = (void *)e->stream;
+    const float *W = e->w;
+    int rc;
+    if ((rc = sgpu_layernorm(xrow, W + e->L.lnfw, W + e->L.lnfb, e->x2, C, e->cfg.eps, 1, s))) return rc;
+    if ((rc = sgpu_gemv_warp(W + e->L.wte, e->x2, e->logits, C, e->cfg.V, s))) return rc;   /* tied lm_head */
+    if (logits_host) {
+        hipError_t he = hipMemcpyAsync(logits_host, e->logits, (size_t)e->cfg.V * 4, hipMemcpyDeviceToHost, e->stream);
+        if (he != hipSuccess) return (int)he;
+        return sgpu_stream_synchronize(s);
+    }
+    return SGPU_OK;
+}
+
+/* One projection y = W x + b, fused (gemv_warp_b) or as the reference's two launches. */
+static int proj(const float *W, const float *x, const float *b, float *y, int K, int N, int fused, void *s) {
+    if (fused) return sgpu_gemv_warp_b(W, x, b, y, K, N, s);
+    int rc = sgpu_gemv_warp(W, x, y, K, N, s);
+    return rc ? rc : sgpu_add_bias(y, b, N, s);
+}
+
+int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host, int fused) {
+    if (!e) return SGPU_ERR_INVALID_ARG;
+    const sgpu_gpt2_cfg *c = &e->cfg;
+    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
+    const int C = c->C, FC = c->FC, T = pos + 1;
+    const float eps = c->eps, scale = 0.125f;   /* 1/sqrt(64), gpt2_engine.c:75 */
+    void *s = (void *)e->stream;
+    const float *W = e->w;
+    int rc;
+#define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+    /* x = wte[token] + wpe[pos] (the reference adds on the host, gpt2_engine.c:176-179) */
+    TRY(sgpu_add2(W + e->L.wte + (size_t)token * C, W + e->L.wpe + (size_t)pos * C, e->x, C, s));
+    for (int l = 0; l < c->NL; l++) {
+        const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
+        TRY(sgpu_layernorm(e->x, b + e->L.ln1w, b + e->L.ln1b, e->ln1, C, eps, 1, s));
+        TRY(proj(b + e->L.qkvw, e->ln1, b + e->L.qkvb, e->qkv, C, 3 * C, fused, s));
+        TRY(sgpu_memcpy_dtod_async(e->kc[l] + (size_t)pos * C, e->qkv + C, (size_t)C * 4, s));
+        TRY(sgpu_memcpy_dtod_async(e->vc[l] + (size_t)pos * C, e->qkv + 2 * C, (size_t)C * 4, s));
+        TRY(sgpu_gpt2_attn_scores(e->qkv, e->kc[l], e->scores, T, scale, s));
+        TRY(sgpu_gpt2_attn_softmax(e->scores, e->probs, T, s));
+        TRY(sgpu_gpt2_attn_mix(e->probs, e->vc[l], e->att, T, s));
+        TRY(proj(b + e->L.aow, e->att, b + e->L.aob, e->y, C, C, fused, s));
+        TRY(sgpu_add2(e->x, e->y, e->x, C, s));
+        TRY(sgpu_layernorm(e->x, b + e->L.ln2w, b + e->L.ln2b, e->ln2, C, eps, 1, s));
+        TRY(proj(b + e->L.fcw, e->ln2, b + e->L.fcb, e->fc, C, FC, fused, s));
+        TRY(sgpu_gelu(e->fc, e->fc, FC, s));
+        TRY(proj(b + e->L.projw, e->fc, b + e->L.projb, e->y, FC, C, fused, s));
+        TRY(sgpu_add2(e->x, e->y, e->x, C, s));
+    }
+#undef TRY
+    return want_logits ? logits_out(e, e->x, logits_host) : SGPU_OK;
+}
+
+int sgpu_gpt2_prefill(sgpu_gpt2 *e, const int *ids, int T, float *logits_host) {
+    if (!e || !ids) return SGPU_ERR_INVALID_ARG;
+    const sgpu_gpt2_cfg *c = &e->cfg;
+    if (T <= 0 || T > c->CTX) return SGPU_ERR_INVALID_ARG;
+    for (int t = 0; t < T; t++)
+        if (ids[t] < 0 || ids[t] >= c->V) return SGPU_ERR_INVALID_ARG;
+    const int C = c->C, FC = c->FC;
+    const float eps = c->eps, scale = 0.125f;
+    void *s = (void *)e->stream;
+    const float *W = e->w;
+    int rc;
+#define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+    for (int t = 0; t < T; t++)
+        TRY(sgpu_add2(W + e->L.wte + (size_t)ids[t] * C, W + e->L.wpe + (size_t)t * C, e->xT + (size_t)t * C, C, s));
+    for (int l = 0; l < c->NL; l++) {
+        const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
+        TRY(sgpu_layernorm(e->xT, b + e->L.ln1w, b + e->L.ln1b, e->ln1T, C, eps, T, s));
+        TRY(sgpu_gemv_multi(b + e->L.qkvw, e->ln1T, b + e->L.qkvb, e->qkvT, C, 3 * C, T, s));
+        for (int t = 0; t < T; t++) {     /* causal attention, one query row at a time */
+            const float *qrow = e->qkvT + (size_t)t * 3 * C;
+            TRY(sgpu_memcpy_dtod_async(e->kc[l] + (size_t)t * C, qrow + C, (size_t)C * 4, s));
+            TRY(sgpu_memcpy_dtod_async(e->vc[l] + (size_t)t * C, qrow + 2 * C, (size_t)C * 4, s));
+            TRY(sgpu_gpt2_attn_scores(qrow, e->kc[l], e->scores, t + 1, scale, s));
+            TRY(sgpu_gpt2_attn_softmax(e->scores, e->probs, t + 1, s));
+            TRY(sgpu_gpt2_attn_mix(e->probs, e->vc[l], e->attT + (size_t)t * C, t + 1, s));
+        }
+        TRY(sgpu_gemv_multi(b + e->L.aow, e->attT, b + e->L.aob, e->yT, C, C, T, s));
+        TRY(sgpu_add2(e->xT, e->yT, e->xT, T * C, s));
+        TRY(sgpu_layernorm(e->xT, b + e->L.ln2w, b + e->L.ln2b, e->ln2T, C, eps, T, s));
+        TRY(sgpu_gemv_multi(b + e->L.fcw, e->ln2T, b + e->L.fcb, e->fcT, C, FC, T, s));
+        TRY(sgpu_gelu(e->fcT, e->fcT, T * FC, s));
+        TRY(sgpu_gemv_multi(b + e->L.projw, e->fcT, b + e->L.projb, e->yT, FC, C, T, s));
+        TRY(sgpu_add2(e->xT, e->yT, e->xT, T * C, s));
+    }
+#undef TRY
+    return logits_out(e, e->xT + (size_t)(T - 1) * C, logits_host);
+}

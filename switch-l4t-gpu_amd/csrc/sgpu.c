@@ -46,6 +46,7 @@ enum {
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI,
     K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
     K_EMBED_H,
+    K_LAYERNORM, K_GELU, K_ADD_BIAS, K_G2_SCORES, K_G2_SOFTMAX, K_G2_MIX,
     NKERN
 };
 static const struct {
@@ -60,6 +61,8 @@ static const struct {
     {MOD_QWEN, "attn_scores_gqa"}, {MOD_QWEN, "attn_softmax"}, {MOD_QWEN, "attn_mix_gqa"},
     {MOD_QWEN, "add2"},
     {MOD_TUNED, "sgpu_embed_h"},
+    {MOD_GPT2, "layernorm"}, {MOD_GPT2, "gelu"}, {MOD_GPT2, "add_bias"}, {MOD_GPT2, "attn_scores"},
+    {MOD_GPT2, "attn_softmax"}, {MOD_GPT2, "attn_mix"},
 };
 
 /* Tuned GEMV table: team sizes x segments-per-lane instantiated in sgpu_tuned.hip. */
@@ -542,6 +545,78 @@ int sgpu_add2(const float *a, const float *bb, float *out, int n, void *stream) 
     unsigned g[3] = {(unsigned)elem_grid(n), 1, 1}, b[3] = {256, 1, 1};
     void *args[] = {(void *)&a, (void *)&bb, (void *)&out, &n};
     return launch(d->fn[K_ADD2], g, b, stream, args);
+}
+
+/* ---- GPT-2 support kernels (fixed 12 x 64 head layout) ---- */
+int sgpu_layernorm(const float *x, const float *w, const float *bb, float *y, int n, float eps, int rows,
+                   void *stream) {
+    if (n < 0 || rows < 0) return SGPU_ERR_INVALID_ARG;
+    if (n == 0 || rows == 0) return SGPU_OK;
+    if (!x || !w || !bb || !y || rows > 0x7fffffff / 1) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)rows, 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&x, (void *)&w, (void *)&bb, (void *)&y, &n, &eps};
+    return launch(d->fn[K_LAYERNORM], g, b, stream, args);
+}
+
+int sgpu_gelu(const float *x, float *y, int n, void *stream) {
+    if (n < 0) return SGPU_ERR_INVALID_ARG;
+    if (n == 0) return SGPU_OK;
+    if (!x || !y) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(n), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&x, (void *)&y, &n};
+    return launch(d->fn[K_GELU], g, b, stream, args);
+}
+
+int sgpu_add_bias(float *y, const float *bias, int n, void *stream) {
+    if (n < 0) return SGPU_ERR_INVALID_ARG;
+    if (n == 0) return SGPU_OK;
+    if (!y || !bias) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(n), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&y, (void *)&bias, &n};
+    return launch(d->fn[K_ADD_BIAS], g, b, stream, args);
+}
+
+int sgpu_gpt2_attn_scores(const float *q, const float *kcache, float *scores, int T, float scale, void *stream) {
+    if (T < 0) return SGPU_ERR_INVALID_ARG;
+    if (T == 0) return SGPU_OK;
+    if (!q || !kcache || !scores || T > 0x7fffffff / 12) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(T * 12), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&q, (void *)&kcache, (void *)&scores, &T, &scale};
+    return launch(d->fn[K_G2_SCORES], g, b, stream, args);
+}
+
+int sgpu_gpt2_attn_softmax(const float *scores, float *probs, int T, void *stream) {
+    if (T < 0) return SGPU_ERR_INVALID_ARG;
+    if (T == 0) return SGPU_OK;
+    if (!scores || !probs) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {3, 1, 1}, b[3] = {256, 1, 1};     /* 12 waves: one per head */
+    void *args[] = {(void *)&scores, (void *)&probs, &T};
+    return launch(d->fn[K_G2_SOFTMAX], g, b, stream, args);
+}
+
+int sgpu_gpt2_attn_mix(const float *probs, const float *vcache, float *out, int T, void *stream) {
+    if (T < 0 || !probs || !vcache || !out) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {3, 1, 1}, b[3] = {256, 1, 1};     /* 768 outputs */
+    void *args[] = {(void *)&probs, (void *)&vcache, (void *)&out, &T};
+    return launch(d->fn[K_G2_MIX], g, b, stream, args);
 }
 
 /* ---- seeded generators ---- */

@@ -42,6 +42,11 @@ class QwenCfg(ct.Structure):
                 ("HD", ct.c_int), ("FC", ct.c_int), ("CTX", ct.c_int), ("eps", ct.c_float), ("theta", ct.c_float)]
 
 
+class Gpt2Cfg(ct.Structure):
+    _fields_ = [("V", ct.c_int), ("C", ct.c_int), ("NL", ct.c_int), ("NH", ct.c_int), ("HD", ct.c_int),
+                ("FC", ct.c_int), ("CTX", ct.c_int), ("eps", ct.c_float)]
+
+
 _P, _I, _F, _S = ct.c_void_p, ct.c_int, ct.c_float, ct.c_size_t
 _SIGS = {
     "sgpu_error_string": (ct.c_char_p, [_I]),
@@ -81,6 +86,19 @@ _SIGS = {
     "sgpu_attn_softmax": (_I, [_P, _P, _I, _I, _P]),
     "sgpu_attn_mix_gqa": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_add2": (_I, [_P, _P, _P, _I, _P]),
+    "sgpu_layernorm": (_I, [_P, _P, _P, _P, _I, _F, _I, _P]),
+    "sgpu_gelu": (_I, [_P, _P, _I, _P]),
+    "sgpu_add_bias": (_I, [_P, _P, _I, _P]),
+    "sgpu_gpt2_attn_scores": (_I, [_P, _P, _P, _I, _F, _P]),
+    "sgpu_gpt2_attn_softmax": (_I, [_P, _P, _I, _P]),
+    "sgpu_gpt2_attn_mix": (_I, [_P, _P, _P, _I, _P]),
+    "sgpu_gpt2_default_cfg": (None, [ct.POINTER(Gpt2Cfg)]),
+    "sgpu_gpt2_file_floats": (_S, [ct.POINTER(Gpt2Cfg)]),
+    "sgpu_gpt2_fill_random": (_I, [_P, ct.POINTER(Gpt2Cfg), ct.c_uint64, _F]),
+    "sgpu_gpt2_create": (_I, [ct.POINTER(_P), ct.POINTER(Gpt2Cfg), _P]),
+    "sgpu_gpt2_destroy": (None, [_P]),
+    "sgpu_gpt2_forward": (_I, [_P, _I, _I, _I, _P, _I]),
+    "sgpu_gpt2_prefill": (_I, [_P, _P, _I, _P]),
     "sgpu_qwen_default_cfg": (None, [ct.POINTER(QwenCfg)]),
     "sgpu_qwen_file_bytes": (_S, [ct.POINTER(QwenCfg)]),
     "sgpu_qwen_fill_random": (_I, [_P, ct.POINTER(QwenCfg), ct.c_uint64, _F]),
@@ -295,6 +313,55 @@ class QwenEngine:
     def close(self):
         if self.h:
             lib().sgpu_qwen_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def gpt2_cfg(**kw) -> Gpt2Cfg:
+    c = Gpt2Cfg()
+    lib().sgpu_gpt2_default_cfg(ct.byref(c))
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def gpt2_random_weights(cfg: Gpt2Cfg, seed: int, amp: float = 0.03) -> np.ndarray:
+    n = lib().sgpu_gpt2_file_floats(ct.byref(cfg))
+    if n == 0:
+        raise SgpuError(SGPU_ERR_INVALID_ARG, "sgpu_gpt2_file_floats")
+    w = np.empty(n, np.float32)
+    call("sgpu_gpt2_fill_random", w.ctypes.data, ct.byref(cfg), seed, amp)
+    return w
+
+
+class Gpt2Engine:
+    """sgpu_gpt2_* engine: fp32 weights resident on the device."""
+
+    def __init__(self, cfg: Gpt2Cfg, weights: np.ndarray):
+        self.cfg = cfg
+        h = ct.c_void_p()
+        call("sgpu_gpt2_create", ct.byref(h), ct.byref(cfg), np.ascontiguousarray(weights, np.float32).ctypes.data)
+        self.h = h.value
+        self.logits = np.empty(cfg.V, np.float32)
+
+    def forward(self, token: int, pos: int, want_logits: bool = True, fused: bool = False):
+        call("sgpu_gpt2_forward", self.h, token, pos, int(want_logits),
+             self.logits.ctypes.data if want_logits else None, int(fused))
+        return self.logits if want_logits else None
+
+    def prefill(self, ids):
+        a = np.ascontiguousarray(ids, np.int32)
+        call("sgpu_gpt2_prefill", self.h, a.ctypes.data, a.size, self.logits.ctypes.data)
+        return self.logits
+
+    def close(self):
+        if self.h:
+            lib().sgpu_gpt2_destroy(self.h)
             self.h = None
 
     def __del__(self):
