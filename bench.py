@@ -90,30 +90,49 @@ def bench_gemv_lm_head(reps=20, copies=4):
     return dict(us=us, bytes=algo_bytes, gbps=algo_bytes / (us * 1e-6) / 1e9, err=err, copies=copies)
 
 
-def bench_decode(prompt_len=32, gen=128):
+def host_loop_tok_s(eng, ids, gen):
+    """The reference's generation loop shape: logits to the host and argmax there per token."""
+    for p, tok in enumerate(ids):
+        logits = eng.forward(tok, p, p == len(ids) - 1)
+    nxt = int(np.argmax(logits))
+    t0 = time.perf_counter()
+    for g in range(gen):
+        logits = eng.forward(nxt, len(ids) + g, True)
+        nxt = int(np.argmax(logits))
+    return gen / (time.perf_counter() - t0)
+
+
+def bench_decode(prompt_len=32, gen=128, path=sgpu.QWEN_PATH_GRAPH, compare=True):
     cfg = sgpu.qwen_default_cfg()
     t = time.perf_counter()
     blob = sgpu.qwen_random_blob(cfg, seed=2024, std=0.02)
-    eng = sgpu.QwenEngine(cfg, blob)
+    eng = sgpu.QwenEngine(cfg, blob, path)
     del blob
     log(f"decode: weights built and uploaded in {time.perf_counter() - t:.1f} s")
     ids = [int(v) for v in np.random.default_rng(32).integers(0, cfg.V, prompt_len)]
-    for p, tok in enumerate(ids):
-        logits = eng.forward(tok, p, p == prompt_len - 1)
-    nxt = int(np.argmax(logits))
+    eng.generate(ids, 4)                      # captures the graphs
     sgpu.synchronize()
+    # greedy decode timed as (prompt + gen positions) minus (prompt only): prefill excluded
     t0 = time.perf_counter()
-    for g in range(gen):
-        logits = eng.forward(nxt, prompt_len + g, True)
-        nxt = int(np.argmax(logits))
-    dt = time.perf_counter() - t0
+    toks = eng.generate(ids, gen)
+    t_full = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    eng.generate(ids, 0)
+    t_prefill = time.perf_counter() - t0
+    dt = t_full - t_prefill
+    host_graph = host_loop_tok_s(eng, ids, gen) if compare else 0.0
+    eng.set_path(sgpu.QWEN_PATH_REFERENCE)
+    host_ref = host_loop_tok_s(eng, ids, 32) if compare else 0.0
     eng.close()
+    log(f"decode: first ids {toks[:8].tolist()}; host-loop tok/s graph {host_graph:.1f}, "
+        f"reference launch sequence {host_ref:.1f}")
     per_layer = (cfg.C + (cfg.C + 2 * cfg.NKV * cfg.HD) * cfg.C + cfg.C * cfg.C + cfg.C
                  + 2 * cfg.FC * cfg.C + cfg.C * cfg.FC) * 2 + (cfg.C + 2 * cfg.NKV * cfg.HD) * 4
     bytes_tok = per_layer * cfg.NL + 2 * cfg.V * cfg.C + 2 * cfg.C
     tps = gen / dt
     return dict(tok_s=tps, ms_per_tok=dt / gen * 1e3, bytes_per_token=bytes_tok,
-                hbm_floor_frac=bytes_tok * tps / (PEAK_HBM_GBPS * 1e9), prompt=prompt_len, generated=gen)
+                hbm_floor_frac=bytes_tok * tps / (PEAK_HBM_GBPS * 1e9), prompt=prompt_len, generated=gen,
+                prefill_ms=t_prefill * 1e3, host_loop_graph=host_graph, host_loop_reference=host_ref)
 
 
 def cpu_baseline(n, target_s=1.5):
@@ -180,7 +199,15 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-probe", action="store_true", help="one launch per measured kernel, for rocprofv3 --pmc")
+    ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (for profiling it)")
+    ap.add_argument("--decode-path", choices=["reference", "fused", "graph"], default="graph")
     args = ap.parse_args()
+    if args.decode_only:
+        sgpu.init(0)
+        path = {"reference": 0, "fused": 1, "graph": 2}[args.decode_path]
+        dec = bench_decode(path=path, compare=False)
+        print(json.dumps({"decode_tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4)}))
+        return
     if args.pmc_probe:
         sgpu.init(0)
         pmc_probe()
@@ -244,7 +271,11 @@ def main():
             "model": "Qwen2.5-0.5B architecture, random-init N(0,0.02) fp16 weights",
             "tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4),
             "prompt": dec["prompt"], "generated": dec["generated"],
-            "bytes_per_token": dec["bytes_per_token"], "hbm_floor_frac": round(dec["hbm_floor_frac"], 4)},
+            "bytes_per_token": dec["bytes_per_token"], "hbm_floor_frac": round(dec["hbm_floor_frac"], 4),
+            "path": "fused kernels (5 per layer) replayed as a HIP graph, greedy argmax on the device",
+            "prefill_ms": round(dec["prefill_ms"], 3),
+            "tok_s_host_argmax_loop": round(dec["host_loop_graph"], 2),
+            "tok_s_reference_launch_sequence": round(dec["host_loop_reference"], 2)},
         "sgemm_normwise_err": sg["err"],
         "device": props.name.decode(),
     }

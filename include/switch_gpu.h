@@ -222,6 +222,23 @@ void sgpu_qwen_destroy(sgpu_qwen *engine);
  * If want_logits, the V logits are copied to host `logits_host` (may be NULL to leave them on
  * the device).  Synchronous when logits are requested, asynchronous otherwise. */
 int sgpu_qwen_forward(sgpu_qwen *engine, int token, int pos, int want_logits, float *logits_host);
+/* Execution paths of sgpu_qwen_forward / sgpu_qwen_generate.  All compute the same
+ * function (checked against the CPU golden); they differ in launch structure:
+ *  REFERENCE -- the reference's per-layer sequence above, 14 launches + 2 copies per layer
+ *  FUSED     -- five fused kernels per layer: RMSNorm+qkv+bias+RoPE+KV write, attention,
+ *               o_proj+residual, RMSNorm+gate|up+SwiGLU, down+residual
+ *  GRAPH     -- FUSED with the layer stack captured once as a HIP graph and replayed
+ * FUSED and GRAPH need CTX <= 8192, HD in {32, 64, 128}, C and FC multiples of 8. */
+#define SGPU_QWEN_PATH_REFERENCE 0
+#define SGPU_QWEN_PATH_FUSED 1
+#define SGPU_QWEN_PATH_GRAPH 2
+int sgpu_qwen_set_path(sgpu_qwen *engine, int path);
+/* Greedy decode (the reference generation loop, qwen_engine.c:534-548, without its EOT
+ * stop): prime with prompt[0..T-1], then n_gen more positions.  out_tokens receives n_gen + 1
+ * ids -- the argmax after the prompt and after each generated position, first max winning.
+ * On the FUSED/GRAPH paths the argmax runs on the device and the loop never waits for the
+ * host; on the REFERENCE path it is the host loop over sgpu_qwen_forward. */
+int sgpu_qwen_generate(sgpu_qwen *engine, const int *prompt, int T, int n_gen, int *out_tokens);
 /* Device pointer to the last logits (V floats). */
 const float *sgpu_qwen_device_logits(const sgpu_qwen *engine);
 

@@ -141,19 +141,119 @@ __device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict
 }
 
 // ---------------------------------------------------------------------------------------
-// Tuned: team of LPR lanes per row, x slice in VGPRs, persistent over rows.
-// Preconditions (checked by the launcher): blockDim == 256, K % VEC == 0, W and x 16-byte
-// aligned, K/VEC <= S*LPR.
-template <class WT, int LPR, int S>
-__device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ W,
-                                          const float* __restrict__ x,
-                                          const float* __restrict__ bias,
-                                          float* __restrict__ y, int K, int N) {
+// Tuned: a team of LPR lanes per row (or per NR rows), the lane's x slice in VGPRs,
+// persistent over rows.  Three hooks make the same loop serve the plain GEMV and the fused
+// decode kernels:
+//   Pro  -- how x is obtained: XPlain (x as given) or XRms (RMSNorm applied on the fly; the
+//           block computes mean(x^2) once, every lane scales its own slice)
+//   Map  -- which weight rows team t reduces: MapRows (row t), MapPair (t and t + off),
+//           MapHalfPairs (rows i and i + H/2 of each H-row block, the RoPE pairs)
+//   Epi  -- what the reducing lane does with the NR sums of team t
+// Preconditions (checked by the launchers): blockDim == 256, K % VEC == 0, W and x 16-byte
+// aligned, K/VEC <= S*LPR, NR == 1 when LPR > 64.
+
+// Sum of v over the team of LPR lanes that holds this lane (teams are aligned groups of LPR
+// consecutive threads), returned to every lane of the team.  Teams of up to one wave use DPP
+// and a cross-lane read; wider teams combine wave sums through LDS (block-wide barriers).
+template <int LPR>
+__device__ __forceinline__ float team_sum_bcast(float v, float* red) {
+    if constexpr (LPR <= 64) {
+        v = sgpu_group_sum<LPR>(v);
+        return __shfl(v, (threadIdx.x & 63) | (LPR - 1));
+    } else {
+        v = sgpu_group_sum<64>(v);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        const int first = (threadIdx.x / LPR) * (LPR / 64);
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < LPR / 64; i++) t += red[first + i];
+        __syncthreads();
+        return t;
+    }
+}
+
+struct XPlain {
+    const float* x;
+    __device__ __forceinline__ sgpu_f32x4 load4(int k) const { return *reinterpret_cast<const sgpu_f32x4*>(x + k); }
+    __device__ __forceinline__ float at(int k) const { return x[k]; }
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&)[S][VEC], const bool (&)[S], int, int, float*) {}
+};
+
+// x'[k] = x[k] * inv * h2f(w[k]), inv = 1 / sqrt(mean(x^2) + eps): cpu_rms (qwen_engine.c:285-290)
+// with the same product order.  A team's lanes together hold all K values of x, so the sum of
+// squares is a team reduction over the registers already loaded: no extra loads, and no
+// barrier for teams of up to one wave.
+struct XRms {
+    const float* x;
+    const uint16_t* w;
+    float eps;
+    float inv;
+    __device__ __forceinline__ sgpu_f32x4 load4(int k) const { return *reinterpret_cast<const sgpu_f32x4*>(x + k); }
+    __device__ __forceinline__ float at(int k) const {
+#pragma clang fp contract(off)
+        return x[k] * inv * sgpu_h2f(w[k]);
+    }
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const bool (&has)[S], int sub, int K, float* red) {
+#pragma clang fp contract(off)
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; j++)
+#pragma unroll
+            for (int e = 0; e < VEC; e++) ss += xr[j][e] * xr[j][e];   // zero where !has
+        ss = team_sum_bcast<LPR>(ss, red);
+        inv = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            if (!has[j]) continue;
+            const int k0 = (sub + LPR * j) * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; e++) xr[j][e] = xr[j][e] * inv * sgpu_h2f(w[k0 + e]);
+        }
+    }
+};
+
+struct MapRows {
+    __device__ __forceinline__ int row(int t, int) const { return t; }
+};
+struct MapPair {
+    int off;
+    __device__ __forceinline__ int row(int t, int j) const { return t + j * off; }
+};
+struct MapHalfPairs {
+    int half;   // H/2: team t covers rows (t/half)*2*half + t%half and that + half
+    __device__ __forceinline__ int row(int t, int j) const { return (t / half) * 2 * half + t % half + j * half; }
+};
+
+// y[row] = acc + bias?[row]
+struct EpiStore {
+    const float* bias;
+    float* y;
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
+        y[rows[0]] = acc[0] + (bias ? bias[rows[0]] : 0.0f);
+    }
+};
+
+// Serial k-ascending re-evaluation of one row with the exact reference decode and the same x.
+template <class WT, class Pro>
+__device__ __noinline__ float recompute_row_x(const typename WT::elem* __restrict__ row, Pro pro, int K) {
+    float acc = 0.0f;
+    for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), pro.at(k), acc);
+    return acc;
+}
+
+template <class WT, int LPR, int S, int NR, class Pro, class Map, class Epi>
+__device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ W, int K, int nteams, Pro pro,
+                                          Map map, Epi epi) {
     static_assert(LPR == 16 || LPR == 32 || LPR == 64 || LPR == 128 || LPR == 256, "team size");
+    static_assert(NR == 1 || LPR <= 64, "multi-row teams must fit in one wave");
     typedef typename WT::vec vec;
     constexpr int VEC = WT::VEC;
     constexpr int NT = 256;
-    constexpr int TEAMS = NT / LPR;                   // rows per block iteration
+    constexpr int TEAMS = NT / LPR;                   // teams per block iteration
     constexpr int WAVES_PER_TEAM = LPR > 64 ? LPR / 64 : 1;
     __shared__ float red[NT / 64];
 
@@ -161,56 +261,97 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
     const int lane = tid & 63, wave = tid >> 6;
     const int team = tid / LPR, sub = tid % LPR;
     const int nseg = K / VEC;
+    bool has[S];
+#pragma unroll
+    for (int j = 0; j < S; j++) has[j] = sub + LPR * j < nseg;
+
+    // Weight loads of a row block; issued one block ahead of their use, so the first block's
+    // fetch overlaps the x prologue and each later fetch overlaps the previous reduction.
+    vec w[NR][S];
+    int rows[NR];
+    bool valid = false;
+    auto fetch = [&](int rb) {
+        const int t = rb * TEAMS + team;
+        valid = t < nteams;
+#pragma unroll
+        for (int r = 0; r < NR; r++) rows[r] = valid ? map.row(t, r) : 0;
+        if (valid) {
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const vec* rv = reinterpret_cast<const vec*>(W + (size_t)rows[r] * K) + sub;
+#pragma unroll
+                for (int j = 0; j < S; j++)
+                    if (has[j]) w[r][j] = sgpu_ldnt(rv + LPR * j);
+            }
+        }
+    };
+    int rb = blockIdx.x;
+    if (rb * TEAMS < nteams) fetch(rb);
 
     // This lane's x slice: segments sub, sub+LPR, ..., kept for every row.
     float xr[S][VEC];
-    bool has[S];
 #pragma unroll
     for (int j = 0; j < S; j++) {
         const int seg = sub + LPR * j;
-        has[j] = seg < nseg;
-        const sgpu_f32x4* xv4 = reinterpret_cast<const sgpu_f32x4*>(x) + (size_t)seg * (VEC / 4);
 #pragma unroll
         for (int q = 0; q < VEC / 4; q++) {
-            const sgpu_f32x4 a = has[j] ? xv4[q] : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const sgpu_f32x4 a = has[j] ? pro.load4(seg * VEC + 4 * q) : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int e = 0; e < 4; e++) xr[j][4 * q + e] = a[e];
         }
     }
+    pro.template prepare<LPR, S, VEC>(xr, has, sub, K, red);
 
-    for (int rb = blockIdx.x; rb * TEAMS < N; rb += gridDim.x) {   // block-uniform loop
-        const int n = rb * TEAMS + team;
-        float acc = 0.0f;
-        if (n < N) {
-            const vec* rv = reinterpret_cast<const vec*>(W + (size_t)n * K) + sub;
-            vec w[S];
+    for (; rb * TEAMS < nteams; rb += gridDim.x) {    // block-uniform loop
+        const int t = rb * TEAMS + team;
+        const bool cur_valid = valid;
+        int cur_rows[NR];
+        float acc[NR];
 #pragma unroll
-            for (int j = 0; j < S; j++)
-                if (has[j]) w[j] = sgpu_ldnt(rv + LPR * j);
-#pragma unroll
-            for (int j = 0; j < S; j++)
-                if (has[j]) acc = WT::dot(w[j], xr[j], acc);
+        for (int r = 0; r < NR; r++) {
+            cur_rows[r] = rows[r];
+            acc[r] = 0.0f;
         }
+        if (cur_valid) {
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int j = 0; j < S; j++)
+                    if (has[j]) acc[r] = WT::dot(w[r][j], xr[j], acc[r]);
+        }
+        if ((rb + (int)gridDim.x) * TEAMS < nteams) fetch(rb + gridDim.x);
         if constexpr (LPR <= 64) {
-            acc = sgpu_group_sum<LPR>(acc);
-            if (sub == LPR - 1 && n < N) {
-                if (WT::NEEDS_RECHECK && !__builtin_isfinite(acc)) acc = recompute_row<WT>(W + (size_t)n * K, x, K);
-                y[n] = acc + (bias ? bias[n] : 0.0f);
+#pragma unroll
+            for (int r = 0; r < NR; r++) acc[r] = sgpu_group_sum<LPR>(acc[r]);
+            if (sub == LPR - 1 && cur_valid) {
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    if (WT::NEEDS_RECHECK && !__builtin_isfinite(acc[r]))
+                        acc[r] = recompute_row_x<WT>(W + (size_t)cur_rows[r] * K, pro, K);
+                epi(t, cur_rows, acc);
             }
         } else {
-            acc = sgpu_group_sum<64>(acc);
-            if (lane == 63) red[wave] = acc;
+            acc[0] = sgpu_group_sum<64>(acc[0]);
+            if (lane == 63) red[wave] = acc[0];
             __syncthreads();
-            if (sub == 0 && n < N) {
+            if (sub == 0 && cur_valid) {
                 float s = 0.0f;
 #pragma unroll
                 for (int i = 0; i < WAVES_PER_TEAM; i++) s += red[team * WAVES_PER_TEAM + i];
-                if (WT::NEEDS_RECHECK && !__builtin_isfinite(s)) s = recompute_row<WT>(W + (size_t)n * K, x, K);
-                y[n] = s + (bias ? bias[n] : 0.0f);
+                if (WT::NEEDS_RECHECK && !__builtin_isfinite(s)) s = recompute_row_x<WT>(W + (size_t)cur_rows[0] * K, pro, K);
+                acc[0] = s;
+                epi(t, cur_rows, acc);
             }
             __syncthreads();
         }
     }
+}
+
+// The plain tuned GEMV: y[n] = W[n,:].x + bias?[n].
+template <class WT, int LPR, int S>
+__device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ W, const float* __restrict__ x,
+                                          const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
+    gemv_team<WT, LPR, S, 1>(W, K, N, XPlain{x}, MapRows{}, EpiStore{bias, y});
 }
 
 // ---------------------------------------------------------------------------------------

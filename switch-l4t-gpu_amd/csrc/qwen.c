@@ -102,7 +102,15 @@ int sgpu_qwen_fill_random(void *blob, const sgpu_qwen_cfg *c, uint64_t seed, flo
 struct sgpu_qwen {
     sgpu_qwen_cfg cfg;
     qlayout L;
+    int path;                                  /* SGPU_QWEN_PATH_* */
     hipStream_t stream;
+    int *d_step;                               /* {token, pos} read by the fused kernels */
+    int *d_tokens;                             /* CTX + 1 greedy ids, indexed by position */
+    float *d_q;                                /* rotated q of the fused path */
+    float *d_amax_v;                           /* argmax partials */
+    int *d_amax_i;
+    hipGraph_t g_layers, g_step;
+    hipGraphExec_t ge_layers, ge_step;
     uint16_t *d_emb, *d_lnfw;
     float *d_cos, *d_sin;
     uint16_t **d_ln1w, **d_qkvw, **d_ow, **d_ln2w, **d_gateupw, **d_downw;
@@ -134,6 +142,15 @@ void sgpu_qwen_destroy(sgpu_qwen *e) {
         for (int l = 0; l < NL; l++) sgpu_free(arr[l]);
         free(arr);
     }
+    sgpu_free(e->d_step);
+    sgpu_free(e->d_tokens);
+    sgpu_free(e->d_q);
+    sgpu_free(e->d_amax_v);
+    sgpu_free(e->d_amax_i);
+    if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
+    if (e->g_layers) hipGraphDestroy(e->g_layers);
+    if (e->ge_step) hipGraphExecDestroy(e->ge_step);
+    if (e->g_step) hipGraphDestroy(e->g_step);
     if (e->stream) hipStreamDestroy(e->stream);
     free(e);
 }
@@ -197,6 +214,11 @@ int sgpu_qwen_create(sgpu_qwen **out, const sgpu_qwen_cfg *c, const void *blob) 
     TRY(dalloc((void **)&e->d_probs, (size_t)c->CTX * c->NH * 4, NULL));
     TRY(dalloc((void **)&e->d_logits, (size_t)c->V * 4, NULL));
     TRY(dalloc((void **)&e->d_x2, (size_t)C * 4, NULL));
+    TRY(dalloc((void **)&e->d_step, 4 * sizeof(int), NULL));
+    TRY(dalloc((void **)&e->d_tokens, ((size_t)c->CTX + 1) * sizeof(int), NULL));
+    TRY(dalloc((void **)&e->d_q, (size_t)c->NH * c->HD * 4, NULL));
+    TRY(dalloc((void **)&e->d_amax_v, SGPU_ARGMAX_PARTS * sizeof(float), NULL));
+    TRY(dalloc((void **)&e->d_amax_i, SGPU_ARGMAX_PARTS * sizeof(int), NULL));
 #undef TRY
     *out = e;
     return SGPU_OK;
@@ -207,10 +229,9 @@ fail:
 
 const float *sgpu_qwen_device_logits(const sgpu_qwen *e) { return e ? e->d_logits : NULL; }
 
-int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host) {
-    if (!e) return SGPU_ERR_INVALID_ARG;
+/* The reference per-layer launch sequence (gpu_forward, qwen_engine.c:205-269). */
+static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host) {
     const sgpu_qwen_cfg *c = &e->cfg;
-    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
     const int C = c->C, NH = c->NH, NKV = c->NKV, HD = c->HD, FC = c->FC;
     const int KVD = e->L.kvd, QKVD = e->L.qkvd, Tp = pos + 1;
     const float eps = c->eps, scale = (float)(1.0 / sqrt((double)HD));
@@ -247,4 +268,142 @@ int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *
     }
 #undef TRY
     return SGPU_OK;
+}
+
+/* ---- fused path: five kernels per layer (sgpu_decode.hip) ---- */
+static int fused_ok(const sgpu_qwen_cfg *c) {
+    return c->CTX <= 8192 && (c->HD == 32 || c->HD == 64 || c->HD == 128) && c->C % 8 == 0 && c->FC % 8 == 0;
+}
+
+static int fused_layers(sgpu_qwen *e) {
+    const sgpu_qwen_cfg *c = &e->cfg;
+    const int C = c->C, NH = c->NH, NKV = c->NKV, HD = c->HD, FC = c->FC, QKVD = e->L.qkvd;
+    const float eps = c->eps, scale = (float)(1.0 / sqrt((double)HD));
+    void *s = (void *)e->stream;
+    int rc;
+#define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+    for (int l = 0; l < c->NL; l++) {
+        TRY(sgpu_internal_dec_qkv(e->d_qkvw[l], C, QKVD, e->d_x, e->d_ln1w[l], eps, e->d_qkvb[l], e->d_q, e->d_kc[l],
+                                  e->d_vc[l], e->d_cos, e->d_sin, e->d_step, NH, NKV, HD, s));
+        TRY(sgpu_internal_dec_attn(e->d_q, e->d_kc[l], e->d_vc[l], e->d_att, e->d_step, NH, NKV, HD, scale, s));
+        TRY(sgpu_internal_dec_res(e->d_ow[l], C, C, e->d_att, NULL, e->d_x, s));
+        TRY(sgpu_internal_dec_gateup(e->d_gateupw[l], C, FC, e->d_x, e->d_ln2w[l], eps, e->d_down, s));
+        TRY(sgpu_internal_dec_res(e->d_downw[l], FC, C, e->d_down, NULL, e->d_x, s));
+    }
+#undef TRY
+    return SGPU_OK;
+}
+
+static int lm_head(sgpu_qwen *e) {
+    return sgpu_internal_dec_lmhead(e->d_emb, e->cfg.C, e->cfg.V, e->d_x, e->d_lnfw, e->cfg.eps, e->d_logits,
+                                    (void *)e->stream);
+}
+
+/* One greedy step entirely on the device: next token from step[0], pos = step[1] + 1. */
+static int device_step(sgpu_qwen *e) {
+    int rc = sgpu_internal_dec_embed_next(e->d_emb, e->d_x, e->cfg.C, e->d_step, (void *)e->stream);
+    if (!rc) rc = fused_layers(e);
+    if (!rc) rc = lm_head(e);
+    if (!rc)
+        rc = sgpu_internal_dec_argmax(e->d_logits, e->cfg.V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
+                                      (void *)e->stream);
+    return rc;
+}
+
+/* Capture fn(e) on the engine stream into a graph and instantiate it. */
+static int capture(sgpu_qwen *e, int (*fn)(sgpu_qwen *), hipGraph_t *g, hipGraphExec_t *ge) {
+    hipError_t he = hipStreamBeginCapture(e->stream, hipStreamCaptureModeRelaxed);
+    if (he != hipSuccess) return (int)he;
+    int rc = fn(e);
+    hipGraph_t graph = NULL;
+    he = hipStreamEndCapture(e->stream, &graph);
+    if (rc || he != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return rc ? rc : (int)he;
+    }
+    he = hipGraphInstantiate(ge, graph, NULL, NULL, 0);
+    if (he != hipSuccess) {
+        hipGraphDestroy(graph);
+        return (int)he;
+    }
+    *g = graph;
+    return SGPU_OK;
+}
+
+static int run_layers(sgpu_qwen *e) {
+    if (e->path != SGPU_QWEN_PATH_GRAPH) return fused_layers(e);
+    if (!e->ge_layers) {
+        int rc = capture(e, fused_layers, &e->g_layers, &e->ge_layers);
+        if (rc) return rc;
+    }
+    hipError_t he = hipGraphLaunch(e->ge_layers, e->stream);
+    return he == hipSuccess ? SGPU_OK : (int)he;
+}
+
+static int logits_to_host(sgpu_qwen *e, float *logits_host) {
+    if (!logits_host) return SGPU_OK;
+    hipError_t he = hipMemcpyAsync(logits_host, e->d_logits, (size_t)e->cfg.V * 4, hipMemcpyDeviceToHost, e->stream);
+    if (he != hipSuccess) return (int)he;
+    return sgpu_stream_synchronize((void *)e->stream);
+}
+
+int sgpu_qwen_set_path(sgpu_qwen *e, int path) {
+    if (!e || path < SGPU_QWEN_PATH_REFERENCE || path > SGPU_QWEN_PATH_GRAPH) return SGPU_ERR_INVALID_ARG;
+    if (path != SGPU_QWEN_PATH_REFERENCE && !fused_ok(&e->cfg)) return SGPU_ERR_INVALID_ARG;
+    e->path = path;
+    return SGPU_OK;
+}
+
+int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host) {
+    if (!e) return SGPU_ERR_INVALID_ARG;
+    const sgpu_qwen_cfg *c = &e->cfg;
+    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
+    if (e->path == SGPU_QWEN_PATH_REFERENCE) return forward_reference(e, token, pos, want_logits, logits_host);
+    int rc = sgpu_internal_dec_embed(e->d_emb, token, pos, e->d_x, c->C, e->d_step, (void *)e->stream);
+    if (!rc) rc = run_layers(e);
+    if (rc || !want_logits) return rc;
+    if ((rc = lm_head(e))) return rc;
+    return logits_to_host(e, logits_host);
+}
+
+int sgpu_qwen_generate(sgpu_qwen *e, const int *prompt, int T, int n_gen, int *out_tokens) {
+    if (!e || !prompt || !out_tokens || T <= 0 || n_gen < 0) return SGPU_ERR_INVALID_ARG;
+    const sgpu_qwen_cfg *c = &e->cfg;
+    if ((long long)T + n_gen > c->CTX) return SGPU_ERR_INVALID_ARG;
+    for (int p = 0; p < T; p++)
+        if (prompt[p] < 0 || prompt[p] >= c->V) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    if (e->path == SGPU_QWEN_PATH_REFERENCE) {       /* host-driven loop, the reference's own */
+        float *logits = malloc(sizeof(float) * (size_t)c->V);
+        if (!logits) return SGPU_ERR_HOST_ALLOC;
+        for (int p = 0; p < T && !(rc = forward_reference(e, prompt[p], p, p == T - 1, logits)); p++) {
+        }
+        for (int g = 0; !rc && g <= n_gen; g++) {
+            int b = 0;
+            for (int i = 1; i < c->V; i++)
+                if (logits[i] > logits[b]) b = i;
+            out_tokens[g] = b;
+            if (g < n_gen) rc = forward_reference(e, b, T + g, 1, logits);
+        }
+        free(logits);
+        return rc;
+    }
+    for (int p = 0; p < T; p++)
+        if ((rc = sgpu_qwen_forward(e, prompt[p], p, p == T - 1, NULL))) return rc;
+    if ((rc = sgpu_internal_dec_argmax(e->d_logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
+                                       (void *)e->stream)))
+        return rc;
+    for (int g = 0; g < n_gen; g++) {
+        if (e->path == SGPU_QWEN_PATH_GRAPH) {
+            if (!e->ge_step && (rc = capture(e, device_step, &e->g_step, &e->ge_step))) return rc;
+            hipError_t he = hipGraphLaunch(e->ge_step, e->stream);
+            if (he != hipSuccess) return (int)he;
+        } else if ((rc = device_step(e))) {
+            return rc;
+        }
+    }
+    hipError_t he = hipMemcpyAsync(out_tokens, e->d_tokens + T, ((size_t)n_gen + 1) * sizeof(int),
+                                   hipMemcpyDeviceToHost, e->stream);
+    if (he != hipSuccess) return (int)he;
+    return sgpu_stream_synchronize((void *)e->stream);
 }

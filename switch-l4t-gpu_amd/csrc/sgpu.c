@@ -27,8 +27,9 @@ extern const unsigned char sgpu_co_gemv[], sgpu_co_gemv_end[];
 extern const unsigned char sgpu_co_gpt2_kernels[], sgpu_co_gpt2_kernels_end[];
 extern const unsigned char sgpu_co_qwen_kernels[], sgpu_co_qwen_kernels_end[];
 extern const unsigned char sgpu_co_sgpu_tuned[], sgpu_co_sgpu_tuned_end[];
+extern const unsigned char sgpu_co_sgpu_decode[], sgpu_co_sgpu_decode_end[];
 
-enum { MOD_SWITCH, MOD_GEMV, MOD_GPT2, MOD_QWEN, MOD_TUNED, NMOD };
+enum { MOD_SWITCH, MOD_GEMV, MOD_GPT2, MOD_QWEN, MOD_TUNED, MOD_DECODE, NMOD };
 static const struct {
     const char *name;
     const unsigned char *start, *end;
@@ -38,6 +39,7 @@ static const struct {
     {"gpt2_kernels", sgpu_co_gpt2_kernels, sgpu_co_gpt2_kernels_end},
     {"qwen_kernels", sgpu_co_qwen_kernels, sgpu_co_qwen_kernels_end},
     {"sgpu_tuned", sgpu_co_sgpu_tuned, sgpu_co_sgpu_tuned_end},
+    {"sgpu_decode", sgpu_co_sgpu_decode, sgpu_co_sgpu_decode_end},
 };
 
 /* Every kernel the launchers use: (module, symbol). */
@@ -71,12 +73,22 @@ static const int g_segs[10] = {1, 2, 3, 4, 6, 7, 8, 10, 12, 16};
 #define NLPR 3
 #define NSEG 10
 
+/* Fused decode GEMV families (sgpu_decode.hip): (lanes per team, segments per lane). */
+static const int g_dec_cfg[][2] = {{16, 1}, {16, 2}, {16, 4}, {16, 7}, {16, 8}, {64, 1}, {64, 2}, {64, 4},
+                                   {64, 8}, {256, 1}, {256, 2}, {256, 3}, {256, 4}, {256, 8}};
+#define NDEC_PAIR 9      /* the first 9 entries: teams of up to one wave (two-row families) */
+#define NDEC_ALL 14
+enum { DEC_QKV, DEC_GATEUP, DEC_RES, DEC_LMHEAD, NDECFAM };
+static const char *g_dec_fam[NDECFAM] = {"qkv", "gateup", "res", "lmhead"};
+
 typedef struct {
     int ready;
     int cus;
     hipModule_t mod[NMOD];
     hipFunction_t fn[NKERN];
     hipFunction_t gemv_f32[NLPR][NSEG], gemv_h[NLPR][NSEG];
+    hipFunction_t dec[NDECFAM][NDEC_ALL];
+    hipFunction_t dec_attn[3], dec_embed, dec_embed_next, dec_argmax_part, dec_argmax_final;
 } devstate;
 
 static devstate g_dev[SGPU_MAX_DEVICES];
@@ -130,6 +142,30 @@ static int load_device(int dev) {
             e = hipModuleGetFunction(&d->gemv_h[i][j], d->mod[MOD_TUNED], name);
             if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
         }
+    for (int f = 0; f < NDECFAM; f++) {
+        int n = (f == DEC_QKV || f == DEC_GATEUP) ? NDEC_PAIR : NDEC_ALL;
+        for (int j = 0; j < n; j++) {
+            char name[64];
+            snprintf(name, sizeof name, "sgpu_dec_%s_l%d_s%d", g_dec_fam[f], g_dec_cfg[j][0], g_dec_cfg[j][1]);
+            e = hipModuleGetFunction(&d->dec[f][j], d->mod[MOD_DECODE], name);
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+        }
+    }
+    {
+        const char *attn[3] = {"sgpu_dec_attn32", "sgpu_dec_attn64", "sgpu_dec_attn128"};
+        for (int j = 0; j < 3; j++)
+            if (hipModuleGetFunction(&d->dec_attn[j], d->mod[MOD_DECODE], attn[j]) != hipSuccess) {
+                rc = SGPU_ERR_NO_KERNEL;
+                goto out;
+            }
+        if (hipModuleGetFunction(&d->dec_embed, d->mod[MOD_DECODE], "sgpu_dec_embed") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_embed_next, d->mod[MOD_DECODE], "sgpu_dec_embed_next") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_argmax_part, d->mod[MOD_DECODE], "sgpu_dec_argmax_part") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_argmax_final, d->mod[MOD_DECODE], "sgpu_dec_argmax_final") != hipSuccess) {
+            rc = SGPU_ERR_NO_KERNEL;
+            goto out;
+        }
+    }
     d->ready = 1;
 out:
     pthread_mutex_unlock(&g_lock);
@@ -263,6 +299,7 @@ int sgpu_event_elapsed_ms(float *ms, void *start, void *stop) {
 }
 
 const void *sgpu_code_object(const char *name, size_t *size) {
+    if (size) *size = 0;
     if (!name) return NULL;
     for (int m = 0; m < NMOD; m++)
         if (!strcmp(name, g_cos[m].name)) {
@@ -730,4 +767,120 @@ int sgpu_internal_embed_h(const uint16_t *emb, int token, float *x, int C, void 
     unsigned g[3] = {(unsigned)elem_grid(C), 1, 1}, b[3] = {256, 1, 1};
     void *args[] = {(void *)&emb, &token, (void *)&x, &C};
     return launch(d->fn[K_EMBED_H], g, b, stream, args);
+}
+
+/* ---- fused decode kernels (sgpu_decode.hip) ---- */
+/* Pick a (team, segments) instance for K columns and nteams teams: the smallest team that
+ * still gives >= 8 waves per CU, else the largest that fits; -1 if none fits. */
+static int dec_pick(const devstate *d, int K, int nteams, int n_entries) {
+    if (K <= 0 || K % 8 || nteams <= 0) return -1;
+    const long long nseg = K / 8, want = 8LL * d->cus;
+    int best = -1, best_lpr = 0;
+    const int lprs[3] = {16, 64, 256};
+    for (int li = 0; li < 3; li++) {
+        int pick = -1;
+        for (int j = 0; j < n_entries; j++)
+            if (g_dec_cfg[j][0] == lprs[li] && (long long)g_dec_cfg[j][1] * lprs[li] >= nseg &&
+                (pick < 0 || g_dec_cfg[j][1] < g_dec_cfg[pick][1]))
+                pick = j;
+        if (pick < 0) continue;
+        best = pick;
+        best_lpr = lprs[li];
+        if ((long long)nteams * best_lpr / 64 >= want) break;
+    }
+    return best;
+}
+
+static int dec_launch_team(devstate *d, int fam, int K, int nteams, void **args, void *stream) {
+    const int n_entries = (fam == DEC_QKV || fam == DEC_GATEUP) ? NDEC_PAIR : NDEC_ALL;
+    const int j = dec_pick(d, K, nteams, n_entries);
+    if (j < 0) return SGPU_ERR_INVALID_ARG;
+    const unsigned teams = 256u / (unsigned)g_dec_cfg[j][0];
+    unsigned g[3] = {umin(cdiv(nteams, teams), (unsigned)d->cus * 8u), 1, 1}, b[3] = {256, 1, 1};
+    return launch(d->dec[fam][j], g, b, stream, args);
+}
+
+int sgpu_internal_dec_qkv(const uint16_t *W, int K, int nrows, const float *x, const uint16_t *lnw, float eps,
+                          const float *bias, float *q, float *kc, float *vc, const float *cosT, const float *sinT,
+                          const int *step, int NH, int NKV, int HD, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    if (HD <= 0 || HD % 2 || nrows != (NH + 2 * NKV) * HD) return SGPU_ERR_INVALID_ARG;
+    int nteams = nrows / 2;
+    void *args[] = {(void *)&W, &K, &nteams, (void *)&x, (void *)&lnw, &eps, (void *)&bias, (void *)&q,
+                    (void *)&kc, (void *)&vc, (void *)&cosT, (void *)&sinT, (void *)&step, &NH, &NKV, &HD};
+    return dec_launch_team(d, DEC_QKV, K, nteams, args, stream);
+}
+
+int sgpu_internal_dec_gateup(const uint16_t *W, int K, int FC, const float *x, const uint16_t *lnw, float eps,
+                             float *y, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    void *args[] = {(void *)&W, &K, &FC, (void *)&x, (void *)&lnw, &eps, (void *)&y};
+    return dec_launch_team(d, DEC_GATEUP, K, FC, args, stream);
+}
+
+int sgpu_internal_dec_res(const uint16_t *W, int K, int N, const float *a, const float *bias, float *x,
+                          void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    void *args[] = {(void *)&W, &K, &N, (void *)&a, (void *)&bias, (void *)&x};
+    return dec_launch_team(d, DEC_RES, K, N, args, stream);
+}
+
+int sgpu_internal_dec_lmhead(const uint16_t *W, int K, int N, const float *x, const uint16_t *lnw, float eps,
+                             float *y, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    void *args[] = {(void *)&W, &K, &N, (void *)&x, (void *)&lnw, &eps, (void *)&y};
+    return dec_launch_team(d, DEC_LMHEAD, K, N, args, stream);
+}
+
+int sgpu_internal_dec_attn(const float *q, const float *kc, const float *vc, float *out, const int *step, int NH,
+                           int NKV, int HD, float scale, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    const int j = HD == 32 ? 0 : HD == 64 ? 1 : HD == 128 ? 2 : -1;
+    if (j < 0 || NKV <= 0 || NH % NKV) return SGPU_ERR_INVALID_ARG;
+    unsigned g[3] = {(unsigned)NH, 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&q, (void *)&kc, (void *)&vc, (void *)&out, (void *)&step, &NH, &NKV, &scale};
+    return launch(d->dec_attn[j], g, b, stream, args);
+}
+
+int sgpu_internal_dec_embed(const uint16_t *emb, int token, int pos, float *x, int C, int *step, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(C), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&emb, &token, &pos, (void *)&x, &C, (void *)&step};
+    return launch(d->dec_embed, g, b, stream, args);
+}
+
+int sgpu_internal_dec_embed_next(const uint16_t *emb, float *x, int C, int *step, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {1, 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&emb, (void *)&x, &C, (void *)&step};
+    return launch(d->dec_embed_next, g, b, stream, args);
+}
+
+int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
+                             void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    if (n <= 0) return SGPU_ERR_INVALID_ARG;
+    int np = SGPU_ARGMAX_PARTS;
+    unsigned g[3] = {(unsigned)np, 1, 1}, b[3] = {256, 1, 1};
+    void *a1[] = {(void *)&v, &n, (void *)&part_v, (void *)&part_i};
+    if ((rc = launch(d->dec_argmax_part, g, b, stream, a1))) return rc;
+    unsigned g2[3] = {1, 1, 1};
+    void *a2[] = {(void *)&part_v, (void *)&part_i, &np, (void *)&step, (void *)&out};
+    return launch(d->dec_argmax_final, g2, b, stream, a2);
 }

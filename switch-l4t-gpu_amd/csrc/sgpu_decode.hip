@@ -1,0 +1,288 @@
+// sgpu_decode.hip -- fused Qwen2.5 decode kernels for gfx950 (five launches per layer).
+//
+// The reference runs 14 launches and 2 device copies per layer (qwen_engine.c:216-259).
+// Here the same arithmetic is grouped so every kernel streams one weight matrix and keeps
+// the small steps around it in its prologue or epilogue:
+//   sgpu_dec_qkv_*    RMSNorm(x) -> qkv GEMV + bias -> RoPE on q and k -> q to its buffer,
+//                     k and v straight into the layer's KV cache at `pos`
+//   sgpu_dec_attn     GQA attention for one head per block: scores, softmax, mix
+//   sgpu_dec_res_*    GEMV + residual add in place: x[n] += W[n,:].a (o_proj, down_proj)
+//   sgpu_dec_gateup_* RMSNorm(x) -> gate and up rows of the same output -> SwiGLU
+//   sgpu_dec_lmhead_* final RMSNorm -> tied lm_head GEMV
+//   sgpu_dec_embed    token embedding (h2f) and the step record {token, pos} for the layers
+//   sgpu_dec_argmax_* first-max argmax of the logits into the step record (greedy decode)
+// The position lives in device memory (`step`), so a whole position can be captured once as
+// a HIP graph and replayed.  Weight rows are fp16 bits with the reference h2f contract (see
+// gemv_core.h); this code object is built with the fp16 denormal mode set to flush.
+#include "gemv_core.h"
+
+namespace {
+
+// ---- epilogues ----
+// y[row] = resid[row] + (acc + bias?[row]); y may alias resid (each row touched by one lane).
+struct EpiResidual {
+    const float* resid;
+    const float* bias;
+    float* y;
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
+        const int r = rows[0];
+        y[r] = resid[r] + (acc[0] + (bias ? bias[r] : 0.0f));
+    }
+};
+
+// y[t] = silu(gate) * up, gate = rows t, up = rows t + FC (qwen_engine.c:349-350 form).
+struct EpiSwiGLU {
+    float* y;
+    __device__ __forceinline__ void operator()(int t, const int*, const float* acc) const {
+#pragma clang fp contract(off)
+        const float g = acc[0];
+        y[t] = (g / (1.0f + expf(-g))) * acc[1];
+    }
+};
+
+// Team t owns rows (i, i + HD/2) of head block hb: add the q/k/v bias, rotate q and k by the
+// RoPE angle of `pos` (qwen_engine.c:303-317 arithmetic), write q to its buffer and k, v to
+// the KV cache row of `pos` (the reference's cache copies, qwen_engine.c:229-230).
+struct EpiQkvRope {
+    const float* bias;
+    float* q;
+    float* kc;
+    float* vc;
+    const float* cosT;
+    const float* sinT;
+    const int* step;
+    int NH, NKV, HD;
+    __device__ __forceinline__ void operator()(int t, const int* rows, const float* acc) const {
+#pragma clang fp contract(off)
+        const int h2 = HD / 2, hb = t / h2, i = t % h2, pos = step[1];
+        const int KVD = NKV * HD;
+        const float a = acc[0] + bias[rows[0]], b = acc[1] + bias[rows[1]];
+        if (hb < NH + NKV) {
+            const float c = cosT[(size_t)pos * h2 + i], s = sinT[(size_t)pos * h2 + i];
+            const float ra = a * c - b * s, rb = a * s + b * c;
+            float* dst = hb < NH ? q + (size_t)hb * HD : kc + (size_t)pos * KVD + (size_t)(hb - NH) * HD;
+            dst[i] = ra;
+            dst[i + h2] = rb;
+        } else {
+            float* dst = vc + (size_t)pos * KVD + (size_t)(hb - NH - NKV) * HD;
+            dst[i] = a;
+            dst[i + h2] = b;
+        }
+    }
+};
+
+constexpr int kMaxCtx = 8192;   // attention scores kept in LDS (32 KB)
+
+// Block max / sum over 256 threads (4 waves), result in every thread.
+__device__ __forceinline__ float block_max256(float v, float* red) {
+    v = sgpu_wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = sgpu_wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One block (256 threads) per query head h; T = pos + 1 cached positions.  Scores: LPT
+// lanes per position (DPL dims each), 256/LPT positions per pass; mix: 256/HD t-slices of HD
+// lanes, eight independent loads in flight per lane.
+template <int HD>
+__device__ __forceinline__ void dec_attn(const float* __restrict__ q, const float* __restrict__ kc,
+                                         const float* __restrict__ vc, float* __restrict__ out,
+                                         const int* __restrict__ step, int NH, int NKV, float scale) {
+    static_assert(HD == 32 || HD == 64 || HD == 128, "head dim");
+    constexpr int LPT = HD >= 64 ? HD / 16 : 4;   // lanes per position
+    constexpr int DPL = HD / LPT;                  // dims per lane (16 or 8)
+    constexpr int PPP = 256 / LPT;                 // positions per pass
+    constexpr int SLICES = 256 / HD;
+    __shared__ float sc[kMaxCtx];
+    __shared__ float red[4];
+    __shared__ float part[256];
+    const int tid = threadIdx.x, h = blockIdx.x, g = h / (NH / NKV);
+    const int T = step[1] + 1, KVD = NKV * HD;
+    const float* kg = kc + (size_t)g * HD;
+    const float* vg = vc + (size_t)g * HD;
+    const int d0 = (tid % LPT) * DPL;
+    float qv[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e += 4) {
+        const sgpu_f32x4 a = *reinterpret_cast<const sgpu_f32x4*>(q + (size_t)h * HD + d0 + e);
+#pragma unroll
+        for (int i = 0; i < 4; i++) qv[e + i] = a[i];
+    }
+    for (int tb = 0; tb < T; tb += PPP) {
+        const int t = tb + tid / LPT;
+        float s = 0.0f;
+        if (t < T) {
+            const float* kr = kg + (size_t)t * KVD + d0;
+#pragma unroll
+            for (int e = 0; e < DPL; e += 4) {
+                const sgpu_f32x4 k4 = *reinterpret_cast<const sgpu_f32x4*>(kr + e);
+#pragma unroll
+                for (int i = 0; i < 4; i++) s = __builtin_fmaf(qv[e + i], k4[i], s);
+            }
+        }
+        s = sgpu_group_sum<LPT>(s);
+        if (tid % LPT == LPT - 1 && t < T) sc[t] = s * scale;
+    }
+    __syncthreads();
+    float m = -1e30f;
+    for (int t = tid; t < T; t += 256) m = fmaxf(m, sc[t]);
+    m = block_max256(m, red);
+    float sum = 0.0f;
+    for (int t = tid; t < T; t += 256) {
+        const float e = expf(sc[t] - m);
+        sc[t] = e;
+        sum += e;
+    }
+    sum = block_sum256(sum, red);          // its barriers also publish sc[]
+    const int slice = tid / HD, d = tid % HD;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int t = slice; t < T; t += SLICES) acc = __builtin_fmaf(sc[t], vg[(size_t)t * KVD + d], acc);
+    part[tid] = acc;
+    __syncthreads();
+    if (slice == 0) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < SLICES; s2++) tot += part[s2 * HD + d];
+        out[(size_t)h * HD + d] = tot / sum;
+    }
+}
+
+// (value, index) of the first maximum: larger value wins, equal values keep the lower index.
+__device__ __forceinline__ void amax_merge(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+__device__ __forceinline__ void amax_block256(float& bv, int& bi, float* sv, int* si) {
+    for (int off = 32; off > 0; off >>= 1) amax_merge(bv, bi, __shfl_xor(bv, off), __shfl_xor(bi, off));
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+    for (int i = 1; i < 4; i++) amax_merge(bv, bi, sv[i], si[i]);
+}
+
+}  // namespace
+
+using sgpu::WF16;
+
+extern "C" {
+
+// x[i] = h2f(emb[token*C + i]); step = {token, pos} for the kernels that follow.
+__global__ void sgpu_dec_embed(const uint16_t* __restrict__ emb, int token, int pos, float* __restrict__ x, int C,
+                               int* __restrict__ step) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        step[0] = token;
+        step[1] = pos;
+    }
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < C; i += gridDim.x * blockDim.x)
+        x[i] = sgpu_h2f(emb[(size_t)token * C + i]);
+}
+
+// Same, with the token taken from step[0] (written by sgpu_dec_argmax) and pos = step[1] + 1.
+// One block: the step record is read before the barrier and rewritten after it.
+__global__ void __launch_bounds__(256) sgpu_dec_embed_next(const uint16_t* __restrict__ emb, float* __restrict__ x,
+                                                           int C, int* __restrict__ step) {
+    __shared__ int tok;
+    if (threadIdx.x == 0) tok = step[0];
+    __syncthreads();
+    for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = sgpu_h2f(emb[(size_t)tok * C + i]);
+    __syncthreads();
+    if (threadIdx.x == 0) step[1] = step[1] + 1;
+}
+
+// First-max argmax over n logits (qwen_engine.c:360-364 tie rule), stage 1: each of the
+// grid's blocks (256 threads) reduces a contiguous chunk to one (value, index) pair.
+__global__ void __launch_bounds__(256) sgpu_dec_argmax_part(const float* __restrict__ v, int n,
+                                                            float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int chunk = (n + gridDim.x - 1) / gridDim.x;
+    const int lo = blockIdx.x * chunk, hi = min(n, lo + chunk);
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = lo + (int)threadIdx.x; i < hi; i += 256)
+        if (v[i] > best) { best = v[i]; idx = i; }
+    amax_block256(best, idx, sv, si);
+    if (threadIdx.x == 0) { pv[blockIdx.x] = best; pi[blockIdx.x] = idx; }
+}
+
+// Stage 2 (one block of 256 threads over np <= 256 partials): the index goes to step[0] and,
+// if out != NULL, to out[step[1] + 1].
+__global__ void __launch_bounds__(256) sgpu_dec_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                             int np, int* __restrict__ step, int* __restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    if ((int)threadIdx.x < np) { best = pv[threadIdx.x]; idx = pi[threadIdx.x]; }
+    amax_block256(best, idx, sv, si);
+    if (threadIdx.x == 0) {
+        if (idx == 0x7fffffff) idx = 0;
+        step[0] = idx;
+        if (out) out[step[1] + 1] = idx;
+    }
+}
+
+__global__ void __launch_bounds__(256) sgpu_dec_attn64(const float* __restrict__ q, const float* __restrict__ kc,
+                                                       const float* __restrict__ vc, float* __restrict__ out,
+                                                       const int* __restrict__ step, int NH, int NKV, float scale) {
+    dec_attn<64>(q, kc, vc, out, step, NH, NKV, scale);
+}
+__global__ void __launch_bounds__(256) sgpu_dec_attn32(const float* __restrict__ q, const float* __restrict__ kc,
+                                                       const float* __restrict__ vc, float* __restrict__ out,
+                                                       const int* __restrict__ step, int NH, int NKV, float scale) {
+    dec_attn<32>(q, kc, vc, out, step, NH, NKV, scale);
+}
+__global__ void __launch_bounds__(256) sgpu_dec_attn128(const float* __restrict__ q, const float* __restrict__ kc,
+                                                        const float* __restrict__ vc, float* __restrict__ out,
+                                                        const int* __restrict__ step, int NH, int NKV, float scale) {
+    dec_attn<128>(q, kc, vc, out, step, NH, NKV, scale);
+}
+
+}  // extern "C"
+
+// ---- GEMV families, one instantiation per (lanes per team, segments per lane) ----
+#define SGPU_DEC_QKV(LPR, S)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_qkv_l##LPR##_s##S(                              \
+        const uint16_t* __restrict__ W, int K, int nteams, const float* __restrict__ x,                        \
+        const uint16_t* __restrict__ lnw, float eps, const float* __restrict__ bias, float* q, float* kc,      \
+        float* vc, const float* __restrict__ cosT, const float* __restrict__ sinT, const int* __restrict__ step, \
+        int NH, int NKV, int HD) {                                                                             \
+        sgpu::gemv_team<WF16, LPR, S, 2>(W, K, nteams, sgpu::XRms{x, lnw, eps, 0.0f}, sgpu::MapHalfPairs{HD / 2}, \
+                                         EpiQkvRope{bias, q, kc, vc, cosT, sinT, step, NH, NKV, HD});         \
+    }
+#define SGPU_DEC_GATEUP(LPR, S)                                                                                \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_gateup_l##LPR##_s##S(                           \
+        const uint16_t* __restrict__ W, int K, int FC, const float* __restrict__ x,                            \
+        const uint16_t* __restrict__ lnw, float eps, float* __restrict__ y) {                                  \
+        sgpu::gemv_team<WF16, LPR, S, 2>(W, K, FC, sgpu::XRms{x, lnw, eps, 0.0f}, sgpu::MapPair{FC},           \
+                                         EpiSwiGLU{y});                                                        \
+    }
+#define SGPU_DEC_RES(LPR, S)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_res_l##LPR##_s##S(                              \
+        const uint16_t* __restrict__ W, int K, int N, const float* __restrict__ a, const float* bias, float* x) { \
+        sgpu::gemv_team<WF16, LPR, S, 1>(W, K, N, sgpu::XPlain{a}, sgpu::MapRows{}, EpiResidual{x, bias, x});  \
+    }
+#define SGPU_DEC_LMHEAD(LPR, S)                                                                                \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_lmhead_l##LPR##_s##S(                           \
+        const uint16_t* __restrict__ W, int K, int N, const float* __restrict__ x,                             \
+        const uint16_t* __restrict__ lnw, float eps, float* __restrict__ y) {                                  \
+        sgpu::gemv_team<WF16, LPR, S, 1>(W, K, N, sgpu::XRms{x, lnw, eps, 0.0f}, sgpu::MapRows{},              \
+                                         sgpu::EpiStore{nullptr, y});                                          \
+    }
+
+#define SGPU_DEC_PAIRS(F) F(16, 1) F(16, 2) F(16, 4) F(16, 7) F(16, 8) F(64, 1) F(64, 2) F(64, 4) F(64, 8)
+#define SGPU_DEC_SINGLE(F) SGPU_DEC_PAIRS(F) F(256, 1) F(256, 2) F(256, 3) F(256, 4) F(256, 8)
+
+SGPU_DEC_PAIRS(SGPU_DEC_QKV)
+SGPU_DEC_PAIRS(SGPU_DEC_GATEUP)
+SGPU_DEC_SINGLE(SGPU_DEC_RES)
+SGPU_DEC_SINGLE(SGPU_DEC_LMHEAD)

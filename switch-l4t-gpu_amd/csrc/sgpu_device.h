@@ -41,16 +41,18 @@ __device__ __forceinline__ float sgpu_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
 }
 
-// Sum over groups of LANES consecutive lanes (16, 32 or 64).  The total of each group ends
+// Sum over groups of LANES consecutive lanes (4, 8, 16, 32 or 64).  The total of each group ends
 // up in the group's LAST lane (lane % LANES == LANES-1); other lanes hold partial sums.
 // Must run with the whole wave active.
 template <int LANES>
 __device__ __forceinline__ float sgpu_group_sum(float v) {
-    static_assert(LANES == 16 || LANES == 32 || LANES == 64, "group of 16/32/64 lanes");
+    static_assert(LANES == 4 || LANES == 8 || LANES == 16 || LANES == 32 || LANES == 64, "group of 4..64 lanes");
+    // row_shr prefix sums: after the shifts 1, 2, .., LANES/2 (within 16-lane rows) lane
+    // LANES*g + LANES-1 holds exactly the sum of its group's LANES lanes.
     v += sgpu_dpp<SGPU_DPP_ROW_SHR(1)>(v);
     v += sgpu_dpp<SGPU_DPP_ROW_SHR(2)>(v);
-    v += sgpu_dpp<SGPU_DPP_ROW_SHR(4)>(v);
-    v += sgpu_dpp<SGPU_DPP_ROW_SHR(8)>(v);
+    if (LANES >= 8) v += sgpu_dpp<SGPU_DPP_ROW_SHR(4)>(v);
+    if (LANES >= 16) v += sgpu_dpp<SGPU_DPP_ROW_SHR(8)>(v);
     if (LANES >= 32) v += sgpu_dpp<SGPU_DPP_ROW_BCAST15, 0xa>(v);
     if (LANES >= 64) v += sgpu_dpp<SGPU_DPP_ROW_BCAST31, 0xc>(v);
     return v;

@@ -106,6 +106,8 @@ _SIGS = {
     "sgpu_qwen_destroy": (None, [_P]),
     "sgpu_qwen_forward": (_I, [_P, _I, _I, _I, _P]),
     "sgpu_qwen_device_logits": (_P, [_P]),
+    "sgpu_qwen_set_path": (_I, [_P, _I]),
+    "sgpu_qwen_generate": (_I, [_P, _P, _I, _I, _P]),
     "sgpu_gen_sgemm_inputs": (None, [_P, _P, _S, ct.c_uint]),
     "sgpu_frand": (_F, [ct.POINTER(ct.c_uint64)]),
     "sgpu_gen_uniform": (None, [_P, _S, ct.POINTER(ct.c_uint64), _F]),
@@ -295,15 +297,29 @@ def qwen_random_blob(cfg: QwenCfg, seed: int, std: float = 0.02) -> np.ndarray:
     return blob
 
 
+QWEN_PATH_REFERENCE, QWEN_PATH_FUSED, QWEN_PATH_GRAPH = 0, 1, 2
+
+
 class QwenEngine:
     """sgpu_qwen_* engine: weights resident on the device, one forward per position."""
 
-    def __init__(self, cfg: QwenCfg, blob: np.ndarray):
+    def __init__(self, cfg: QwenCfg, blob: np.ndarray, path: int = QWEN_PATH_REFERENCE):
         self.cfg = cfg
         h = ct.c_void_p()
         call("sgpu_qwen_create", ct.byref(h), ct.byref(cfg), np.ascontiguousarray(blob).ctypes.data)
         self.h = h.value
         self.logits = np.empty(cfg.V, np.float32)
+        call("sgpu_qwen_set_path", self.h, path)
+
+    def set_path(self, path: int) -> None:
+        call("sgpu_qwen_set_path", self.h, path)
+
+    def generate(self, prompt, n_gen: int) -> np.ndarray:
+        """Greedy ids: the argmax after the prompt and after each of n_gen generated positions."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_gen + 1, np.int32)
+        call("sgpu_qwen_generate", self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data)
+        return out
 
     def forward(self, token: int, pos: int, want_logits: bool = True):
         call("sgpu_qwen_forward", self.h, token, pos, int(want_logits),

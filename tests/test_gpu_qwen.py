@@ -102,11 +102,17 @@ def test_attention_kernels(gpu, T):
         assert np.array_equal(dout.to_host().reshape(NH, HD), vc.reshape(NKV, HD)[g])
 
 
+PATHS = {"reference": 0, "fused": 1, "graph": 2}
+
+
+@pytest.mark.parametrize("path", sorted(PATHS))
 @pytest.mark.parametrize("std", [0.02, 0.15])
-def test_engine_small_teacher_forced(gpu, og, std):
+def test_engine_small_teacher_forced(gpu, og, std, path):
+    """Every position's logits against the CPU golden, for each launch structure (the graph
+    path replays one captured graph at every position, with eager launches between)."""
     cfg = SMALL
     blob = gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=21, std=std)
-    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob)
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob, PATHS[path])
     gold = og.QwenGolden(og.qwen_cfg(**cfg), blob, NT)
     ids = [int(v) for v in np.random.default_rng(4).integers(0, cfg["V"], 40)]
     for p, t in enumerate(ids):
@@ -118,9 +124,51 @@ def test_engine_small_teacher_forced(gpu, og, std):
     eng.close()
 
 
+@pytest.mark.parametrize("path", ["reference", "graph"])
+def test_engine_small_generate(gpu, og, path):
+    """sgpu_qwen_generate (on-device argmax loop for the graph path) gives the CPU golden's
+    greedy ids."""
+    cfg = SMALL
+    blob = gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=33, std=0.15)
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob, PATHS[path])
+    prompt = [int(v) for v in np.random.default_rng(5).integers(0, cfg["V"], 9)]
+    got = eng.generate(prompt, 20)
+    gold = og.QwenGolden(og.qwen_cfg(**cfg), blob, NT)
+    for p, t in enumerate(prompt):
+        ref = gold.forward(t, p, p == len(prompt) - 1)
+    want = [og.argmax(ref)]
+    for g in range(20):
+        ref = gold.forward(want[-1], len(prompt) + g)
+        want.append(og.argmax(ref))
+    assert got.tolist() == want
+    # a second call restarts the sequence at position 0 and must repeat itself
+    assert eng.generate(prompt, 20).tolist() == want
+    eng.close()
+
+
+def test_engine_full_generate_graph_token_identical(gpu, og):
+    """Full Qwen2.5-0.5B architecture, graph path, on-device greedy loop: 32-token prompt,
+    64 generated positions; the CPU golden, fed the same ids, picks the same argmax at every
+    position."""
+    cfg_g = gpu.qwen_default_cfg()
+    blob = gpu.qwen_random_blob(cfg_g, seed=2024, std=0.02)
+    eng = gpu.QwenEngine(cfg_g, blob, 2)
+    prompt = [int(v) for v in np.random.default_rng(32).integers(0, cfg_g.V, 32)]
+    got = eng.generate(prompt, 64).tolist()
+    ocfg = og.qwen_cfg(cfg_g.V, cfg_g.C, cfg_g.NL, cfg_g.NH, cfg_g.NKV, cfg_g.HD, cfg_g.FC, cfg_g.CTX)
+    gold = og.QwenGolden(ocfg, blob, NT)
+    seq = prompt + got
+    for p in range(len(prompt) + 64):
+        ref = gold.forward(seq[p], p, p >= len(prompt) - 1)
+        if p >= len(prompt) - 1:
+            assert og.argmax(ref) == seq[p + 1], (p, og.argmax(ref), seq[p + 1])
+    eng.close()
+
+
 def test_engine_full_greedy_token_identical(gpu, og):
     """Random-init Qwen2.5-0.5B architecture (N(0, 0.02) weights), 32-token seeded prompt,
-    64 greedy tokens: every GPU token equals the CPU golden's argmax on the same history."""
+    64 greedy tokens on the reference launch sequence: every GPU token equals the CPU
+    golden's argmax on the same history."""
     cfg_g = gpu.qwen_default_cfg()
     say("building full-size random weights")
     blob = gpu.qwen_random_blob(cfg_g, seed=2024, std=0.02)
