@@ -99,7 +99,11 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * reference kernels require multiples of 32/64, switch_gpu.cu:58,98).
  * Replaces cuLaunchKernel(sgemm_*, ...) at gpu_workload.c:90,117,142,168; kernel
  * signatures switch_gpu.cu:5-8 (sgemm_tiled), :59-62 (sgemm_tiled4), :99-102 (sgemm_opt),
- * :140-143 (sgemm_naive). */
+ * :140-143 (sgemm_naive).
+ * sgpu_sgemm_tiled / _tiled4 / _naive launch their own code-object symbol (tiles 64x64,
+ * 128x128; one output per thread).  sgpu_sgemm_opt is the tuned entry: it launches the
+ * sgemm_opt symbol (128x256 tiles) when that grid gives every CU two blocks, else the
+ * 128x128 or 64x64 member, whichever is the largest that does (64x64 at the smallest). */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);

@@ -313,10 +313,12 @@ const void *sgpu_code_object(const char *name, size_t *size) {
 static unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
 static unsigned umin(unsigned a, unsigned b) { return a < b ? a : b; }
 
-static int sgemm_tile(const char *k) {
-    if (!strcmp(k, "sgemm_tiled")) return 64;
-    if (!strcmp(k, "sgemm_tiled4") || !strcmp(k, "sgemm_opt")) return 128;
-    return 0;
+/* Tile shape (rows x columns of C) of each tiled member; 0 for other kernels. */
+static int sgemm_tile(const char *k, int *tn) {
+    if (!strcmp(k, "sgemm_tiled")) return *tn = 64, 64;
+    if (!strcmp(k, "sgemm_tiled4")) return *tn = 128, 128;
+    if (!strcmp(k, "sgemm_opt")) return *tn = 256, 128;
+    return *tn = 0, 0;
 }
 
 static int geometry(const devstate *d, const char *kernel, int M, int N, int K, unsigned g[3], unsigned b[3]) {
@@ -324,9 +326,9 @@ static int geometry(const devstate *d, const char *kernel, int M, int N, int K, 
     const unsigned cus = d ? (unsigned)d->cus : 256u;
     g[0] = g[1] = g[2] = 1;
     b[0] = b[1] = b[2] = 1;
-    int tile = sgemm_tile(kernel);
+    int tile_n, tile = sgemm_tile(kernel, &tile_n);
     if (tile) {
-        long long nt = (long long)cdiv(M, tile) * cdiv(N, tile);
+        long long nt = (long long)cdiv(M, tile) * cdiv(N, tile_n);
         g[0] = (unsigned)(nt > 0 ? nt : 1);
         b[0] = 256;
         return SGPU_OK;
@@ -391,8 +393,21 @@ int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
 }
+/* The optimised entry picks the largest tile whose grid still gives every CU two blocks
+ * (all three run two or more blocks per CU), falling back to the 64x64 member. */
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
-    return sgemm_common(K_SGEMM_OPT, "sgemm_opt", A, B, C, M, N, K, stream);
+    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    if (!C || (K > 0 && (!A || !B))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    const long long want = 2LL * d->cus;
+    if ((long long)cdiv(M, 128) * cdiv(N, 256) >= want)
+        return sgemm_common(K_SGEMM_OPT, "sgemm_opt", A, B, C, M, N, K, stream);
+    if ((long long)cdiv(M, 128) * cdiv(N, 128) >= want)
+        return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
+    return sgemm_common(K_SGEMM_TILED, "sgemm_tiled", A, B, C, M, N, K, stream);
 }
 int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_NAIVE, "sgemm_naive", A, B, C, M, N, K, stream);

@@ -58,84 +58,252 @@ __device__ __forceinline__ void sgemm_tile_coords(int t, int ntm, int ntn, bool 
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN>
+struct SgemmLds {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+    float As[2][BK][T::LDA];
+    float Bs[2][BK][T::LDB];
+};
+
+// Per-thread constants of one tile's staging and operand reads.
+template <int BM, int BN, int BK, int WGM, int WGN>
+struct SgemmThread {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+    int tid, wm, wn, l32, khalf;
+    __device__ __forceinline__ SgemmThread() {
+        tid = sgpu_tid();
+        const int lane = tid & 63, wave = tid >> 6;
+        wm = wave / WGN;
+        wn = wave % WGN;
+        l32 = lane & 31;
+        khalf = lane >> 5;
+    }
+};
+
+// Registers -> LDS buffer s (A transposed to k-major).
+template <int BM, int BN, int BK, int WGM, int WGN>
+__device__ __forceinline__ void sgemm_store_slice(SgemmLds<BM, BN, BK, WGM, WGN>& L, int s, int tid,
+                                                  const sgpu_f32x4* ra, const sgpu_f32x4* rb) {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+#pragma unroll
+    for (int r = 0; r < T::A_PER_T; r++) {
+        const int idx = tid + r * T::NT, row = idx / T::KQ, kq = idx % T::KQ;
+        L.As[s][4 * kq + 0][row] = ra[r].x;
+        L.As[s][4 * kq + 1][row] = ra[r].y;
+        L.As[s][4 * kq + 2][row] = ra[r].z;
+        L.As[s][4 * kq + 3][row] = ra[r].w;
+    }
+#pragma unroll
+    for (int r = 0; r < T::B_PER_T; r++) {
+        const int idx = tid + r * T::NT, kr = idx / T::NQ, nq = idx % T::NQ;
+        *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][kr][4 * nq]) = rb[r];
+    }
+}
+
+// D layout of a 32x32 block: lane l, acc r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+template <int BM, int BN, int BK, int WGM, int WGN>
+__device__ __forceinline__ void sgemm_store_c(float* __restrict__ C, int M, int N, int m0, int n0, bool interior,
+                                              const SgemmThread<BM, BN, BK, WGM, WGN>& th,
+                                              sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+#pragma unroll
+    for (int i = 0; i < T::FM; i++)
+#pragma unroll
+        for (int j = 0; j < T::FN; j++) {
+            const int gn = n0 + th.wn * T::WTN + j * 32 + th.l32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int gm = m0 + th.wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * th.khalf + (r & 3);
+                if (interior || (gm < M && gn < N)) C[(size_t)gm * N + gn] = acc[i][j][r];
+            }
+        }
+}
+
+// One tile, any shape: bounds-checked scalar loads where the fast dwordx4 path does not apply.
+template <int BM, int BN, int BK, int WGM, int WGN>
+__device__ __forceinline__ void sgemm_tile_generic(const float* __restrict__ A, const float* __restrict__ B,
+                                                   int M, int N, int K, int m0, int n0, bool interior, bool aligned,
+                                                   SgemmLds<BM, BN, BK, WGM, WGN>& L,
+                                                   const SgemmThread<BM, BN, BK, WGM, WGN>& th,
+                                                   sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+    const int tid = th.tid, nk = (K + BK - 1) / BK;
+    sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
+    auto load_slice = [&](int kt) {
+        const int k0 = kt * BK;
+        const bool fast = interior && aligned && (k0 + BK <= K);
+#pragma unroll
+        for (int r = 0; r < T::A_PER_T; r++) {
+            const int idx = tid + r * T::NT, row = idx / T::KQ, kq = idx % T::KQ;
+            const int gm = m0 + row, gk = k0 + 4 * kq;
+            if (fast) {
+                ra[r] = *reinterpret_cast<const sgpu_f32x4*>(A + (size_t)gm * K + gk);
+            } else {
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    v[j] = (gm < M && gk + j < K) ? A[(size_t)gm * K + gk + j] : 0.0f;
+                ra[r] = sgpu_f32x4{v[0], v[1], v[2], v[3]};
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < T::B_PER_T; r++) {
+            const int idx = tid + r * T::NT, kr = idx / T::NQ, nq = idx % T::NQ;
+            const int gk = k0 + kr, gn = n0 + 4 * nq;
+            if (fast) {
+                rb[r] = *reinterpret_cast<const sgpu_f32x4*>(B + (size_t)gk * N + gn);
+            } else {
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    v[j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : 0.0f;
+                rb[r] = sgpu_f32x4{v[0], v[1], v[2], v[3]};
+            }
+        }
+    };
+
+    if (nk > 0) {
+        load_slice(0);
+        sgemm_store_slice(L, 0, tid, ra, rb);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int s = kt & 1;
+        if (kt + 1 < nk) load_slice(kt + 1);      // in flight while the MFMAs run
+#pragma unroll
+        for (int ks = 0; ks < BK / 2; ks++) {
+            const int kk = 2 * ks + th.khalf;     // MFMA src layout: lane = i + 32*k
+            float a[T::FM], b[T::FN];
+#pragma unroll
+            for (int i = 0; i < T::FM; i++) a[i] = L.As[s][kk][th.wm * T::WTM + i * 32 + th.l32];
+#pragma unroll
+            for (int j = 0; j < T::FN; j++) b[j] = L.Bs[s][kk][th.wn * T::WTN + j * 32 + th.l32];
+#pragma unroll
+            for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                for (int j = 0; j < T::FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) sgemm_store_slice(L, s ^ 1, tid, ra, rb);
+        __syncthreads();
+    }
+}
+
+// One interior tile with K a multiple of BK (at least two slices) and 16-byte aligned rows:
+// software-pipelined.  Slice kt+1's global loads are issued before slice kt's MFMAs; each
+// k-step's LDS operands are read one step ahead into a second register set, so their
+// latency runs under the previous step's MFMAs; slice kt+1 is written to the idle LDS buffer
+// after MFMA step STORE_AT of slice kt, once its loads have had that long to land.  One
+// barrier per slice.  Same MFMA sequence per accumulator as the generic path.
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT>
+__device__ __forceinline__ void sgemm_tile_fast(const float* __restrict__ A, const float* __restrict__ B,
+                                                int N, int K, int m0, int n0,
+                                                SgemmLds<BM, BN, BK, WGM, WGN>& L,
+                                                const SgemmThread<BM, BN, BK, WGM, WGN>& th,
+                                                sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+    constexpr int NS = BK / 2;                    // MFMA k-steps per slice
+    static_assert(STORE_AT >= 0 && STORE_AT < NS, "store point inside the slice");
+    const int tid = th.tid, nk = K / BK;
+    static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
+    // Load round r of a thread reads A row (tid/KQ + r*NT/KQ) and B row (tid/NQ + r*NT/NQ):
+    // one base pointer each plus wave-uniform strides.
+    const float* pa = A + (size_t)(m0 + tid / T::KQ) * K + 4 * (tid % T::KQ);
+    const float* pb = B + (size_t)(tid / T::NQ) * N + n0 + 4 * (tid % T::NQ);
+    const size_t astep = (size_t)(T::NT / T::KQ) * K, bstep_r = (size_t)(T::NT / T::NQ) * N;
+    const size_t bstep = (size_t)BK * N;
+    sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
+    auto load_slice = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < T::A_PER_T; r++)
+            ra[r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
+#pragma unroll
+        for (int r = 0; r < T::B_PER_T; r++)
+            rb[r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
+    };
+    auto read_ops = [&](int s, int ks, float* a, float* b) __attribute__((always_inline)) {
+        const int kk = 2 * ks + th.khalf;
+#pragma unroll
+        for (int i = 0; i < T::FM; i++) a[i] = L.As[s][kk][th.wm * T::WTM + i * 32 + th.l32];
+#pragma unroll
+        for (int j = 0; j < T::FN; j++) b[j] = L.Bs[s][kk][th.wn * T::WTN + j * 32 + th.l32];
+    };
+    auto slice = [&](int s, bool more) __attribute__((always_inline)) {
+        float a[2][T::FM], b[2][T::FN];
+        read_ops(s, 0, a[0], b[0]);
+#pragma unroll
+        for (int ks = 0; ks < NS; ks++) {
+            const int c = ks & 1;
+            if (ks + 1 < NS) read_ops(s, ks + 1, a[c ^ 1], b[c ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);    // keep the next step's reads ahead of these MFMAs
+#pragma unroll
+            for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                for (int j = 0; j < T::FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
+            if (more && ks == STORE_AT) sgemm_store_slice(L, s ^ 1, tid, ra, rb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    load_slice(0);
+    sgemm_store_slice(L, 0, tid, ra, rb);
+    __syncthreads();
+    for (int kt = 0; kt + 1 < nk; kt++) {
+        load_slice(kt + 1);
+        __builtin_amdgcn_sched_barrier(0);        // issue the loads before the first MFMA
+        slice(kt & 1, true);
+        __syncthreads();
+    }
+    slice((nk - 1) & 1, false);
+    __syncthreads();                              // the next tile overwrites both buffers
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT = -1>
 __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const float* __restrict__ B,
                                            float* __restrict__ C, int M, int N, int K) {
     using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    __shared__ __attribute__((aligned(16))) float As[2][BK][T::LDA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][T::LDB];   // rows written as float4
+    __shared__ __attribute__((aligned(16))) SgemmLds<BM, BN, BK, WGM, WGN> L;
 
     // The tile split assumes exactly NT threads per block; any other block size is rejected
     // by every thread alike (no barrier is reached, C is left untouched).
     if (sgpu_nthreads() != T::NT) return;
-    const int tid = sgpu_tid();
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int l32 = lane & 31, khalf = lane >> 5;
+    const SgemmThread<BM, BN, BK, WGM, WGN> th;
 
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN, ntiles = ntm * ntn;
     const int nb = sgpu_nblocks();
     const bool remap = (nb == ntiles) && (ntiles % kXcds == 0);
     const bool aligned = ((K & 3) == 0) && ((N & 3) == 0) &&
                          ((((uintptr_t)A) | ((uintptr_t)B)) & 15) == 0;
-    const int nk = (K + BK - 1) / BK;
 
+    // Whole-problem check (uniform): every tile interior, K whole slices, 16-byte rows.  The
+    // pipelined and generic paths get separate tile loops so neither carries the other's
+    // registers.
+    const bool all_fast = STORE_AT >= 0 && aligned && M % BM == 0 && N % BN == 0 &&
+                          K % BK == 0 && K >= 2 * BK;
+    if constexpr (STORE_AT >= 0) {
+        if (all_fast) {
+            for (int t = sgpu_bid(); t < ntiles; t += nb) {
+                int tm, tn;
+                sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+                const int m0 = tm * BM, n0 = tn * BN;
+                sgpu_f32x16 acc[T::FM][T::FN];
+#pragma unroll
+                for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                    for (int j = 0; j < T::FN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+                sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
+                sgemm_store_c(C, M, N, m0, n0, true, th, acc);
+            }
+            return;
+        }
+    }
     for (int t = sgpu_bid(); t < ntiles; t += nb) {
         int tm, tn;
         sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
         const int m0 = tm * BM, n0 = tn * BN;
         const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
-
-        float4 ra[T::A_PER_T], rb[T::B_PER_T];
-        // Global -> registers for k-slice kt (fast dwordx4 path or bounds-checked scalars).
-        auto load_slice = [&](int kt) {
-            const int k0 = kt * BK;
-            const bool fast = interior && aligned && (k0 + BK <= K);
-#pragma unroll
-            for (int r = 0; r < T::A_PER_T; r++) {
-                const int idx = tid + r * T::NT, row = idx / T::KQ, kq = idx % T::KQ;
-                const int gm = m0 + row, gk = k0 + 4 * kq;
-                if (fast) {
-                    ra[r] = *reinterpret_cast<const float4*>(A + (size_t)gm * K + gk);
-                } else {
-                    float v[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        v[j] = (gm < M && gk + j < K) ? A[(size_t)gm * K + gk + j] : 0.0f;
-                    ra[r] = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < T::B_PER_T; r++) {
-                const int idx = tid + r * T::NT, kr = idx / T::NQ, nq = idx % T::NQ;
-                const int gk = k0 + kr, gn = n0 + 4 * nq;
-                if (fast) {
-                    rb[r] = *reinterpret_cast<const float4*>(B + (size_t)gk * N + gn);
-                } else {
-                    float v[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        v[j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : 0.0f;
-                    rb[r] = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            }
-        };
-        // Registers -> LDS buffer s (A transposed to k-major).
-        auto store_slice = [&](int s) {
-#pragma unroll
-            for (int r = 0; r < T::A_PER_T; r++) {
-                const int idx = tid + r * T::NT, row = idx / T::KQ, kq = idx % T::KQ;
-                As[s][4 * kq + 0][row] = ra[r].x;
-                As[s][4 * kq + 1][row] = ra[r].y;
-                As[s][4 * kq + 2][row] = ra[r].z;
-                As[s][4 * kq + 3][row] = ra[r].w;
-            }
-#pragma unroll
-            for (int r = 0; r < T::B_PER_T; r++) {
-                const int idx = tid + r * T::NT, kr = idx / T::NQ, nq = idx % T::NQ;
-                *reinterpret_cast<float4*>(&Bs[s][kr][4 * nq]) = rb[r];
-            }
-        };
-
         sgpu_f32x16 acc[T::FM][T::FN];
 #pragma unroll
         for (int i = 0; i < T::FM; i++)
@@ -143,45 +311,8 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
             for (int j = 0; j < T::FN; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-
-        if (nk > 0) {
-            load_slice(0);
-            store_slice(0);
-        }
-        __syncthreads();
-        for (int kt = 0; kt < nk; kt++) {
-            const int s = kt & 1;
-            if (kt + 1 < nk) load_slice(kt + 1);      // in flight while the MFMAs run
-#pragma unroll
-            for (int ks = 0; ks < BK / 2; ks++) {
-                const int kk = 2 * ks + khalf;        // MFMA src layout: lane = i + 32*k
-                float a[T::FM], b[T::FN];
-#pragma unroll
-                for (int i = 0; i < T::FM; i++) a[i] = As[s][kk][wm * T::WTM + i * 32 + l32];
-#pragma unroll
-                for (int j = 0; j < T::FN; j++) b[j] = Bs[s][kk][wn * T::WTN + j * 32 + l32];
-#pragma unroll
-                for (int i = 0; i < T::FM; i++)
-#pragma unroll
-                    for (int j = 0; j < T::FN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-            }
-            if (kt + 1 < nk) store_slice(s ^ 1);
-            __syncthreads();
-        }
-
-        // D layout of a 32x32 block: lane l, acc r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
-#pragma unroll
-        for (int i = 0; i < T::FM; i++)
-#pragma unroll
-            for (int j = 0; j < T::FN; j++) {
-                const int gn = n0 + wn * T::WTN + j * 32 + l32;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int gm = m0 + wm * T::WTM + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-                    if (interior || (gm < M && gn < N)) C[(size_t)gm * N + gn] = acc[i][j][r];
-                }
-            }
+        sgemm_tile_generic(A, B, M, N, K, m0, n0, interior, aligned, L, th, acc);
+        sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
     }
 }
 
@@ -189,22 +320,25 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 
 extern "C" {
 
-// 64x64 tile, 4 waves of 32x32: the small-tile member (more blocks at small sizes).
-__global__ void __launch_bounds__(256) sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B,
-                                                   float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<64, 64, 16, 2, 2>(A, B, C, M, N, K);
+// The three tiled members differ only in tile shape; each takes the pipelined path on
+// interior-only shapes (M, N multiples of the tile, K a multiple of BK, 16-byte rows) and
+// the bounds-checked path otherwise.
+//   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each) -- small shapes
+//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks)
+//   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks) -- large shapes
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    sgemm_mfma<64, 64, 32, 2, 2, 8>(A, B, C, M, N, K);
 }
 
-// 128x128 tile, 4 waves of 64x64 (2x2 MFMA blocks per wave).
-__global__ void __launch_bounds__(256) sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B,
-                                                    float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 128, 16, 2, 2>(A, B, C, M, N, K);
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    sgemm_mfma<128, 128, 32, 2, 2, 4>(A, B, C, M, N, K);
 }
 
-// Large-matrix member: 128x128 tile, BK 32.
-__global__ void __launch_bounds__(256) sgemm_opt(const float* __restrict__ A, const float* __restrict__ B,
-                                                 float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 128, 32, 2, 2>(A, B, C, M, N, K);
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+sgemm_opt(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    sgemm_mfma<128, 256, 16, 2, 2, 4>(A, B, C, M, N, K);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:

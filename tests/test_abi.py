@@ -74,6 +74,8 @@ def test_geometry_contract(sg):
     g, b = (ct.c_uint * 3)(), (ct.c_uint * 3)()
     L = sg.lib()
     assert L.sgpu_kernel_geometry(b"sgemm_opt", 4096, 4096, 4096, g, b) == 0
+    assert tuple(b) == (256, 1, 1) and g[0] == 32 * 16          # one 128x256 tile per block
+    assert L.sgpu_kernel_geometry(b"sgemm_tiled4", 4096, 4096, 4096, g, b) == 0
     assert tuple(b) == (256, 1, 1) and g[0] == 32 * 32          # one 128x128 tile per block
     assert L.sgpu_kernel_geometry(b"sgemm_tiled", 1023, 1025, 997, g, b) == 0
     assert g[0] == 16 * 17                                       # ceil(1023/64) * ceil(1025/64)
