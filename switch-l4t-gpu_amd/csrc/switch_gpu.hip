@@ -19,6 +19,8 @@
 // grid of 64*WGM*WGN-thread blocks is correct (surplus blocks exit); with one block per tile
 // the index is remapped so each XCD (blocks are dealt round-robin to the 8 XCDs) works on a
 // compact group of tiles that shares A and B panels in its own L2.
+#include <type_traits>
+
 #include "sgpu_device.h"
 
 typedef float sgpu_f32x16 __attribute__((ext_vector_type(16)));
@@ -258,11 +260,146 @@ __device__ __forceinline__ void sgemm_tile_fast(const float* __restrict__ A, con
     __syncthreads();                              // the next tile overwrites both buffers
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT = -1>
+// Second LDS layout for the pipelined path: A m-major (row pitch BK+4 floats), B k-major
+// (row pitch BN+8).  Both are written straight from the dwordx4 global loads.  Inside a
+// slice the MFMA k-steps run in groups of four with the k order permuted per lane half:
+// at step t of group g, lane half h supplies k = 8g + 4h + t, so a lane's four A operands of
+// a group are four consecutive floats of one LDS row (one ds_read_b128; rows BK+4 apart put
+// 16 lanes on 64 distinct banks) and its B operands are four single floats of rows
+// 8g+4h+t (the two lane halves 4 rows = 32 banks apart).
+template <int BM, int BN, int BK, int WGM, int WGN>
+struct SgemmLdsM {
+    static constexpr int LDAM = BK + 4, LDBM = BN + 8;
+    float As[2][BM][LDAM];
+    float Bs[2][BK][LDBM];
+};
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false>
+__device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, const float* __restrict__ B,
+                                                  int N, int K, int m0, int n0,
+                                                  SgemmLdsM<BM, BN, BK, WGM, WGN>& L,
+                                                  const SgemmThread<BM, BN, BK, WGM, WGN>& th,
+                                                  sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
+    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+    constexpr int NG = BK / 8;                    // 4-step groups per slice
+    static_assert(BK % 8 == 0, "k slice of whole 8-deep groups");
+    static_assert(STORE_G >= 0 && STORE_G < NG, "store point inside the slice");
+    static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
+    const int tid = th.tid, nk = K / BK;
+    const float* pa = A + (size_t)(m0 + tid / T::KQ) * K + 4 * (tid % T::KQ);
+    const float* pb = B + (size_t)(tid / T::NQ) * N + n0 + 4 * (tid % T::NQ);
+    const size_t astep = (size_t)(T::NT / T::KQ) * K, bstep_r = (size_t)(T::NT / T::NQ) * N;
+    const size_t bstep = (size_t)BK * N;
+    sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
+    auto load_slice = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < T::A_PER_T; r++)
+            ra[r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
+#pragma unroll
+        for (int r = 0; r < T::B_PER_T; r++)
+            rb[r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
+    };
+    auto store_slice = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < T::A_PER_T; r++) {
+            const int idx = tid + r * T::NT;
+            *reinterpret_cast<sgpu_f32x4*>(&L.As[s][idx / T::KQ][4 * (idx % T::KQ)]) = ra[r];
+        }
+#pragma unroll
+        for (int r = 0; r < T::B_PER_T; r++) {
+            const int idx = tid + r * T::NT;
+            *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][idx / T::NQ][4 * (idx % T::NQ)]) = rb[r];
+        }
+    };
+    auto read_group = [&](int s, int g, sgpu_f32x4* a, sgpu_f32x4* b) __attribute__((always_inline)) {
+        const int kc = 8 * g + 4 * th.khalf;
+#pragma unroll
+        for (int i = 0; i < T::FM; i++)
+            a[i] = *reinterpret_cast<const sgpu_f32x4*>(&L.As[s][th.wm * T::WTM + i * 32 + th.l32][kc]);
+#pragma unroll
+        for (int t = 0; t < 4; t++)                // step-major, so step 0 can start first
+#pragma unroll
+            for (int j = 0; j < T::FN; j++) b[j][t] = L.Bs[s][kc + t][th.wn * T::WTN + j * 32 + th.l32];
+    };
+    // SPREAD: the slice's memory instructions (next slice's global loads in group 0, next
+    // group's LDS reads, the slice store in group STORE_G) are dealt out one per MFMA instead
+    // of issued in bursts, so the MFMA stream never waits behind a full memory queue.
+    auto slice = [&](int s, int kt_next, auto more_c) __attribute__((always_inline)) {
+        constexpr bool more = decltype(more_c)::value;
+        constexpr int NMF = 4 * T::FM * T::FN;
+        sgpu_f32x4 a[2][T::FM], b[2][T::FN];
+        if constexpr (!SPREAD) {
+            if (more) load_slice(kt_next);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        read_group(s, 0, a[0], b[0]);
+        if constexpr (SPREAD) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const int c = g & 1;
+            if constexpr (SPREAD) {
+                if (more && g == 0) load_slice(kt_next);
+            }
+            if (g + 1 < NG) read_group(s, g + 1, a[c ^ 1], b[c ^ 1]);
+            if constexpr (!SPREAD) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                    for (int j = 0; j < T::FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i][t], b[c][j][t], acc[i][j], 0, 0, 0);
+            if (more && g == STORE_G) store_slice(s ^ 1);
+            if constexpr (SPREAD) {
+#pragma unroll
+                for (int q = 0; q < NMF; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // 1 MFMA
+                    if (more && g == 0 && q < T::A_PER_T + T::B_PER_T)
+                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);              // 1 global load
+                    if (g + 1 < NG && q < T::FM + 4 * T::FN)
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // 1 LDS read
+                    if (more && g == STORE_G && q >= NMF / 2 && q < NMF / 2 + T::A_PER_T + T::B_PER_T)
+                        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);              // 1 LDS write
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    load_slice(0);
+    store_slice(0);
+    __syncthreads();
+    for (int kt = 0; kt + 1 < nk; kt++) {
+        slice(kt & 1, kt + 1, std::true_type{});
+        __syncthreads();
+    }
+    slice((nk - 1) & 1, 0, std::false_type{});
+    __syncthreads();
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN>
+union SgemmLdsU {
+    SgemmLds<BM, BN, BK, WGM, WGN> k;
+    SgemmLdsM<BM, BN, BK, WGM, WGN> m;
+};
+
+template <int BM, int BN, int BK, int WGM, int WGN>
+__device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLds<BM, BN, BK, WGM, WGN>& l) { return l; }
+template <int BM, int BN, int BK, int WGM, int WGN>
+__device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLdsU<BM, BN, BK, WGM, WGN>& u) { return u.k; }
+
+// STORE_AT < 0: generic path only.  Otherwise the pipelined path runs on interior-only
+// shapes with the slice store after k-step (LAYOUT 0) or 4-step group (LAYOUT 1, 2) STORE_AT.
+// LAYOUT 0: k-major A staging; 1: m-major A staging; 2: m-major with memory instructions
+// spread one per MFMA.
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT = -1, int LAYOUT = 0>
 __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const float* __restrict__ B,
                                            float* __restrict__ C, int M, int N, int K) {
     using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    __shared__ __attribute__((aligned(16))) SgemmLds<BM, BN, BK, WGM, WGN> L;
+    using LdsT = typename std::conditional<LAYOUT >= 1, SgemmLdsU<BM, BN, BK, WGM, WGN>,
+                                           SgemmLds<BM, BN, BK, WGM, WGN>>::type;
+    __shared__ __attribute__((aligned(16))) LdsT LU;
+    SgemmLds<BM, BN, BK, WGM, WGN>& L = sgemm_lds_k(LU);
 
     // The tile split assumes exactly NT threads per block; any other block size is rejected
     // by every thread alike (no barrier is reached, C is left untouched).
@@ -293,7 +430,10 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                     for (int j = 0; j < T::FN; j++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-                sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
+                if constexpr (LAYOUT >= 1)
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT == 2>(A, B, N, K, m0, n0, LU.m, th, acc);
+                else
+                    sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
                 sgemm_store_c(C, M, N, m0, n0, true, th, acc);
             }
             return;
@@ -323,9 +463,12 @@ extern "C" {
 // The three tiled members differ only in tile shape; each takes the pipelined path on
 // interior-only shapes (M, N multiples of the tile, K a multiple of BK, 16-byte rows) and
 // the bounds-checked path otherwise.
-//   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each) -- small shapes
-//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks)
-//   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks) -- large shapes
+//   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), k-major A
+//                  staging -- small shapes
+//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks), m-major A staging,
+//                  memory instructions spread over the MFMA stream
+//   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks), m-major A staging,
+//                  spread -- large shapes
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_mfma<64, 64, 32, 2, 2, 8>(A, B, C, M, N, K);
@@ -333,12 +476,12 @@ sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __r
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 128, 32, 2, 2, 4>(A, B, C, M, N, K);
+    sgemm_mfma<128, 128, 32, 2, 2, 3, 2>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_opt(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 256, 16, 2, 2, 4>(A, B, C, M, N, K);
+    sgemm_mfma<128, 256, 16, 2, 2, 0, 2>(A, B, C, M, N, K);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:
