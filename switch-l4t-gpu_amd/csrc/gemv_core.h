@@ -18,6 +18,8 @@
 //    for 256-lane teams, one LDS exchange across the four waves.
 // Weights are read with the nontemporal hint: each byte is used exactly once per call.
 #pragma once
+#include <type_traits>
+
 #include "sgpu_device.h"
 
 namespace sgpu {
@@ -355,6 +357,133 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------
+// Batched GEMV on the fp32 matrix cores (gemv_multi role when K % 4 == 0 and the rows are
+// 16-byte aligned): Y[t*N+n] = sum_k W[n*K+k] * X[t*K+k] + bias?[n], with
+// v_mfma_f32_32x32x2_f32 (fp32 inputs, fp32 accumulate).
+//
+// A 256-thread block owns a 32-token x 32*FN-row output tile; its four waves split K into
+// contiguous ranges of 32-deep chunks and their partial tiles are summed through LDS in wave
+// order (deterministic).  Per chunk a wave loads its 32 token rows and 32*FN weight rows with
+// coalesced dwordx4 loads (8 lanes cover one 128-byte row segment), writes them to its own
+// LDS region (row pitch 36 floats) and reads them back in the MFMA operand layout: lane
+// (i, h) (i = lane % 32, h = lane / 32) takes floats k0 + 16h + 4v .. +3 of row i as one
+// ds_read_b128 per v, and MFMA step s = 4v + e uses element e, so lane half h covers
+// k = k0 + 16h + s on both operands.  The region is private to the wave (in-order LDS
+// access, no block barrier).  The next chunk's global loads are issued before the current
+// chunk's MFMAs.  Rows past T or N read a clamped (valid) row and are never stored; a K tail
+// chunk loads zeros past K.  Tiles are walked grid-stride over a linear block id (any grid of
+// 256-thread blocks); with one block per tile, block ids are regrouped so each XCD runs a
+// contiguous run of tiles (token tiles fastest: the blocks on one XCD share W panels in its
+// L2).
+template <int FN>
+__device__ __forceinline__ void gemm_nt_mfma(const float* __restrict__ W, const float* __restrict__ X,
+                                             const float* __restrict__ bias, float* __restrict__ Y,
+                                             int K, int N, int T) {
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    constexpr int NW = 4;                                   // waves per block (K split)
+    constexpr int R = 32 * (1 + FN);                        // staged rows per wave: tokens, then W
+    constexpr int NI = R / 8;                               // coalesced loads per lane per chunk
+    constexpr int P = 36;                                   // LDS row pitch (floats)
+    __shared__ __attribute__((aligned(16))) float stage[NW][R][P];
+    static_assert(16 * FN * 64 <= R * P, "partial tile fits the wave's staging region");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 31, h = lane >> 5;
+    const int lr = lane >> 3, lq = lane & 7;                // coalesced: row in 8-row group, quad
+    const int ntt = (T + 31) / 32, ntn = (N + 32 * FN - 1) / (32 * FN), ntiles = ntt * ntn;
+    const int nch = (K + 31) / 32;
+    const int c0 = wave * nch / NW, c1 = (wave + 1) * nch / NW;
+    const int nb = gridDim.x * gridDim.y;
+    const int bid = blockIdx.x + blockIdx.y * gridDim.x;
+    const bool remap = (nb == ntiles) && (ntiles % 8 == 0);
+    float (*st)[P] = stage[wave];
+
+    for (int tile = bid; tile < ntiles; tile += nb) {
+        const int tl = remap ? (tile % 8) * (ntiles / 8) + tile / 8 : tile;
+        const int t0 = (tl % ntt) * 32, n0 = (tl / ntt) * 32 * FN;
+        // Row q*8 + lr of the staged block: token rows first, then weight rows.
+        const float* src[NI];
+#pragma unroll
+        for (int q = 0; q < NI; q++) {
+            const int r = 8 * q + lr;
+            src[q] = r < 32 ? X + (size_t)min(t0 + r, T - 1) * K + 4 * lq
+                            : W + (size_t)min(n0 + r - 32, N - 1) * K + 4 * lq;
+        }
+
+        f32x16 acc[FN];
+#pragma unroll
+        for (int f = 0; f < FN; f++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[f][r] = 0.0f;
+        sgpu_f32x4 g[NI];
+        auto load = [&](int c) __attribute__((always_inline)) {
+            const int k0 = 32 * c;
+            const bool ok = k0 + 4 * lq < K;                // K % 4 == 0: whole quads
+            const sgpu_f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < NI; q++) g[q] = ok ? *reinterpret_cast<const sgpu_f32x4*>(src[q] + k0) : z;
+        };
+        auto chunk = [&](bool more, int cn) __attribute__((always_inline)) {
+#pragma unroll
+            for (int q = 0; q < NI; q++) *reinterpret_cast<sgpu_f32x4*>(&st[8 * q + lr][4 * lq]) = g[q];
+            if (more) load(cn);                             // next chunk in flight during the MFMAs
+            sgpu_f32x4 xa[4], wa[FN][4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                xa[v] = *reinterpret_cast<const sgpu_f32x4*>(&st[i][16 * h + 4 * v]);
+#pragma unroll
+                for (int f = 0; f < FN; f++)
+                    wa[f][v] = *reinterpret_cast<const sgpu_f32x4*>(&st[32 + 32 * f + i][16 * h + 4 * v]);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; s++)
+#pragma unroll
+                for (int f = 0; f < FN; f++)
+                    acc[f] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[s >> 2][s & 3], wa[f][s >> 2][s & 3], acc[f], 0, 0, 0);
+        };
+        if (c0 < c1) load(c0);
+        for (int c = c0; c < c1; c++) chunk(c + 1 < c1, c + 1);
+
+        // Partial tiles go to each wave's own staging region (done with it for this tile).
+        auto red = [&](int w, int a) __attribute__((always_inline)) -> float& {
+            return (&stage[w][0][0])[a * 64 + lane];
+        };
+#pragma unroll
+        for (int f = 0; f < FN; f++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) red(wave, 16 * f + r) = acc[f][r];
+        __syncthreads();
+        // Wave w finishes accumulator rows r = w*16/NW .. (w+1)*16/NW - 1 of every block,
+        // summing the NW partials in wave order.  D layout: lane l, acc r -> token
+        // 8*(r/4) + 4*(l/32) + r%4, row l%32.
+        constexpr int RPW = 16 / NW;
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+            const int n = n0 + 32 * f + i;
+            const float bv = (bias && n < N) ? bias[n] : 0.0f;
+#pragma unroll
+            for (int rr = 0; rr < RPW; rr++) {
+                const int r = RPW * wave + rr;
+                float v = red(0, 16 * f + r);
+#pragma unroll
+                for (int w = 1; w < NW; w++) v += red(w, 16 * f + r);
+                const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (t < T && n < N) Y[(size_t)t * N + n] = v + bv;
+            }
+        }
+        __syncthreads();                          // staging is reused by the next tile
+    }
+}
+
+// Choice of the matrix-core path: whole 16-byte quads on 16-byte aligned rows, blocks of
+// exactly 256 threads in x, and enough tokens to beat the vector path (below 4 tokens, or
+// up to 8 tokens on rows longer than 1024, the wave-per-row kernel is as fast or faster:
+// with so few 32x32 tiles the weight stream runs on too few CUs).  The host launcher
+// applies the same rule (sgpu.c) to size the grid.
+__device__ __forceinline__ bool gemm_nt_ok(const float* W, const float* X, int K, int T) {
+    return K > 0 && (K % 4 == 0) && ((((uintptr_t)W) | ((uintptr_t)X)) & 15) == 0 && blockDim.x == 256 &&
+           blockDim.y == 1 && blockDim.z == 1 && T >= 4 && !(T <= 8 && K > 1024);
+}
+
 // Weight-stationary batched GEMV (gemv_multi role): Y[t*N+n] = W[n,:].X[t,:] + bias?[n].
 // A wave owns one row and a chunk of up to TW tokens: the row is streamed once per chunk
 // while TW register accumulators collect the chunk's dot products.

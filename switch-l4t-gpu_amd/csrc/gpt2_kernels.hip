@@ -47,10 +47,16 @@ __global__ void gemv_warp_b(const float* __restrict__ W, const float* __restrict
     sgpu::gemv_generic<sgpu::WF32>(W, x, bias, y, K, N);
 }
 
+// Matrix-core path (32-token x 32-row tiles) for whole-quad aligned rows, 256-thread blocks
+// and four or more tokens; otherwise the wave-per-row vector path (any K, alignment, block
+// size, token count).
 __global__ void __launch_bounds__(256) gemv_multi(const float* __restrict__ W, const float* __restrict__ X,
                                                   const float* __restrict__ bias, float* __restrict__ Y,
                                                   int K, int N, int T) {
-    sgpu::gemv_multi_f32<16>(W, X, bias, Y, K, N, T);
+    if (sgpu::gemm_nt_ok(W, X, K, T))
+        sgpu::gemm_nt_mfma<1>(W, X, bias, Y, K, N, T);
+    else
+        sgpu::gemv_multi_f32<16>(W, X, bias, Y, K, N, T);
 }
 
 // y = (x - mean) / sqrt(var + eps) * w + b per row (grid = rows), with the two-pass

@@ -350,9 +350,17 @@ static int geometry(const devstate *d, const char *kernel, int M, int N, int K, 
         b[0] = 256;
         return SGPU_OK;
     }
-    if (!strcmp(kernel, "gemv_multi")) {   /* M carries T for this kernel */
-        g[0] = umin(cdiv(N > 0 ? N : 1, 4), cus * 16);
-        g[1] = umin(cdiv(M > 0 ? M : 1, 16), 65535u);
+    if (!strcmp(kernel, "gemv_multi")) {   /* M carries T */
+        /* One block per 32-token x 32-row tile on the matrix-core path; a wave per row (4 per
+         * block, at most 16 blocks per CU) on the vector path.  The kernel takes the matrix
+         * cores for T >= 4 (and T > 8 when K > 1024) on aligned rows (gemm_nt_ok). */
+        if (M >= 4 && !(M <= 8 && K > 1024)) {
+            long long nt = (long long)cdiv(M, 32) * cdiv(N > 0 ? N : 1, 32);
+            g[0] = (unsigned)(nt < 0x7fffffffLL ? nt : 0x7fffffffLL);
+        } else {
+            g[0] = umin(cdiv(N > 0 ? N : 1, 4), cus * 16);
+            g[1] = umin(cdiv(M > 0 ? M : 1, 16), 65535u);
+        }
         b[0] = 256;
         return SGPU_OK;
     }

@@ -118,6 +118,45 @@ def test_gemv_multi(gpu, og, T, with_bias):
     assert np.all(np.abs(Y - ref) <= 1e-4 * np.abs(ref) + 1e-4)
 
 
+# (K, N, T): matrix-core path (32-token x 32-row tiles) with ragged token/row tiles, K tails
+# inside a 32-deep chunk, K shorter than the four-wave split, the GPT-2 shapes, and both
+# sides of the token-count switch to the vector path (T < 4, or T <= 8 with K > 1024).
+MULTI_SHAPES = [(768, 2304, 128), (772, 100, 33), (64, 65, 1), (3072, 768, 64), (40, 1000, 300),
+                (768, 2048, 512), (36, 37, 31), (768, 50257, 3), (4, 7, 5), (3072, 3072, 257),
+                (64, 100, 3), (64, 100, 4), (1028, 40, 8), (1028, 40, 9), (1024, 40, 8)]
+
+
+@pytest.mark.parametrize("K,N,T", MULTI_SHAPES)
+def test_gemv_multi_integer_shapes(gpu, K, N, T):
+    say(f"gemv_multi integer K={K} N={N} T={T}")
+    rng = np.random.default_rng(K * 7 + N * 3 + T)
+    W = rng.integers(-3, 4, (N, K))
+    X = rng.integers(-3, 4, (T, K))
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    dW, dX = gpu.DeviceArray.from_host(W.astype(np.float32)), gpu.DeviceArray.from_host(X.astype(np.float32))
+    db = gpu.DeviceArray.from_host(bias)
+    dY = gpu.DeviceArray((T, N))
+    dY.fill_bytes(0xFF)
+    gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, db.ptr, dY.ptr, K, N, T, None)
+    gpu.synchronize()
+    want = (X @ W.T + bias.astype(np.int64)).astype(np.float32)    # |sum| < 2^24: exact
+    assert np.array_equal(dY.to_host(), want)
+
+
+def test_gemv_multi_unaligned_rows_take_vector_path(gpu):
+    rng = np.random.default_rng(8)
+    K, N, T = 64, 96, 40
+    W = rng.integers(-3, 4, (N, K)).astype(np.float32)
+    X = rng.integers(-3, 4, (T, K)).astype(np.float32)
+    dW = gpu.DeviceArray(N * K + 1)
+    gpu.call("sgpu_memcpy_htod", dW.offset(1), W.ctypes.data, W.nbytes)
+    dX = gpu.DeviceArray.from_host(X)
+    dY = gpu.DeviceArray((T, N))
+    gpu.call("sgpu_gemv_multi", dW.offset(1), dX.ptr, None, dY.ptr, K, N, T, None)
+    gpu.synchronize()
+    assert np.array_equal(dY.to_host(), (X.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32))
+
+
 def test_gemv_multi_integer_ragged(gpu):
     rng = np.random.default_rng(6)
     K, N, T = 37, 29, 21
