@@ -103,7 +103,7 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * sgpu_sgemm_tiled / _tiled4 / _naive launch their own code-object symbol (tiles 64x64,
  * 128x128; one output per thread).  sgpu_sgemm_opt is the tuned entry: it launches the
  * sgemm_opt symbol (128x256 tiles) when that grid gives every CU two blocks, else the
- * 128x128 or 64x64 member, whichever is the largest that does (64x64 at the smallest). */
+ * 128x128 member when its grid gives every CU one block, else the 64x64 member. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);

@@ -401,8 +401,9 @@ int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
 }
-/* The optimised entry picks the largest tile whose grid still gives every CU two blocks
- * (all three run two or more blocks per CU), falling back to the 64x64 member. */
+/* The optimised entry takes the 128x256 member when its grid gives every CU two blocks, the
+ * 128x128 member when its grid gives every CU at least one, else the 64x64 member (measured
+ * at 4096^3 / 2048^3 / 1024^3 respectively). */
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
     if (M == 0 || N == 0) return SGPU_OK;
@@ -413,7 +414,7 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     const long long want = 2LL * d->cus;
     if ((long long)cdiv(M, 128) * cdiv(N, 256) >= want)
         return sgemm_common(K_SGEMM_OPT, "sgemm_opt", A, B, C, M, N, K, stream);
-    if ((long long)cdiv(M, 128) * cdiv(N, 128) >= want)
+    if ((long long)cdiv(M, 128) * cdiv(N, 128) >= d->cus)
         return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
     return sgemm_common(K_SGEMM_TILED, "sgemm_tiled", A, B, C, M, N, K, stream);
 }
