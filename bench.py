@@ -14,6 +14,7 @@ The CPU baseline is the oracle's serial-order SGEMM (row-parallel over the host 
 bounded sample of rows of the same 4096^3 problem.
 """
 import argparse
+import ctypes as ct
 import json
 import os
 import sys
@@ -135,6 +136,31 @@ def bench_decode(prompt_len=32, gen=128, path=sgpu.QWEN_PATH_GRAPH, compare=True
                 prefill_ms=t_prefill * 1e3, host_loop_graph=host_graph, host_loop_reference=host_ref)
 
 
+def bench_gpt2_decode(prompt_len=8, gen=128):
+    """GPT-2 124M (random-init fp32 weights), graph path with the greedy loop on the device:
+    decode tok/s over `gen` positions after the reference's deterministic 8-id prompt."""
+    cfg = sgpu.gpt2_cfg()
+    w = sgpu.gpt2_random_weights(cfg, 42, 0.03)
+    eng = sgpu.Gpt2Engine(cfg, w, sgpu.GPT2_PATH_GRAPH)
+    del w
+    ids = [(i * 7919 + 42) % cfg.V for i in range(prompt_len)]
+    eng.generate(ids, 4)                          # captures the graphs
+    sgpu.synchronize()
+    t0 = time.perf_counter()
+    eng.generate(ids, gen)
+    t_full = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    eng.generate(ids, 0)
+    t_prefill = time.perf_counter() - t0
+    eng.close()
+    dt = t_full - t_prefill
+    bytes_tok = 4 * sgpu.lib().sgpu_gpt2_file_floats(ct.byref(cfg)) - 4 * cfg.CTX * cfg.C   # all weights but wpe
+    tps = gen / dt
+    return dict(tok_s=tps, ms_per_tok=dt / gen * 1e3, bytes_per_token=bytes_tok,
+                hbm_floor_frac=bytes_tok * tps / (PEAK_HBM_GBPS * 1e9), prompt=prompt_len, generated=gen,
+                prefill_ms=t_prefill * 1e3)
+
+
 def cpu_baseline(n, target_s=1.5):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -232,11 +258,14 @@ def main():
     gv = bench_gemv_lm_head()
     log(f"gemv_h lm_head: {gv['us']:.1f} us, {gv['gbps']:.0f} GB/s ({gv['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), "
         f"err {gv['err']:.2e}")
-    dec = None
+    dec = g2 = None
     if not args.no_decode:
         dec = bench_decode()
         log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['ms_per_tok']:.3f} ms/token, "
             f"{dec['hbm_floor_frac']:.1%} of the HBM floor)")
+        g2 = bench_gpt2_decode()
+        log(f"gpt2 decode: {g2['tok_s']:.1f} tok/s ({g2['ms_per_tok']:.3f} ms/token, "
+            f"{g2['hbm_floor_frac']:.1%} of the HBM floor)")
     cpu = None if args.no_cpu else cpu_baseline(n)
     traffic = {}
     if os.path.exists(PROFILE_TRAFFIC):
@@ -276,6 +305,12 @@ def main():
             "prefill_ms": round(dec["prefill_ms"], 3),
             "tok_s_host_argmax_loop": round(dec["host_loop_graph"], 2),
             "tok_s_reference_launch_sequence": round(dec["host_loop_reference"], 2)},
+        "gpt2_decode": None if g2 is None else {
+            "model": "GPT-2 124M architecture, random-init fp32 weights ((frand()-0.5)*0.06)",
+            "tok_s": round(g2["tok_s"], 2), "ms_per_token": round(g2["ms_per_tok"], 4),
+            "prompt": g2["prompt"], "generated": g2["generated"], "bytes_per_token": g2["bytes_per_token"],
+            "hbm_floor_frac": round(g2["hbm_floor_frac"], 4), "prefill_ms": round(g2["prefill_ms"], 3),
+            "path": "fused kernels (5 per layer) replayed as a HIP graph, greedy argmax on the device"},
         "sgemm_normwise_err": sg["err"],
         "device": props.name.decode(),
     }

@@ -199,6 +199,22 @@ int sgpu_gpt2_forward(sgpu_gpt2 *engine, int token, int pos, int want_logits, fl
 /* gpu_prefill (gpt2_engine.c:269-326): all T prompt positions through the layers with the
  * weight-stationary gemv_multi; fills cache positions 0..T-1; logits of the last row. */
 int sgpu_gpt2_prefill(sgpu_gpt2 *engine, const int *ids, int T, float *logits_host);
+/* Execution paths of sgpu_gpt2_forward / sgpu_gpt2_generate (same arithmetic, results within
+ * fp32 reordering of each other):
+ *  REFERENCE -- the gpu_forward launch sequence above (its `fused` flag chooses gemv_warp_b)
+ *  FUSED     -- five kernels per layer: LayerNorm+qkv+bias+KV-cache write, attention,
+ *               o+bias+residual, LayerNorm+fc+bias+GELU, proj+bias+residual (`fused` ignored)
+ *  GRAPH     -- FUSED with the layer stack captured once as a HIP graph and replayed
+ * No counterpart in the reference beyond the sequence it restates. */
+#define SGPU_GPT2_PATH_REFERENCE 0
+#define SGPU_GPT2_PATH_FUSED 1
+#define SGPU_GPT2_PATH_GRAPH 2
+int sgpu_gpt2_set_path(sgpu_gpt2 *engine, int path);
+/* Greedy decode (the reference generation loop, gpt2_engine.c:551-562, without its EOT stop):
+ * prime with prompt[0..T-1], then n_gen more positions; out_tokens receives n_gen + 1 ids, the
+ * argmax (first max) after the prompt and after each generated position.  FUSED/GRAPH keep
+ * the argmax and the next embedding on the device. */
+int sgpu_gpt2_generate(sgpu_gpt2 *engine, const int *prompt, int T, int n_gen, int *out_tokens);
 
 /* ---- Qwen2.5 decode engine (qwen_engine.c:105-269): weights resident on the device,
  * fp32 KV cache, the reference's per-layer launch sequence per position. ---- */

@@ -218,6 +218,52 @@ struct XRms {
     }
 };
 
+// x'[k] = (x[k] - mean) * inv * w[k] + b[k], the two-pass mean/variance LayerNorm of the
+// GPT-2 CPU golden (gpt2_engine.c:333-341) with the same operation order.  As with XRms the
+// team's lanes hold all K values, so both passes are team reductions over registers.
+struct XLn {
+    const float* x;
+    const float* w;
+    const float* b;
+    float eps;
+    float mean;
+    float inv;
+    __device__ __forceinline__ sgpu_f32x4 load4(int k) const { return *reinterpret_cast<const sgpu_f32x4*>(x + k); }
+    __device__ __forceinline__ float at(int k) const {
+#pragma clang fp contract(off)
+        return (x[k] - mean) * inv * w[k] + b[k];
+    }
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const bool (&has)[S], int sub, int K, float* red) {
+#pragma clang fp contract(off)
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; j++)
+#pragma unroll
+            for (int e = 0; e < VEC; e++) s += xr[j][e];             // zero where !has
+        mean = team_sum_bcast<LPR>(s, red) / (float)K;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            if (!has[j]) continue;
+#pragma unroll
+            for (int e = 0; e < VEC; e++) {
+                const float d = xr[j][e] - mean;
+                q += d * d;
+            }
+        }
+        const float var = team_sum_bcast<LPR>(q, red) / (float)K;
+        inv = 1.0f / __builtin_sqrtf(var + eps);
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            if (!has[j]) continue;
+            const int k0 = (sub + LPR * j) * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; e++) xr[j][e] = (xr[j][e] - mean) * inv * w[k0 + e] + b[k0 + e];
+        }
+    }
+};
+
 struct MapRows {
     __device__ __forceinline__ int row(int t, int) const { return t; }
 };

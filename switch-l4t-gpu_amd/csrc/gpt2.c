@@ -14,6 +14,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "sgpu_internal.h"
 #include "switch_gpu.h"
 
 typedef struct {
@@ -65,18 +66,33 @@ int sgpu_gpt2_fill_random(float *blob, const sgpu_gpt2_cfg *c, uint64_t seed, fl
 struct sgpu_gpt2 {
     sgpu_gpt2_cfg cfg;
     g2layout L;
+    int path;                                       /* SGPU_GPT2_PATH_* */
     hipStream_t stream;
     float *w;                                       /* the whole weight file on the device */
     float **kc, **vc;
     float *x, *ln1, *qkv, *att, *y, *ln2, *fc, *scores, *probs, *logits, *x2;
     float *xT, *ln1T, *qkvT, *attT, *yT, *ln2T, *fcT;     /* batched prefill */
+    float *d_q;                                     /* q of the fused path */
+    int *d_step;                                    /* {token, pos} read by the fused kernels */
+    int *d_tokens;                                  /* CTX + 1 greedy ids, by position */
+    float *d_amax_v;                                /* argmax partials */
+    int *d_amax_i;
+    hipGraph_t g_layers, g_step;
+    hipGraphExec_t ge_layers, ge_step;
 };
 
 void sgpu_gpt2_destroy(sgpu_gpt2 *e) {
     if (!e) return;
     float *bufs[] = {e->w, e->x, e->ln1, e->qkv, e->att, e->y, e->ln2, e->fc, e->scores, e->probs, e->logits,
-                     e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT};
+                     e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT, e->d_q, e->d_amax_v};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) sgpu_free(bufs[i]);
+    sgpu_free(e->d_step);
+    sgpu_free(e->d_tokens);
+    sgpu_free(e->d_amax_i);
+    if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
+    if (e->g_layers) hipGraphDestroy(e->g_layers);
+    if (e->ge_step) hipGraphExecDestroy(e->ge_step);
+    if (e->g_step) hipGraphDestroy(e->g_step);
     for (int l = 0; l < e->cfg.NL; l++) {
         if (e->kc) sgpu_free(e->kc[l]);
         if (e->vc) sgpu_free(e->vc[l]);
@@ -121,6 +137,12 @@ int sgpu_gpt2_create(sgpu_gpt2 **out, const sgpu_gpt2_cfg *c, const float *blob)
     TRY(zalloc(&e->xT, CTX * C)); TRY(zalloc(&e->ln1T, CTX * C)); TRY(zalloc(&e->qkvT, CTX * 3 * C));
     TRY(zalloc(&e->attT, CTX * C)); TRY(zalloc(&e->yT, CTX * C)); TRY(zalloc(&e->ln2T, CTX * C));
     TRY(zalloc(&e->fcT, CTX * FC));
+    TRY(zalloc(&e->d_q, C));
+    TRY(zalloc(&e->d_amax_v, SGPU_ARGMAX_PARTS));
+    TRY(sgpu_malloc((void **)&e->d_amax_i, SGPU_ARGMAX_PARTS * sizeof(int)));
+    TRY(sgpu_malloc((void **)&e->d_step, 4 * sizeof(int)));
+    TRY(sgpu_memset_d8(e->d_step, 0, 4 * sizeof(int)));
+    TRY(sgpu_malloc((void **)&e->d_tokens, (CTX + 1) * sizeof(int)));
 #undef TRY
     *out = e;
     return SGPU_OK;
@@ -151,8 +173,103 @@ static int proj(const float *W, const float *x, const float *b, float *y, int K,
     return rc ? rc : sgpu_add_bias(y, b, N, s);
 }
 
+/* ---- fused path: five kernels per layer (sgpu_decode.hip g2 families) ----
+ * LayerNorm + qkv + bias + K/V cache write; attention (one block per head); o + bias +
+ * residual; LayerNorm + fc + bias + GELU; proj + bias + residual.  Same arithmetic as the
+ * reference sequence below, grouped so each kernel streams one weight matrix. */
+static int fused_layers(sgpu_gpt2 *e) {
+    const sgpu_gpt2_cfg *c = &e->cfg;
+    const int C = c->C, FC = c->FC;
+    const float eps = c->eps;
+    void *s = (void *)e->stream;
+    const float *W = e->w;
+    int rc;
+#define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+    for (int l = 0; l < c->NL; l++) {
+        const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
+        TRY(sgpu_internal_g2_qkv(b + e->L.qkvw, C, 3 * C, e->x, b + e->L.ln1w, b + e->L.ln1b, eps, b + e->L.qkvb,
+                                 e->d_q, e->kc[l], e->vc[l], e->d_step, s));
+        TRY(sgpu_internal_dec_attn(e->d_q, e->kc[l], e->vc[l], e->att, e->d_step, c->NH, c->NH, c->HD, 0.125f, s));
+        TRY(sgpu_internal_g2_res(b + e->L.aow, C, C, e->att, b + e->L.aob, e->x, s));
+        TRY(sgpu_internal_g2_fc(b + e->L.fcw, C, FC, e->x, b + e->L.ln2w, b + e->L.ln2b, eps, b + e->L.fcb, e->fc, s));
+        TRY(sgpu_internal_g2_res(b + e->L.projw, FC, C, e->fc, b + e->L.projb, e->x, s));
+    }
+#undef TRY
+    return SGPU_OK;
+}
+
+static int fused_lm_head(sgpu_gpt2 *e) {
+    const float *W = e->w;
+    return sgpu_internal_g2_lmhead(W + e->L.wte, e->cfg.C, e->cfg.V, e->x, W + e->L.lnfw, W + e->L.lnfb, e->cfg.eps,
+                                   e->logits, (void *)e->stream);
+}
+
+/* One greedy step on the device: token from step[0], pos = step[1] + 1. */
+static int device_step(sgpu_gpt2 *e) {
+    const float *W = e->w;
+    int rc = sgpu_internal_g2_embed_next(W + e->L.wte, W + e->L.wpe, e->x, e->cfg.C, e->d_step, (void *)e->stream);
+    if (!rc) rc = fused_layers(e);
+    if (!rc) rc = fused_lm_head(e);
+    if (!rc)
+        rc = sgpu_internal_dec_argmax(e->logits, e->cfg.V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
+                                      (void *)e->stream);
+    return rc;
+}
+
+static int capture(sgpu_gpt2 *e, int (*fn)(sgpu_gpt2 *), hipGraph_t *g, hipGraphExec_t *ge) {
+    hipError_t he = hipStreamBeginCapture(e->stream, hipStreamCaptureModeRelaxed);
+    if (he != hipSuccess) return (int)he;
+    int rc = fn(e);
+    hipGraph_t graph = NULL;
+    he = hipStreamEndCapture(e->stream, &graph);
+    if (rc || he != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return rc ? rc : (int)he;
+    }
+    he = hipGraphInstantiate(ge, graph, NULL, NULL, 0);
+    if (he != hipSuccess) {
+        hipGraphDestroy(graph);
+        return (int)he;
+    }
+    *g = graph;
+    return SGPU_OK;
+}
+
+static int run_layers(sgpu_gpt2 *e) {
+    if (e->path != SGPU_GPT2_PATH_GRAPH) return fused_layers(e);
+    if (!e->ge_layers) {
+        int rc = capture(e, fused_layers, &e->g_layers, &e->ge_layers);
+        if (rc) return rc;
+    }
+    hipError_t he = hipGraphLaunch(e->ge_layers, e->stream);
+    return he == hipSuccess ? SGPU_OK : (int)he;
+}
+
+int sgpu_gpt2_set_path(sgpu_gpt2 *e, int path) {
+    if (!e || path < SGPU_GPT2_PATH_REFERENCE || path > SGPU_GPT2_PATH_GRAPH) return SGPU_ERR_INVALID_ARG;
+    e->path = path;
+    return SGPU_OK;
+}
+
+static int forward_fused(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host) {
+    const float *W = e->w;
+    int rc = sgpu_internal_g2_embed(W + e->L.wte, W + e->L.wpe, token, pos, e->x, e->cfg.C, e->d_step,
+                                    (void *)e->stream);
+    if (!rc) rc = run_layers(e);
+    if (rc || !want_logits) return rc;
+    if ((rc = fused_lm_head(e))) return rc;
+    if (!logits_host) return SGPU_OK;
+    hipError_t he = hipMemcpyAsync(logits_host, e->logits, (size_t)e->cfg.V * 4, hipMemcpyDeviceToHost, e->stream);
+    if (he != hipSuccess) return (int)he;
+    return sgpu_stream_synchronize((void *)e->stream);
+}
+
 int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host, int fused) {
     if (!e) return SGPU_ERR_INVALID_ARG;
+    if (e->path != SGPU_GPT2_PATH_REFERENCE) {
+        if (token < 0 || token >= e->cfg.V || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
+        return forward_fused(e, token, pos, want_logits, logits_host);
+    }
     const sgpu_gpt2_cfg *c = &e->cfg;
     if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
     const int C = c->C, FC = c->FC, T = pos + 1;
@@ -220,4 +337,46 @@ int sgpu_gpt2_prefill(sgpu_gpt2 *e, const int *ids, int T, float *logits_host) {
     }
 #undef TRY
     return logits_out(e, e->xT + (size_t)(T - 1) * C, logits_host);
+}
+
+int sgpu_gpt2_generate(sgpu_gpt2 *e, const int *prompt, int T, int n_gen, int *out_tokens) {
+    if (!e || !prompt || !out_tokens || T <= 0 || n_gen < 0) return SGPU_ERR_INVALID_ARG;
+    const sgpu_gpt2_cfg *c = &e->cfg;
+    if ((long long)T + n_gen > c->CTX) return SGPU_ERR_INVALID_ARG;
+    for (int p = 0; p < T; p++)
+        if (prompt[p] < 0 || prompt[p] >= c->V) return SGPU_ERR_INVALID_ARG;
+    int rc = SGPU_OK;
+    if (e->path == SGPU_GPT2_PATH_REFERENCE) {       /* host-driven loop, the reference's own */
+        float *logits = malloc(sizeof(float) * (size_t)c->V);
+        if (!logits) return SGPU_ERR_HOST_ALLOC;
+        for (int p = 0; p < T && !(rc = sgpu_gpt2_forward(e, prompt[p], p, p == T - 1, logits, 0)); p++) {
+        }
+        for (int g = 0; !rc && g <= n_gen; g++) {
+            int b = 0;
+            for (int i = 1; i < c->V; i++)
+                if (logits[i] > logits[b]) b = i;
+            out_tokens[g] = b;
+            if (g < n_gen) rc = sgpu_gpt2_forward(e, b, T + g, 1, logits, 0);
+        }
+        free(logits);
+        return rc;
+    }
+    for (int p = 0; p < T; p++)
+        if ((rc = forward_fused(e, prompt[p], p, p == T - 1, NULL))) return rc;
+    if ((rc = sgpu_internal_dec_argmax(e->logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
+                                       (void *)e->stream)))
+        return rc;
+    for (int g = 0; g < n_gen; g++) {
+        if (e->path == SGPU_GPT2_PATH_GRAPH) {
+            if (!e->ge_step && (rc = capture(e, device_step, &e->g_step, &e->ge_step))) return rc;
+            hipError_t he = hipGraphLaunch(e->ge_step, e->stream);
+            if (he != hipSuccess) return (int)he;
+        } else if ((rc = device_step(e))) {
+            return rc;
+        }
+    }
+    hipError_t he = hipMemcpyAsync(out_tokens, e->d_tokens + T, ((size_t)n_gen + 1) * sizeof(int),
+                                   hipMemcpyDeviceToHost, e->stream);
+    if (he != hipSuccess) return (int)he;
+    return sgpu_stream_synchronize((void *)e->stream);
 }

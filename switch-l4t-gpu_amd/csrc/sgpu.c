@@ -78,8 +78,12 @@ static const int g_dec_cfg[][2] = {{16, 1}, {16, 2}, {16, 4}, {16, 7}, {16, 8}, 
                                    {64, 8}, {256, 1}, {256, 2}, {256, 3}, {256, 4}, {256, 8}};
 #define NDEC_PAIR 9      /* the first 9 entries: teams of up to one wave (two-row families) */
 #define NDEC_ALL 14
-enum { DEC_QKV, DEC_GATEUP, DEC_RES, DEC_LMHEAD, NDECFAM };
-static const char *g_dec_fam[NDECFAM] = {"qkv", "gateup", "res", "lmhead"};
+enum { DEC_QKV, DEC_GATEUP, DEC_RES, DEC_LMHEAD, DEC_G2QKV, DEC_G2RES, DEC_G2FC, DEC_G2LMHEAD, NDECFAM };
+static const char *g_dec_fam[NDECFAM] = {"qkv", "gateup", "res", "lmhead", "g2qkv", "g2res", "g2fc", "g2lmhead"};
+/* Two-row (pair) families use the first NDEC_PAIR configurations; weights per 16-byte
+ * segment: 8 fp16 (Qwen families) or 4 fp32 (GPT-2 families). */
+static int dec_is_pair(int f) { return f == DEC_QKV || f == DEC_GATEUP; }
+static int dec_vec(int f) { return f >= DEC_G2QKV ? 4 : 8; }
 
 typedef struct {
     int ready;
@@ -89,6 +93,7 @@ typedef struct {
     hipFunction_t gemv_f32[NLPR][NSEG], gemv_h[NLPR][NSEG];
     hipFunction_t dec[NDECFAM][NDEC_ALL];
     hipFunction_t dec_attn[3], dec_embed, dec_embed_next, dec_argmax_part, dec_argmax_final;
+    hipFunction_t dec_g2embed, dec_g2embed_next;
 } devstate;
 
 static devstate g_dev[SGPU_MAX_DEVICES];
@@ -143,7 +148,7 @@ static int load_device(int dev) {
             if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
         }
     for (int f = 0; f < NDECFAM; f++) {
-        int n = (f == DEC_QKV || f == DEC_GATEUP) ? NDEC_PAIR : NDEC_ALL;
+        int n = dec_is_pair(f) ? NDEC_PAIR : NDEC_ALL;
         for (int j = 0; j < n; j++) {
             char name[64];
             snprintf(name, sizeof name, "sgpu_dec_%s_l%d_s%d", g_dec_fam[f], g_dec_cfg[j][0], g_dec_cfg[j][1]);
@@ -161,7 +166,9 @@ static int load_device(int dev) {
         if (hipModuleGetFunction(&d->dec_embed, d->mod[MOD_DECODE], "sgpu_dec_embed") != hipSuccess ||
             hipModuleGetFunction(&d->dec_embed_next, d->mod[MOD_DECODE], "sgpu_dec_embed_next") != hipSuccess ||
             hipModuleGetFunction(&d->dec_argmax_part, d->mod[MOD_DECODE], "sgpu_dec_argmax_part") != hipSuccess ||
-            hipModuleGetFunction(&d->dec_argmax_final, d->mod[MOD_DECODE], "sgpu_dec_argmax_final") != hipSuccess) {
+            hipModuleGetFunction(&d->dec_argmax_final, d->mod[MOD_DECODE], "sgpu_dec_argmax_final") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_g2embed, d->mod[MOD_DECODE], "sgpu_dec_g2embed") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_g2embed_next, d->mod[MOD_DECODE], "sgpu_dec_g2embed_next") != hipSuccess) {
             rc = SGPU_ERR_NO_KERNEL;
             goto out;
         }
@@ -796,9 +803,9 @@ int sgpu_internal_embed_h(const uint16_t *emb, int token, float *x, int C, void 
 /* ---- fused decode kernels (sgpu_decode.hip) ---- */
 /* Pick a (team, segments) instance for K columns and nteams teams: the smallest team that
  * still gives >= 8 waves per CU, else the largest that fits; -1 if none fits. */
-static int dec_pick(const devstate *d, int K, int nteams, int n_entries) {
-    if (K <= 0 || K % 8 || nteams <= 0) return -1;
-    const long long nseg = K / 8, want = 8LL * d->cus;
+static int dec_pick(const devstate *d, int K, int nteams, int n_entries, int vec) {
+    if (K <= 0 || K % vec || nteams <= 0) return -1;
+    const long long nseg = K / vec, want = 8LL * d->cus;
     int best = -1, best_lpr = 0;
     const int lprs[3] = {16, 64, 256};
     for (int li = 0; li < 3; li++) {
@@ -816,8 +823,8 @@ static int dec_pick(const devstate *d, int K, int nteams, int n_entries) {
 }
 
 static int dec_launch_team(devstate *d, int fam, int K, int nteams, void **args, void *stream) {
-    const int n_entries = (fam == DEC_QKV || fam == DEC_GATEUP) ? NDEC_PAIR : NDEC_ALL;
-    const int j = dec_pick(d, K, nteams, n_entries);
+    const int n_entries = dec_is_pair(fam) ? NDEC_PAIR : NDEC_ALL;
+    const int j = dec_pick(d, K, nteams, n_entries, dec_vec(fam));
     if (j < 0) return SGPU_ERR_INVALID_ARG;
     const unsigned teams = 256u / (unsigned)g_dec_cfg[j][0];
     unsigned g[3] = {umin(cdiv(nteams, teams), (unsigned)d->cus * 8u), 1, 1}, b[3] = {256, 1, 1};
@@ -907,4 +914,64 @@ int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, 
     unsigned g2[3] = {1, 1, 1};
     void *a2[] = {(void *)&part_v, (void *)&part_i, &np, (void *)&step, (void *)&out};
     return launch(d->dec_argmax_final, g2, b, stream, a2);
+}
+
+/* ---- GPT-2 fused decode (sgpu_decode.hip, fp32 weights) ---- */
+int sgpu_internal_g2_qkv(const float *W, int K, int N, const float *x, const float *lnw, const float *lnb, float eps,
+                         const float *bias, float *q, float *kc, float *vc, const int *step, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    if (N != 3 * K || ((uintptr_t)W & 15) || ((uintptr_t)x & 15)) return SGPU_ERR_INVALID_ARG;
+    void *args[] = {(void *)&W, &K, &N, (void *)&x, (void *)&lnw, (void *)&lnb, &eps, (void *)&bias,
+                    (void *)&q, (void *)&kc, (void *)&vc, (void *)&step};
+    return dec_launch_team(d, DEC_G2QKV, K, N, args, stream);
+}
+
+int sgpu_internal_g2_res(const float *W, int K, int N, const float *a, const float *bias, float *x, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    if (((uintptr_t)W & 15) || ((uintptr_t)a & 15)) return SGPU_ERR_INVALID_ARG;
+    void *args[] = {(void *)&W, &K, &N, (void *)&a, (void *)&bias, (void *)&x};
+    return dec_launch_team(d, DEC_G2RES, K, N, args, stream);
+}
+
+int sgpu_internal_g2_fc(const float *W, int K, int N, const float *x, const float *lnw, const float *lnb, float eps,
+                        const float *bias, float *y, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    if (((uintptr_t)W & 15) || ((uintptr_t)x & 15)) return SGPU_ERR_INVALID_ARG;
+    void *args[] = {(void *)&W, &K, &N, (void *)&x, (void *)&lnw, (void *)&lnb, &eps, (void *)&bias, (void *)&y};
+    return dec_launch_team(d, DEC_G2FC, K, N, args, stream);
+}
+
+int sgpu_internal_g2_lmhead(const float *W, int K, int N, const float *x, const float *lnw, const float *lnb,
+                            float eps, float *y, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    if (((uintptr_t)W & 15) || ((uintptr_t)x & 15)) return SGPU_ERR_INVALID_ARG;
+    void *args[] = {(void *)&W, &K, &N, (void *)&x, (void *)&lnw, (void *)&lnb, &eps, (void *)&y};
+    return dec_launch_team(d, DEC_G2LMHEAD, K, N, args, stream);
+}
+
+int sgpu_internal_g2_embed(const float *wte, const float *wpe, int token, int pos, float *x, int C, int *step,
+                           void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid(C), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&wte, (void *)&wpe, &token, &pos, (void *)&x, &C, (void *)&step};
+    return launch(d->dec_g2embed, g, b, stream, args);
+}
+
+int sgpu_internal_g2_embed_next(const float *wte, const float *wpe, float *x, int C, int *step, void *stream) {
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {1, 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&wte, (void *)&wpe, (void *)&x, &C, (void *)&step};
+    return launch(d->dec_g2embed_next, g, b, stream, args);
 }

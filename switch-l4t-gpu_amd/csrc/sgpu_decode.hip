@@ -11,6 +11,8 @@
 //   sgpu_dec_lmhead_* final RMSNorm -> tied lm_head GEMV
 //   sgpu_dec_embed    token embedding (h2f) and the step record {token, pos} for the layers
 //   sgpu_dec_argmax_* first-max argmax of the logits into the step record (greedy decode)
+//   sgpu_dec_g2*      the GPT-2 (fp32) counterparts: LayerNorm+qkv+bias+KV write, GEMV+bias+
+//                     residual, LayerNorm+fc+bias+GELU, LayerNorm+lm_head, wte+wpe embedding
 // The position lives in device memory (`step`), so a whole position can be captured once as
 // a HIP graph and replayed.  Weight rows are fp16 bits with the reference h2f contract (see
 // gemv_core.h); this code object is built with the fp16 denormal mode set to flush.
@@ -68,6 +70,39 @@ struct EpiQkvRope {
             dst[i] = a;
             dst[i + h2] = b;
         }
+    }
+};
+
+// GPT-2 qkv epilogue: row r of the fused [3C x C] projection plus its bias goes to q (rows
+// 0..C-1) or to the layer's K / V cache row of `pos` (rows C..2C-1 / 2C..3C-1): the
+// reference's add_bias and its two cache copies (gpt2_engine.c:184-196).
+struct EpiG2Qkv {
+    const float* bias;
+    float* q;
+    float* kc;
+    float* vc;
+    const int* step;
+    int C;
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
+        const int r = rows[0], pos = step[1];
+        const float v = acc[0] + bias[r];
+        if (r < C) q[r] = v;
+        else if (r < 2 * C) kc[(size_t)pos * C + (r - C)] = v;
+        else vc[(size_t)pos * C + (r - 2 * C)] = v;
+    }
+};
+
+// y[r] = gelu(acc + bias[r]), the tanh form of the reference gelu kernel
+// (gpt2_kernels.cu:199-206) with the arithmetic of this build's gelu.
+struct EpiBiasGelu {
+    const float* bias;
+    float* y;
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
+#pragma clang fp contract(off)
+        const int r = rows[0];
+        const float v = acc[0] + bias[r];
+        const float t = 0.7978845608f * (v + 0.044715f * v * v * v);
+        y[r] = 0.5f * v * (1.0f + tanhf(t));
     }
 };
 
@@ -172,6 +207,7 @@ __device__ __forceinline__ void amax_block256(float& bv, int& bi, float* sv, int
 }  // namespace
 
 using sgpu::WF16;
+using sgpu::WF32;
 
 extern "C" {
 
@@ -196,6 +232,34 @@ __global__ void __launch_bounds__(256) sgpu_dec_embed_next(const uint16_t* __res
     for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = sgpu_h2f(emb[(size_t)tok * C + i]);
     __syncthreads();
     if (threadIdx.x == 0) step[1] = step[1] + 1;
+}
+
+// GPT-2: x = wte[token] + wpe[pos] (fp32; the reference adds on the host,
+// gpt2_engine.c:176-179); step = {token, pos}.
+__global__ void sgpu_dec_g2embed(const float* __restrict__ wte, const float* __restrict__ wpe, int token, int pos,
+                                 float* __restrict__ x, int C, int* __restrict__ step) {
+#pragma clang fp contract(off)
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        step[0] = token;
+        step[1] = pos;
+    }
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < C; i += gridDim.x * blockDim.x)
+        x[i] = wte[(size_t)token * C + i] + wpe[(size_t)pos * C + i];
+}
+
+// Same, with the token from step[0] and pos = step[1] + 1 (one block).
+__global__ void __launch_bounds__(256) sgpu_dec_g2embed_next(const float* __restrict__ wte, const float* __restrict__ wpe,
+                                                             float* __restrict__ x, int C, int* __restrict__ step) {
+#pragma clang fp contract(off)
+    __shared__ int tok, pos;
+    if (threadIdx.x == 0) {
+        tok = step[0];
+        pos = step[1] + 1;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = wte[(size_t)tok * C + i] + wpe[(size_t)pos * C + i];
+    __syncthreads();
+    if (threadIdx.x == 0) step[1] = pos;
 }
 
 // First-max argmax over n logits (qwen_engine.c:360-364 tie rule), stage 1: each of the
@@ -279,6 +343,37 @@ __global__ void __launch_bounds__(256) sgpu_dec_attn128(const float* __restrict_
                                          sgpu::EpiStore{nullptr, y});                                          \
     }
 
+// GPT-2 (fp32 weights): LayerNorm + qkv + bias + KV-cache write; GEMV + bias + residual
+// (attention output and MLP projections); LayerNorm + fc + bias + GELU; LayerNorm + tied
+// lm_head.
+#define SGPU_DEC_G2QKV(LPR, S)                                                                                 \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_g2qkv_l##LPR##_s##S(                            \
+        const float* __restrict__ W, int K, int N, const float* __restrict__ x, const float* __restrict__ lnw, \
+        const float* __restrict__ lnb, float eps, const float* __restrict__ bias, float* q, float* kc, float* vc, \
+        const int* __restrict__ step) {                                                                        \
+        sgpu::gemv_team<WF32, LPR, S, 1>(W, K, N, sgpu::XLn{x, lnw, lnb, eps, 0.0f, 0.0f}, sgpu::MapRows{},    \
+                                         EpiG2Qkv{bias, q, kc, vc, step, K});                                 \
+    }
+#define SGPU_DEC_G2RES(LPR, S)                                                                                 \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_g2res_l##LPR##_s##S(                            \
+        const float* __restrict__ W, int K, int N, const float* __restrict__ a, const float* bias, float* x) {  \
+        sgpu::gemv_team<WF32, LPR, S, 1>(W, K, N, sgpu::XPlain{a}, sgpu::MapRows{}, EpiResidual{x, bias, x});  \
+    }
+#define SGPU_DEC_G2FC(LPR, S)                                                                                  \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_g2fc_l##LPR##_s##S(                             \
+        const float* __restrict__ W, int K, int N, const float* __restrict__ x, const float* __restrict__ lnw, \
+        const float* __restrict__ lnb, float eps, const float* __restrict__ bias, float* __restrict__ y) {     \
+        sgpu::gemv_team<WF32, LPR, S, 1>(W, K, N, sgpu::XLn{x, lnw, lnb, eps, 0.0f, 0.0f}, sgpu::MapRows{},    \
+                                         EpiBiasGelu{bias, y});                                                \
+    }
+#define SGPU_DEC_G2LMHEAD(LPR, S)                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_dec_g2lmhead_l##LPR##_s##S(                         \
+        const float* __restrict__ W, int K, int N, const float* __restrict__ x, const float* __restrict__ lnw, \
+        const float* __restrict__ lnb, float eps, float* __restrict__ y) {                                     \
+        sgpu::gemv_team<WF32, LPR, S, 1>(W, K, N, sgpu::XLn{x, lnw, lnb, eps, 0.0f, 0.0f}, sgpu::MapRows{},    \
+                                         sgpu::EpiStore{nullptr, y});                                          \
+    }
+
 #define SGPU_DEC_PAIRS(F) F(16, 1) F(16, 2) F(16, 4) F(16, 7) F(16, 8) F(64, 1) F(64, 2) F(64, 4) F(64, 8)
 #define SGPU_DEC_SINGLE(F) SGPU_DEC_PAIRS(F) F(256, 1) F(256, 2) F(256, 3) F(256, 4) F(256, 8)
 
@@ -286,3 +381,7 @@ SGPU_DEC_PAIRS(SGPU_DEC_QKV)
 SGPU_DEC_PAIRS(SGPU_DEC_GATEUP)
 SGPU_DEC_SINGLE(SGPU_DEC_RES)
 SGPU_DEC_SINGLE(SGPU_DEC_LMHEAD)
+SGPU_DEC_SINGLE(SGPU_DEC_G2QKV)
+SGPU_DEC_SINGLE(SGPU_DEC_G2RES)
+SGPU_DEC_SINGLE(SGPU_DEC_G2FC)
+SGPU_DEC_SINGLE(SGPU_DEC_G2LMHEAD)

@@ -27,4 +27,18 @@ SGPU_HIDDEN int sgpu_internal_dec_embed_next(const uint16_t *emb, float *x, int 
 #define SGPU_ARGMAX_PARTS 256
 SGPU_HIDDEN int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
                                          void *stream);
+/* GPT-2 fused decode (fp32 weights), see gpt2.c. */
+SGPU_HIDDEN int sgpu_internal_g2_qkv(const float *W, int K, int N, const float *x, const float *lnw,
+                                     const float *lnb, float eps, const float *bias, float *q, float *kc,
+                                     float *vc, const int *step, void *stream);
+SGPU_HIDDEN int sgpu_internal_g2_res(const float *W, int K, int N, const float *a, const float *bias, float *x,
+                                     void *stream);
+SGPU_HIDDEN int sgpu_internal_g2_fc(const float *W, int K, int N, const float *x, const float *lnw,
+                                    const float *lnb, float eps, const float *bias, float *y, void *stream);
+SGPU_HIDDEN int sgpu_internal_g2_lmhead(const float *W, int K, int N, const float *x, const float *lnw,
+                                        const float *lnb, float eps, float *y, void *stream);
+SGPU_HIDDEN int sgpu_internal_g2_embed(const float *wte, const float *wpe, int token, int pos, float *x, int C,
+                                       int *step, void *stream);
+SGPU_HIDDEN int sgpu_internal_g2_embed_next(const float *wte, const float *wpe, float *x, int C, int *step,
+                                            void *stream);
 #endif

@@ -99,6 +99,8 @@ _SIGS = {
     "sgpu_gpt2_destroy": (None, [_P]),
     "sgpu_gpt2_forward": (_I, [_P, _I, _I, _I, _P, _I]),
     "sgpu_gpt2_prefill": (_I, [_P, _P, _I, _P]),
+    "sgpu_gpt2_set_path": (_I, [_P, _I]),
+    "sgpu_gpt2_generate": (_I, [_P, _P, _I, _I, _P]),
     "sgpu_qwen_default_cfg": (None, [ct.POINTER(QwenCfg)]),
     "sgpu_qwen_file_bytes": (_S, [ct.POINTER(QwenCfg)]),
     "sgpu_qwen_fill_random": (_I, [_P, ct.POINTER(QwenCfg), ct.c_uint64, _F]),
@@ -355,15 +357,29 @@ def gpt2_random_weights(cfg: Gpt2Cfg, seed: int, amp: float = 0.03) -> np.ndarra
     return w
 
 
+GPT2_PATH_REFERENCE, GPT2_PATH_FUSED, GPT2_PATH_GRAPH = 0, 1, 2
+
+
 class Gpt2Engine:
     """sgpu_gpt2_* engine: fp32 weights resident on the device."""
 
-    def __init__(self, cfg: Gpt2Cfg, weights: np.ndarray):
+    def __init__(self, cfg: Gpt2Cfg, weights: np.ndarray, path: int = GPT2_PATH_REFERENCE):
         self.cfg = cfg
         h = ct.c_void_p()
         call("sgpu_gpt2_create", ct.byref(h), ct.byref(cfg), np.ascontiguousarray(weights, np.float32).ctypes.data)
         self.h = h.value
         self.logits = np.empty(cfg.V, np.float32)
+        call("sgpu_gpt2_set_path", self.h, path)
+
+    def set_path(self, path: int) -> None:
+        call("sgpu_gpt2_set_path", self.h, path)
+
+    def generate(self, prompt, n_gen: int) -> np.ndarray:
+        """Greedy ids: the argmax after the prompt and after each of n_gen generated positions."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_gen + 1, np.int32)
+        call("sgpu_gpt2_generate", self.h, p.ctypes.data, p.size, n_gen, out.ctypes.data)
+        return out
 
     def forward(self, token: int, pos: int, want_logits: bool = True, fused: bool = False):
         call("sgpu_gpt2_forward", self.h, token, pos, int(want_logits),

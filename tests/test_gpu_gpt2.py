@@ -94,11 +94,18 @@ def test_attention(gpu, T):
     assert np.allclose(dout.to_host(), out, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_engine_small_teacher_forced(gpu, og, fused):
+PATHS = {"reference": 0, "reference-fused": 0, "fused": 1, "graph": 2}
+
+
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_engine_small_teacher_forced(gpu, og, path):
+    """Every position's logits against the CPU golden for each launch structure: the
+    reference sequence (plain and --fused), five fused kernels per layer, and those replayed
+    as one captured graph (position in device memory)."""
     cfg = SMALL
+    fused = path == "reference-fused"
     w = unit_gain_weights(gpu, cfg, 23)
-    eng = gpu.Gpt2Engine(gpu.gpt2_cfg(**cfg), w)
+    eng = gpu.Gpt2Engine(gpu.gpt2_cfg(**cfg), w, PATHS[path])
     gold = og.Gpt2Golden(og.gpt2_cfg(**cfg), w, NT)
     ids = [int(v) for v in np.random.default_rng(7).integers(0, cfg["V"], 30)]
     for p, t in enumerate(ids):
@@ -107,6 +114,45 @@ def test_engine_small_teacher_forced(gpu, og, fused):
         scale = np.abs(want).max()
         assert np.abs(got - want).max() <= 1e-4 * scale, (p, np.abs(got - want).max(), scale)
         assert int(np.argmax(got)) == og.argmax(want)
+    eng.close()
+
+
+@pytest.mark.parametrize("path", ["reference", "fused", "graph"])
+def test_engine_small_generate(gpu, og, path):
+    """sgpu_gpt2_generate (device-side argmax and embedding on the fused/graph paths) gives the
+    CPU golden's greedy ids, and a second call restarts at position 0."""
+    cfg = SMALL
+    w = unit_gain_weights(gpu, cfg, 31)
+    eng = gpu.Gpt2Engine(gpu.gpt2_cfg(**cfg), w, PATHS[path])
+    prompt = [int(v) for v in np.random.default_rng(9).integers(0, cfg["V"], 7)]
+    got = eng.generate(prompt, 16)
+    gold = og.Gpt2Golden(og.gpt2_cfg(**cfg), w, NT)
+    for p, t in enumerate(prompt):
+        ref = gold.forward(t, p, p == len(prompt) - 1)
+    want = [og.argmax(ref)]
+    for g in range(16):
+        ref = gold.forward(want[-1], len(prompt) + g)
+        want.append(og.argmax(ref))
+    assert got.tolist() == want
+    assert eng.generate(prompt, 16).tolist() == want
+    eng.close()
+
+
+def test_engine_full_generate_graph_token_identical(gpu, og):
+    """Full GPT-2 124M random init, graph path, on-device greedy loop: the 8-id deterministic
+    prompt and 32 generated positions; the CPU golden, fed the same ids, picks the same argmax
+    at every position."""
+    cfg = gpu.gpt2_cfg()
+    w = gpu.gpt2_random_weights(cfg, 42, 0.03)
+    eng = gpu.Gpt2Engine(cfg, w, 2)
+    prompt = [(i * 7919 + 42) % cfg.V for i in range(8)]       # gpt2_engine.c deterministic prompt
+    got = eng.generate(prompt, 32).tolist()
+    gold = og.Gpt2Golden(og.gpt2_cfg(), w, NT)
+    seq = prompt + got
+    for p in range(8 + 32):
+        ref = gold.forward(seq[p], p, p >= 7)
+        if p >= 7:
+            assert og.argmax(ref) == seq[p + 1], (p, og.argmax(ref), seq[p + 1])
     eng.close()
 
 
@@ -157,9 +203,13 @@ def test_engine_full_greedy_token_identical(gpu, og):
 
 def test_engine_cli_json(gpu):
     exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "gpt2_engine")
-    for extra in ([], ["--fused"], ["--batch-prefill"]):
+    runs = {}
+    for extra in ([], ["--fused"], ["--batch-prefill"], ["--path", "fused"], ["--path", "graph"]):
         out = subprocess.run([exe, "--random", "5", "--gen", "5", "--json"] + extra,
                              capture_output=True, text=True, timeout=300)
         assert out.returncode == 0, out.stderr
         d = json.loads(out.stdout.strip().splitlines()[-1])
         assert d["done"] and d["prompt"] == 8 and d["tok_s"] > 0
+        runs[" ".join(extra)] = d["ids"]
+    # the device-side greedy loop emits the same ids as the host loop (no EOT in 5 steps)
+    assert runs["--path graph"] == runs[""][:len(runs["--path graph"])]
