@@ -100,6 +100,28 @@ def test_argument_errors_before_device(sg):
     assert L.sgpu_rope(None, None, None, 1, 2, 7, 0, None) == sg.SGPU_ERR_INVALID_ARG  # odd HD
     assert L.sgpu_attn_scores_gqa(None, None, None, 1, 0.1, 3, 128, 64, None) == sg.SGPU_ERR_INVALID_ARG
     assert L.sgpu_membw_read4(None, None, 16, 1, None, None) == sg.SGPU_ERR_INVALID_ARG
+    # engine entry points: NULL engines and out-of-range paths are rejected
+    assert L.sgpu_qwen_set_path(None, 1) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_gpt2_set_path(None, 1) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_qwen_generate(None, None, 1, 1, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_gpt2_generate(None, None, 1, 1, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_gpt2_forward(None, 0, 0, 1, None, 0) == sg.SGPU_ERR_INVALID_ARG
+
+
+def test_gemv_multi_geometry_follows_the_token_rule(sg):
+    """The matrix-core path (one 256-thread block per 32-token x 32-row tile) from T = 4, and
+    from T = 9 once K > 1024; below that a wave per row (gemm_nt_ok in gemv_core.h)."""
+    import ctypes as ct
+
+    L = sg.lib()
+    g, b = (ct.c_uint * 3)(), (ct.c_uint * 3)()
+    for T, K, mfma in [(3, 768, False), (4, 768, True), (8, 1028, False), (9, 1028, True), (8, 1024, True)]:
+        assert L.sgpu_kernel_geometry(b"gemv_multi", T, 2304, K, g, b) == 0
+        assert b[0] == 256
+        if mfma:
+            assert (g[0], g[1]) == (((T + 31) // 32) * (2304 // 32), 1), (T, K)
+        else:
+            assert g[0] == 2304 // 4 and g[1] == (T + 15) // 16, (T, K)
 
 
 def test_error_strings(sg):
