@@ -276,12 +276,21 @@ struct MapHalfPairs {
     __device__ __forceinline__ int row(int t, int j) const { return (t / half) * 2 * half + t % half + j * half; }
 };
 
+// Epilogues.  Per-row operands an epilogue needs besides the dot products (bias, residual,
+// tables) are read by load(t, rows, pre) when the row block's weights are fetched -- one block
+// ahead of use -- so they arrive with the weights instead of after the reduction;
+// operator()(t, rows, acc, pre) then writes the outputs.
+
 // y[row] = acc + bias?[row]
 struct EpiStore {
     const float* bias;
     float* y;
-    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
-        y[rows[0]] = acc[0] + (bias ? bias[rows[0]] : 0.0f);
+    struct Pre {
+        float b;
+    };
+    __device__ __forceinline__ void load(int, const int* rows, Pre& p) const { p.b = bias ? bias[rows[0]] : 0.0f; }
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc, const Pre& p) const {
+        y[rows[0]] = acc[0] + p.b;
     }
 };
 
@@ -318,6 +327,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
     vec w[NR][S];
     int rows[NR];
     bool valid = false;
+    typename Epi::Pre pre{};
     auto fetch = [&](int rb) {
         const int t = rb * TEAMS + team;
         valid = t < nteams;
@@ -331,6 +341,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
                 for (int j = 0; j < S; j++)
                     if (has[j]) w[r][j] = sgpu_ldnt(rv + LPR * j);
             }
+            epi.load(t, rows, pre);
         }
     };
     int rb = blockIdx.x;
@@ -353,6 +364,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
     for (; rb * TEAMS < nteams; rb += gridDim.x) {    // block-uniform loop
         const int t = rb * TEAMS + team;
         const bool cur_valid = valid;
+        const typename Epi::Pre cur_pre = pre;
         int cur_rows[NR];
         float acc[NR];
 #pragma unroll
@@ -376,7 +388,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
                 for (int r = 0; r < NR; r++)
                     if (WT::NEEDS_RECHECK && !__builtin_isfinite(acc[r]))
                         acc[r] = recompute_row_x<WT>(W + (size_t)cur_rows[r] * K, pro, K);
-                epi(t, cur_rows, acc);
+                epi(t, cur_rows, acc, cur_pre);
             }
         } else {
             acc[0] = sgpu_group_sum<64>(acc[0]);
@@ -388,7 +400,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
                 for (int i = 0; i < WAVES_PER_TEAM; i++) s += red[team * WAVES_PER_TEAM + i];
                 if (WT::NEEDS_RECHECK && !__builtin_isfinite(s)) s = recompute_row_x<WT>(W + (size_t)cur_rows[0] * K, pro, K);
                 acc[0] = s;
-                epi(t, cur_rows, acc);
+                epi(t, cur_rows, acc, cur_pre);
             }
             __syncthreads();
         }

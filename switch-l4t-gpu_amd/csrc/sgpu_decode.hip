@@ -26,16 +26,24 @@ struct EpiResidual {
     const float* resid;
     const float* bias;
     float* y;
-    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
-        const int r = rows[0];
-        y[r] = resid[r] + (acc[0] + (bias ? bias[r] : 0.0f));
+    struct Pre {
+        float res, b;
+    };
+    __device__ __forceinline__ void load(int, const int* rows, Pre& p) const {
+        p.res = resid[rows[0]];                   // only this team writes row rows[0]
+        p.b = bias ? bias[rows[0]] : 0.0f;
+    }
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc, const Pre& p) const {
+        y[rows[0]] = p.res + (acc[0] + p.b);
     }
 };
 
 // y[t] = silu(gate) * up, gate = rows t, up = rows t + FC (qwen_engine.c:349-350 form).
 struct EpiSwiGLU {
     float* y;
-    __device__ __forceinline__ void operator()(int t, const int*, const float* acc) const {
+    struct Pre {};
+    __device__ __forceinline__ void load(int, const int*, Pre&) const {}
+    __device__ __forceinline__ void operator()(int t, const int*, const float* acc, const Pre&) const {
 #pragma clang fp contract(off)
         const float g = acc[0];
         y[t] = (g / (1.0f + expf(-g))) * acc[1];
@@ -54,13 +62,25 @@ struct EpiQkvRope {
     const float* sinT;
     const int* step;
     int NH, NKV, HD;
-    __device__ __forceinline__ void operator()(int t, const int* rows, const float* acc) const {
+    struct Pre {
+        float b0, b1, c, s;
+        int pos;
+    };
+    __device__ __forceinline__ void load(int t, const int* rows, Pre& p) const {
+        const int h2 = HD / 2, i = t % h2;
+        p.pos = step[1];
+        p.b0 = bias[rows[0]];
+        p.b1 = bias[rows[1]];
+        p.c = cosT[(size_t)p.pos * h2 + i];
+        p.s = sinT[(size_t)p.pos * h2 + i];
+    }
+    __device__ __forceinline__ void operator()(int t, const int* rows, const float* acc, const Pre& p) const {
 #pragma clang fp contract(off)
-        const int h2 = HD / 2, hb = t / h2, i = t % h2, pos = step[1];
+        const int h2 = HD / 2, hb = t / h2, i = t % h2, pos = p.pos;
         const int KVD = NKV * HD;
-        const float a = acc[0] + bias[rows[0]], b = acc[1] + bias[rows[1]];
+        const float a = acc[0] + p.b0, b = acc[1] + p.b1;
         if (hb < NH + NKV) {
-            const float c = cosT[(size_t)pos * h2 + i], s = sinT[(size_t)pos * h2 + i];
+            const float c = p.c, s = p.s;
             const float ra = a * c - b * s, rb = a * s + b * c;
             float* dst = hb < NH ? q + (size_t)hb * HD : kc + (size_t)pos * KVD + (size_t)(hb - NH) * HD;
             dst[i] = ra;
@@ -83,9 +103,17 @@ struct EpiG2Qkv {
     float* vc;
     const int* step;
     int C;
-    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
-        const int r = rows[0], pos = step[1];
-        const float v = acc[0] + bias[r];
+    struct Pre {
+        float b;
+        int pos;
+    };
+    __device__ __forceinline__ void load(int, const int* rows, Pre& p) const {
+        p.b = bias[rows[0]];
+        p.pos = step[1];
+    }
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc, const Pre& p) const {
+        const int r = rows[0], pos = p.pos;
+        const float v = acc[0] + p.b;
         if (r < C) q[r] = v;
         else if (r < 2 * C) kc[(size_t)pos * C + (r - C)] = v;
         else vc[(size_t)pos * C + (r - 2 * C)] = v;
@@ -97,10 +125,14 @@ struct EpiG2Qkv {
 struct EpiBiasGelu {
     const float* bias;
     float* y;
-    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc) const {
+    struct Pre {
+        float b;
+    };
+    __device__ __forceinline__ void load(int, const int* rows, Pre& p) const { p.b = bias[rows[0]]; }
+    __device__ __forceinline__ void operator()(int, const int* rows, const float* acc, const Pre& p) const {
 #pragma clang fp contract(off)
         const int r = rows[0];
-        const float v = acc[0] + bias[r];
+        const float v = acc[0] + p.b;
         const float t = 0.7978845608f * (v + 0.044715f * v * v * v);
         y[r] = 0.5f * v * (1.0f + tanhf(t));
     }
