@@ -239,7 +239,7 @@ def main():
         pmc_probe()
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (bench.py has no "
               f"multi-GPU path; run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     if args.steps < 1 or args.warmup < 0:

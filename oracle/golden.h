@@ -2,8 +2,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This library is the oracle: the C restatement of the
  * reference's own CPU golden models.  Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load it, and only as the checker (or, in the
- * bench, as the timed CPU baseline).  The product path never calls into it.
+ * bench.py's cpu_baseline leg may load it, and only to check results against (or, in
+ * the bench, as the timed CPU baseline).  The product path never calls into it.
  *
  * Every function cites the reference lines it restates.  All arithmetic is plain
  * fp32 in the reference's serial k-ascending order; the library is compiled with

@@ -1,7 +1,7 @@
 """ctypes binding of oracle/liboracle.so -- the CPU golden models.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg, as the checker (and, in the bench, the timed CPU baseline).  Nothing in
+cpu_baseline leg, to check results against (and, in the bench, the timed CPU baseline).  Nothing in
 the product imports it.  Function-by-function citations of the reference lines it restates
 are in golden.h / golden.c.
 """

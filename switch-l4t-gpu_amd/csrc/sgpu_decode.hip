@@ -121,7 +121,7 @@ struct EpiG2Qkv {
 };
 
 // y[r] = gelu(acc + bias[r]), the tanh form of the reference gelu kernel
-// (gpt2_kernels.cu:199-206) with the arithmetic of this build's gelu.
+// (gpt2_kernels.cu:199-206) with the arithmetic of the gelu kernel in gpt2_kernels.hip.
 struct EpiBiasGelu {
     const float* bias;
     float* y;

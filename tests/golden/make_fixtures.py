@@ -4,7 +4,7 @@ sgemm_srand42_head.json: the first 16 (A, B) pairs of the SGEMM input generator
 (srand(42); A[i], B[i] = (rand()%2000 - 1000)/1000.0f interleaved, gpu_workload.c:81-82),
 produced through libswitchgpu.so's sgpu_gen_sgemm_inputs on this image's glibc.  The
 reference holds no stored vectors for this path; the fixture pins the generator against
-drift (a different libc rand(), a changed interleave) between this container and the GPU box.
+drift (a different libc rand(), a changed interleave) between machines.
 
 Run: python tests/golden/make_fixtures.py  (after building the package)
 """
