@@ -3,18 +3,23 @@
  * Command-line front end of the reference engine (gpu-llm/engine/qwen_engine.c:446-558) over
  * libswitchgpu.so: load the flat weight file (or build a random-init one in memory), prime
  * the KV cache with the prompt one position at a time, then greedy-decode, printing tok/s.
- * The per-position device work is sgpu_qwen_forward (the reference gpu_forward sequence).
+ * The per-position device work is sgpu_qwen_forward on the chosen launch path.
  *
  * Usage: qwen_engine (--weights FILE | --random SEED) [--ids FILE | --prompt-random N]
  *                    [--gen N] [--greedy] [--serve] [--json] [--write-weights FILE]
+ *                    [--path reference|fused|graph]
  *   --weights        flat file in the qwen_engine.c:8-16 layout (conv_qwen.py writer)
  *   --random SEED    random-init model: every fp16 tensor N(0, 0.02), RoPE theta 1e6 tables
  *   --ids FILE       u32 count + u32 ids (qwen_engine.c:477-486)
  *   --prompt-random  N ids drawn from the seeded LCG (default: the 8 deterministic ids of
  *                    qwen_engine.c:488)
  *   --serve          u32 request protocol on stdin/stdout (qwen_engine.c:406-444), greedy
- * Decoding is greedy (argmax, first max wins, qwen_engine.c:360-364); --greedy is accepted
- * for command-line compatibility.
+ *   --path P         reference: the gpu_forward launch sequence (qwen_engine.c:205-269);
+ *                    fused: five kernels per layer; graph (default): those replayed as a HIP
+ *                    graph.  Same tokens on every path.
+ * Decoding is greedy (argmax, first max wins, qwen_engine.c:360-364) and stops at EOT or
+ * <|im_end|> as the reference does (:539); --greedy is accepted for command-line
+ * compatibility.
  */
 #include <stdint.h>
 #include <stdio.h>
@@ -85,7 +90,7 @@ int main(int argc, char **argv) {
     setvbuf(stdout, NULL, _IONBF, 0);
     const char *weights = NULL, *ids_file = NULL, *write_weights = NULL;
     long long seed = -1;
-    int n_gen = 24, prompt_random = 0, serve = 0, json = 0;
+    int n_gen = 24, prompt_random = 0, serve = 0, json = 0, path = SGPU_QWEN_PATH_GRAPH;
     for (int i = 1; i < argc; i++) {
         if (!strcmp(argv[i], "--weights") && i + 1 < argc) weights = argv[++i];
         else if (!strcmp(argv[i], "--random") && i + 1 < argc) seed = atoll(argv[++i]);
@@ -96,6 +101,13 @@ int main(int argc, char **argv) {
         else if (!strcmp(argv[i], "--greedy")) { /* always greedy */ }
         else if (!strcmp(argv[i], "--serve")) serve = 1;
         else if (!strcmp(argv[i], "--json")) json = 1;
+        else if (!strcmp(argv[i], "--path") && i + 1 < argc) {
+            const char *v = argv[++i];
+            if (!strcmp(v, "reference")) path = SGPU_QWEN_PATH_REFERENCE;
+            else if (!strcmp(v, "fused")) path = SGPU_QWEN_PATH_FUSED;
+            else if (!strcmp(v, "graph")) path = SGPU_QWEN_PATH_GRAPH;
+            else { fprintf(stderr, "unknown path %s\n", v); return 2; }
+        }
         else { fprintf(stderr, "unknown arg %s\n", argv[i]); return 2; }
     }
     if (!weights && seed < 0) { fprintf(stderr, "--weights or --random required\n"); return 2; }
@@ -127,6 +139,7 @@ int main(int argc, char **argv) {
     CHK(sgpu_init(0));
     sgpu_qwen *eng = NULL;
     CHK(sgpu_qwen_create(&eng, &cfg, blob));
+    CHK(sgpu_qwen_set_path(eng, path));
     free(blob);
     float *logits = malloc(sizeof(float) * (size_t)cfg.V);
     if (serve) {
@@ -171,6 +184,7 @@ int main(int argc, char **argv) {
     double t_start = now_s();
     int emitted = 0;
     for (int g = 0; g < n_gen && total < cfg.CTX; g++) {
+        if (next == EOT || next == IM_END) break;
         CHK(sgpu_qwen_forward(eng, next, total - 1, 1, logits));
         next = argmax(logits, cfg.V);
         ids[total++] = next;

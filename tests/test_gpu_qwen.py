@@ -227,8 +227,41 @@ def test_engine_full_greedy_token_identical(gpu, og):
 
 def test_engine_cli_json(gpu):
     exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
-    out = subprocess.run([exe, "--random", "7", "--prompt-random", "8", "--gen", "6", "--json"],
-                         capture_output=True, text=True, timeout=300)
-    assert out.returncode == 0, out.stderr
-    d = json.loads(out.stdout.strip().splitlines()[-1])
-    assert d["done"] and d["generated"] == 6 and len(d["ids"]) == 8 + 1 + 6 and d["tok_s"] > 0
+    runs = {}
+    for path in ("reference", "graph"):
+        out = subprocess.run([exe, "--random", "7", "--prompt-random", "8", "--gen", "6", "--json", "--path", path],
+                             capture_output=True, text=True, timeout=300)
+        assert out.returncode == 0, out.stderr
+        d = json.loads(out.stdout.strip().splitlines()[-1])
+        assert d["done"] and d["tok_s"] > 0
+        runs[path] = d["ids"]
+    assert runs["reference"] == runs["graph"]
+
+
+def test_engine_serve_protocol(gpu):
+    """--serve (qwen_engine.c:406-444): per request u32 T, T u32 ids, u32 max_gen on stdin;
+    u32 M then M u32 ids (the prompt echoed, then the greedy continuation) on stdout.  Two
+    requests on one process; each continuation equals sgpu_qwen_generate on the same weights
+    (the CLI's --random SEED model) up to an EOT / <|im_end|> stop."""
+    import struct
+
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
+    reqs = [([5, 17, 9000, 151000, 42], 6), ([123] * 3 + [7], 4)]
+    payload = b"".join(struct.pack(f"<I{len(ids)}II", len(ids), *ids, g) for ids, g in reqs)
+    out = subprocess.run([exe, "--random", "7", "--serve"], input=payload, capture_output=True, timeout=300)
+    assert out.returncode == 0, out.stderr.decode()
+    buf, off, got = out.stdout, 0, []
+    for _ in reqs:
+        (m,) = struct.unpack_from("<I", buf, off)
+        got.append(list(struct.unpack_from(f"<{m}I", buf, off + 4)))
+        off += 4 + 4 * m
+    assert off == len(buf)
+    cfg = gpu.qwen_default_cfg()
+    eng = gpu.QwenEngine(cfg, gpu.qwen_random_blob(cfg, seed=7, std=0.02), 2)
+    for (ids, g), resp in zip(reqs, got):
+        assert resp[:len(ids)] == ids
+        want = eng.generate(ids, g).tolist()
+        cont = resp[len(ids):]
+        stop = next((i for i, t in enumerate(want) if t in (151643, 151645)), None)
+        assert cont == (want if stop is None else want[:stop + 1]), (cont, want)
+    eng.close()
