@@ -14,6 +14,9 @@
  *   --prompt-random  N ids drawn from the seeded LCG (default: the 8 deterministic ids of
  *                    qwen_engine.c:488)
  *   --serve          u32 request protocol on stdin/stdout (qwen_engine.c:406-444), greedy
+ *   --write-weights F  write the model (loaded or random-init) as a flat file in the same
+ *                    layout and exit without touching the device (the writer role of
+ *                    conv_qwen.py:63-99)
  *   --path P         reference: the gpu_forward launch sequence (qwen_engine.c:205-269);
  *                    fused: five kernels per layer; graph (default): those replayed as a HIP
  *                    graph.  Same tokens on every path.
@@ -133,7 +136,10 @@ int main(int argc, char **argv) {
     if (write_weights) {
         FILE *f = fopen(write_weights, "wb");
         if (!f || fwrite(blob, 1, bytes, f) != bytes) { fprintf(stderr, "cannot write %s\n", write_weights); return 2; }
-        fclose(f);
+        if (fclose(f)) { fprintf(stderr, "cannot write %s\n", write_weights); return 2; }
+        fprintf(stderr, "wrote %zu bytes to %s\n", bytes, write_weights);
+        free(blob);
+        return 0;
     }
     fprintf(log, "weights: %.1f MiB (%d-layer Qwen2.5-0.5B architecture, fp16)\n", bytes / 1048576.0, cfg.NL);
     CHK(sgpu_init(0));
