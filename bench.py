@@ -3,8 +3,9 @@
 Metric (headline): SGEMM TFLOPS at 4096^3 fp32 + batch-1 GEMV GB/s (fraction of HBM peak)
 + decode tok/s.  `value` is the SGEMM figure: a step is one C = A*B, M = N = K = 4096, fp32
 row-major, A and B from the reference generator (srand(42), gpu_workload.c:81-82), computed
-by sgemm_opt through libswitchgpu.so.  W untimed warm-up steps, then exactly K timed steps
-between device synchronisations.  Inputs are resident in HBM before timing starts.
+by sgpu_sgemm_opt through libswitchgpu.so (the 256x256-tile member sgemm_opt256 at this
+shape).  One verified launch, then W untimed warm-up steps immediately followed by exactly K
+timed steps between device synchronisations.  Inputs are resident in HBM before timing starts.
 
 Secondary figures measured in the same run (same JSON line):
   gemv   -- fp16-weight GEMV on the Qwen2.5-0.5B lm_head shape [151936 x 896], rotating
@@ -41,15 +42,18 @@ def bench_sgemm(n, steps, warmup):
     A, B = sgpu.gen_sgemm_inputs(n * n, 42)
     dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((n, n))
     run = lambda: sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, n, n, n, None)
-    for _ in range(max(warmup, 1)):
-        run()
+    run()
     sgpu.synchronize()
     # correctness of what is timed: sampled rows against the oracle-free float64 product
     C = dC.to_host()
     rows = np.linspace(0, n - 1, 8).astype(int)
     ref = A.reshape(n, n)[rows].astype(np.float64) @ B.reshape(n, n).astype(np.float64)
     err = float(np.abs(C[rows] - ref).max() / np.abs(ref).max())
+    # warm-up right before the timed launches: the GPU clock climbs from idle over tens of
+    # milliseconds, and a host-side pause between warm-up and timing would let it fall again
     ev = sgpu.Events()
+    for _ in range(warmup):
+        run()
     sgpu.synchronize()
     t0 = time.perf_counter()
     ev.record_start(None)
@@ -63,7 +67,7 @@ def bench_sgemm(n, steps, warmup):
     return dict(wall_s=wall, kernel_ms=kernel_ms, flops=flops, err=err)
 
 
-def bench_gemv_lm_head(reps=20, copies=4):
+def bench_gemv_lm_head(reps=100, copies=4, warm=1000):
     N, K = 151936, 896
     Wf, s = sgpu.gen_normal(N * K, 42, 0.0, 0.02)
     W = sgpu.f32_to_f16(Wf)
@@ -82,6 +86,9 @@ def bench_gemv_lm_head(reps=20, copies=4):
     ref = Wd @ x.astype(np.float64)
     err = float(np.abs(y[rows] - ref).max() / np.abs(ref).max())
     ev = sgpu.Events()
+    for i in range(warm):                      # ~45 ms: clocks to steady state, then timed
+        run(i)
+    sgpu.synchronize()
     ev.record_start(None)
     for i in range(reps * copies):
         run(i)
@@ -185,8 +192,8 @@ def cpu_baseline(n, target_s=1.5):
 
 def pmc_probe():
     """One launch each of: add2 over 64 Mi floats (a plain elementwise kernel whose HBM
-    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), sgemm_opt
-    4096^3 and the lm_head gemv_h.  Run under `rocprofv3 --pmc FETCH_SIZE` and again with
+    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), sgpu_sgemm_opt
+    4096^3 (sgemm_opt256) and the lm_head gemv_h.  Run under `rocprofv3 --pmc FETCH_SIZE` and again with
     WRITE_SIZE; prints the algorithmic bytes of each launch as one JSON line."""
     n = 64 << 20
     a = sgpu.DeviceArray(n)
@@ -220,8 +227,8 @@ def pmc_probe():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--pmc-probe", action="store_true", help="one launch per measured kernel, for rocprofv3 --pmc")
@@ -253,7 +260,7 @@ def main():
     sg = bench_sgemm(n, args.steps, args.warmup)
     tflops = sg["flops"] * args.steps / sg["wall_s"] / 1e12
     achieved = sg["flops"] / (sg["kernel_ms"] * 1e-3) / 1e12
-    log(f"sgemm_opt {n}^3: {sg['kernel_ms']:.3f} ms/launch, {achieved:.1f} TFLOP/s kernel, "
+    log(f"sgpu_sgemm_opt {n}^3: {sg['kernel_ms']:.3f} ms/launch, {achieved:.1f} TFLOP/s kernel, "
         f"{tflops:.1f} TFLOP/s wall, normwise err {sg['err']:.2e}")
     gv = bench_gemv_lm_head()
     log(f"gemv_h lm_head: {gv['us']:.1f} us, {gv['gbps']:.0f} GB/s ({gv['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), "
@@ -284,7 +291,8 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": "SGEMM C=A*B M=N=K=4096 fp32 row-major, A,B from srand(42) "
-                               "(rand()%2000-1000)/1000, alpha=1 beta=0, kernel sgemm_opt",
+                               "(rand()%2000-1000)/1000, alpha=1 beta=0, sgpu_sgemm_opt (launches the 256x256-tile "
+                               "member sgemm_opt256 at this shape)",
                    "M": n, "N": n, "K": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MATRIX_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),

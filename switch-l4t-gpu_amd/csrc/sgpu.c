@@ -44,7 +44,7 @@ static const struct {
 
 /* Every kernel the launchers use: (module, symbol). */
 enum {
-    K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_NAIVE, K_MEMBW,
+    K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_NAIVE, K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI,
     K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
     K_EMBED_H,
@@ -56,7 +56,7 @@ static const struct {
     const char *sym;
 } g_kern[NKERN] = {
     {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
-    {MOD_SWITCH, "sgemm_naive"}, {MOD_SWITCH, "membw_read4"},
+    {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_naive"}, {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"},
     {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
@@ -325,6 +325,7 @@ static int sgemm_tile(const char *k, int *tn) {
     if (!strcmp(k, "sgemm_tiled")) return *tn = 64, 64;
     if (!strcmp(k, "sgemm_tiled4")) return *tn = 128, 128;
     if (!strcmp(k, "sgemm_opt")) return *tn = 256, 128;
+    if (!strcmp(k, "sgemm_opt256")) return *tn = 256, 256;
     return *tn = 0, 0;
 }
 
@@ -408,9 +409,14 @@ int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
 }
-/* The optimised entry takes the 128x256 member when its grid gives every CU two blocks, the
- * 128x128 member when its grid gives every CU at least one, else the 64x64 member (measured
- * at 4096^3 / 2048^3 / 1024^3 respectively). */
+int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    return sgemm_common(K_SGEMM_OPT256, "sgemm_opt256", A, B, C, M, N, K, stream);
+}
+/* The optimised entry takes the 256x256 member when the shape is whole 256x256 tiles and
+ * 32-deep slices on 16-byte aligned operands and those tiles (one block per CU) fill at least
+ * 90% of their last round of CUs; otherwise the 128x256 member when its grid gives every CU two
+ * blocks, the 128x128 member when its grid gives every CU at least one, else the 64x64 member
+ * (measured at 4096^3 and 8192^3 / 6144^3 / 2048^3 / 1024^3). */
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
     if (M == 0 || N == 0) return SGPU_OK;
@@ -418,6 +424,12 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    if (M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 64 &&
+        (((uintptr_t)A | (uintptr_t)B) & 15) == 0) {
+        const long long t = (long long)(M / 256) * (N / 256), rounds = (t + d->cus - 1) / d->cus;
+        if (t >= d->cus && 10 * t >= 9 * rounds * d->cus)
+            return sgemm_common(K_SGEMM_OPT256, "sgemm_opt256", A, B, C, M, N, K, stream);
+    }
     const long long want = 2LL * d->cus;
     if ((long long)cdiv(M, 128) * cdiv(N, 256) >= want)
         return sgemm_common(K_SGEMM_OPT, "sgemm_opt", A, B, C, M, N, K, stream);

@@ -469,6 +469,10 @@ extern "C" {
 //                  memory instructions spread over the MFMA stream
 //   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks), m-major A staging,
 //                  spread -- large shapes
+//   sgemm_opt256 : 256x256 tile, BK 32, 4 waves of 128x128 (4x4 blocks), one wave per SIMD
+//                  (104 KB of LDS, 256 accumulator registers): half the LDS operand traffic
+//                  per flop of the 64x128 wave tile and 16384 MFMA cycles between barriers --
+//                  shapes whose 256x256 tiles fill the CUs in whole rounds
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_mfma<64, 64, 32, 2, 2, 8>(A, B, C, M, N, K);
@@ -482,6 +486,11 @@ sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B, float* __
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_opt(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_mfma<128, 256, 16, 2, 2, 0, 2>(A, B, C, M, N, K);
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgemm_opt256(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    sgemm_mfma<256, 256, 32, 2, 2, 1, 2>(A, B, C, M, N, K);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:

@@ -11,7 +11,8 @@ import pytest
 # qwen_kernels.cu) and that hosts resolve by name (gpu_workload.c:69-74, gemv_test.c:68-72,
 # gpt2_engine.c:119-128 GEMV subset, qwen_engine.c:148-155).
 REFERENCE_KERNELS = {
-    "switch_gpu": {"sgemm_tiled", "sgemm_tiled4", "sgemm_opt", "sgemm_naive", "membw_read4"},
+    "switch_gpu": {"sgemm_tiled", "sgemm_tiled4", "sgemm_opt", "sgemm_naive", "membw_read4",
+                   "sgemm_opt256"},   # the last one is an added member (no reference counterpart)
     "gemv": {"gemv", "gemv4", "gemv_warp"},
     "gpt2_kernels": {"gemv_warp", "gemv_warp_b", "gemv_multi"},
     "qwen_kernels": {"gemv_h", "rmsnorm", "rope", "swiglu", "attn_scores_gqa", "attn_softmax",
@@ -75,6 +76,8 @@ def test_geometry_contract(sg):
     L = sg.lib()
     assert L.sgpu_kernel_geometry(b"sgemm_opt", 4096, 4096, 4096, g, b) == 0
     assert tuple(b) == (256, 1, 1) and g[0] == 32 * 16          # one 128x256 tile per block
+    assert L.sgpu_kernel_geometry(b"sgemm_opt256", 4096, 4096, 4096, g, b) == 0
+    assert tuple(b) == (256, 1, 1) and g[0] == 16 * 16          # one 256x256 tile per block
     assert L.sgpu_kernel_geometry(b"sgemm_tiled4", 4096, 4096, 4096, g, b) == 0
     assert tuple(b) == (256, 1, 1) and g[0] == 32 * 32          # one 128x128 tile per block
     assert L.sgpu_kernel_geometry(b"sgemm_tiled", 1023, 1025, 997, g, b) == 0

@@ -101,11 +101,12 @@ def test_integer_exact(gpu, fn, M, N, K):
 # Shapes that steer sgpu_sgemm_opt to each member and each member to both its pipelined path
 # (M, N whole tiles, K whole slices, at least two slices) and its bounds-checked path.
 DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 4096, 16),
-                   (2048, 4096, 64), (2048, 4096, 96), (256, 256, 64), (192, 320, 40)]
+                   (2048, 4096, 64), (2048, 4096, 96), (256, 256, 64), (192, 320, 40),
+                   (4096, 4096, 96), (4096, 4352, 64), (4352, 4096, 160)]
 
 
 @pytest.mark.parametrize("M,N,K", DISPATCH_SHAPES)
-@pytest.mark.parametrize("fn", ["sgpu_sgemm_opt", "sgpu_sgemm_tiled4", "sgpu_sgemm_tiled"])
+@pytest.mark.parametrize("fn", ["sgpu_sgemm_opt", "sgpu_sgemm_opt256", "sgpu_sgemm_tiled4", "sgpu_sgemm_tiled"])
 def test_tile_paths_integer_exact(gpu, fn, M, N, K):
     say(f"sgemm {fn} integer {M}x{N}x{K}")
     rng = np.random.default_rng(M + N * 3 + K * 11)
@@ -115,7 +116,7 @@ def test_tile_paths_integer_exact(gpu, fn, M, N, K):
     assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
 
 
-@pytest.mark.parametrize("fn", VARIANTS[:3])
+@pytest.mark.parametrize("fn", VARIANTS[:3] + ["sgpu_sgemm_opt256"])
 def test_unaligned_pointers(gpu, fn):
     M, N, K = 200, 136, 72
     rng = np.random.default_rng(4)
@@ -133,7 +134,7 @@ def test_k_zero_writes_zeros_and_empty_is_noop(gpu, fn):
 
 
 @pytest.mark.parametrize("n", [2048, 4096])
-@pytest.mark.parametrize("fn", ["sgpu_sgemm_tiled4", "sgpu_sgemm_opt"])
+@pytest.mark.parametrize("fn", ["sgpu_sgemm_tiled4", "sgpu_sgemm_opt", "sgpu_sgemm_opt256"])
 def test_full_size_integer_exact(gpu, fn, n):
     say(f"sgemm {fn} integer {n}^3")
     rng = np.random.default_rng(n)
