@@ -220,7 +220,7 @@ def pmc_probe():
     sgpu.call("sgpu_gemv_h", dW.ptr, dx.ptr, None, dy.ptr, K, N, None)
     sgpu.synchronize()
     print(json.dumps({"add2_read": 2 * 4 * n, "add2_write": 4 * n,
-                      "sgemm_opt_read_min": 2 * 4 * N4 * N4, "sgemm_opt_write": 4 * N4 * N4,
+                      "sgemm_read_min": 2 * 4 * N4 * N4, "sgemm_write": 4 * N4 * N4,
                       "gemv_h_read": 2 * N * K + 4 * K, "gemv_h_write": 4 * N}), flush=True)
 
 
@@ -296,7 +296,7 @@ def main():
                    "M": n, "N": n, "K": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MATRIX_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),
-                     "traffic": traffic.get("sgemm_opt_4096")},
+                     "traffic": traffic.get("sgemm_opt256_4096")},
         "cpu_baseline": cpu,
         "gemv": {"kernel": "gemv_h (fp16 weights, fp32 x/y)", "shape": [151936, 896],
                  "us_per_call": round(gv["us"], 3), "gbps": round(gv["gbps"], 1),
