@@ -102,11 +102,9 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * :140-143 (sgemm_naive).
  * sgpu_sgemm_tiled / _tiled4 / _naive launch their own code-object symbol (tiles 64x64,
  * 128x128; one output per thread).  sgpu_sgemm_opt is the tuned entry: it launches the
- * sgemm_opt256 symbol (256x256 tiles, one block per CU) on shapes of whole 256x256 tiles
- * and 32-deep slices with 16-byte aligned A and B whose tiles fill at least 90% of their
- * last round of CUs; otherwise the sgemm_opt symbol (128x256 tiles) when that grid gives
- * every CU two blocks, else the 128x128 member when its grid gives every CU one block, else
- * the 64x64 member. */
+ * member (sgemm_opt256 256x256, sgemm_opt 128x256, sgemm_tiled4 128x128 or sgemm_tiled
+ * 64x64 tiles) whose busiest CU has the least work: ceil(tiles / CUs) tiles times the
+ * tile's area over the member's sustained rate. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);

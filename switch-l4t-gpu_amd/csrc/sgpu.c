@@ -412,11 +412,38 @@ int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, in
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_OPT256, "sgemm_opt256", A, B, C, M, N, K, stream);
 }
-/* The optimised entry takes the 256x256 member when the shape is whole 256x256 tiles and
- * 32-deep slices on 16-byte aligned operands and those tiles (one block per CU) fill at least
- * 90% of their last round of CUs; otherwise the 128x256 member when its grid gives every CU two
- * blocks, the 128x128 member when its grid gives every CU at least one, else the 64x64 member
- * (measured at 4096^3 and 8192^3 / 6144^3 / 2048^3 / 1024^3). */
+/* The optimised entry picks the member with the least work on its busiest CU: tiles are one
+ * block each, dealt over the CUs, so a launch lasts about ceil(tiles / CUs) tile times, and a
+ * tile time is the tile's area over the member's sustained rate.  Rates are each member's
+ * measured steady-state TFLOP/s at 4096^3 on MI355X (srand inputs): edge tiles and K tails
+ * run at about the same rate as whole tiles. */
+static const struct {
+    int kid;
+    const char *name;
+    int bm, bn;
+    double tflops;
+} g_sgemm_members[] = {
+    {K_SGEMM_OPT256, "sgemm_opt256", 256, 256, 143.5},
+    {K_SGEMM_OPT, "sgemm_opt", 128, 256, 139.3},
+    {K_SGEMM_TILED4, "sgemm_tiled4", 128, 128, 127.6},
+    {K_SGEMM_TILED, "sgemm_tiled", 64, 64, 125.3},
+};
+
+static int sgemm_pick(int M, int N, int cus) {
+    int best = 0;
+    double best_t = 0.0;
+    for (int m = 0; m < (int)(sizeof g_sgemm_members / sizeof g_sgemm_members[0]); m++) {
+        const long long tiles = (long long)cdiv(M, g_sgemm_members[m].bm) * cdiv(N, g_sgemm_members[m].bn);
+        const double t = (double)((tiles + cus - 1) / cus) * g_sgemm_members[m].bm * g_sgemm_members[m].bn /
+                         g_sgemm_members[m].tflops;
+        if (m == 0 || t < best_t) {
+            best = m;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
     if (M == 0 || N == 0) return SGPU_OK;
@@ -424,18 +451,8 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
-    if (M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 64 &&
-        (((uintptr_t)A | (uintptr_t)B) & 15) == 0) {
-        const long long t = (long long)(M / 256) * (N / 256), rounds = (t + d->cus - 1) / d->cus;
-        if (t >= d->cus && 10 * t >= 9 * rounds * d->cus)
-            return sgemm_common(K_SGEMM_OPT256, "sgemm_opt256", A, B, C, M, N, K, stream);
-    }
-    const long long want = 2LL * d->cus;
-    if ((long long)cdiv(M, 128) * cdiv(N, 256) >= want)
-        return sgemm_common(K_SGEMM_OPT, "sgemm_opt", A, B, C, M, N, K, stream);
-    if ((long long)cdiv(M, 128) * cdiv(N, 128) >= d->cus)
-        return sgemm_common(K_SGEMM_TILED4, "sgemm_tiled4", A, B, C, M, N, K, stream);
-    return sgemm_common(K_SGEMM_TILED, "sgemm_tiled", A, B, C, M, N, K, stream);
+    const int m = sgemm_pick(M, N, d->cus);
+    return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }
 int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_NAIVE, "sgemm_naive", A, B, C, M, N, K, stream);

@@ -5,17 +5,19 @@
 //   sgemm_tiled, sgemm_tiled4, sgemm_opt : (const float*A, const float*B, float*C, int M, int N, int K)
 //   sgemm_naive                          : same arguments, one output per thread
 //   membw_read4                          : (const float4*buf, float*out, int n4, int iters)
+// plus sgemm_opt256, a larger-tile member with the same arguments.
 //
 // C = A*B, fp32, row-major (A: MxK stride K, B: KxN stride N, C: MxN stride N), overwrite
-// (alpha 1, beta 0).  Unlike the reference kernels, every shape is accepted: edge tiles and
-// unaligned K/N take a bounds-checked load/store path, interior tiles take dwordx4 loads.
+// (alpha 1, beta 0).  Unlike the reference kernels, every shape is accepted: interior tiles
+// of problems with 16-byte rows take dwordx4 loads, edge tiles, K tails and unaligned rows
+// take masked loads, both through the same software pipeline.
 //
 // The tiled kernels run on the fp32 matrix cores: v_mfma_f32_32x32x2_f32 (true fp32 inputs,
 // fp32 accumulate; no reduced-precision xf32).  A block of 64*WGM*WGN threads owns a BMxBN
-// tile of C; each wave owns a (BM/WGM)x(BN/WGN) sub-tile held in AGPRs as 32x32 MFMA blocks.
+// tile of C; each wave owns a (BM/WGM)x(BN/WGN) sub-tile held as 32x32 MFMA blocks.
 // A and B k-slices of depth BK are staged through LDS, double-buffered (one barrier per
-// slice): A transposed to k-major with a 2-float row pad (conflict-free transposing stores),
-// B row-major.  Tiles are walked with a grid-stride loop over a linear tile index, so any
+// slice): A either k-major with a 2-float row pad or m-major with a 4-float pad, B row-major
+// with a pad.  Tiles are walked with a grid-stride loop over a linear tile index, so any
 // grid of 64*WGM*WGN-thread blocks is correct (surplus blocks exit); with one block per tile
 // the index is remapped so each XCD (blocks are dealt round-robin to the 8 XCDs) works on a
 // compact group of tiles that shares A and B panels in its own L2.
@@ -120,76 +122,6 @@ __device__ __forceinline__ void sgemm_store_c(float* __restrict__ C, int M, int 
         }
 }
 
-// One tile, any shape: bounds-checked scalar loads where the fast dwordx4 path does not apply.
-template <int BM, int BN, int BK, int WGM, int WGN>
-__device__ __forceinline__ void sgemm_tile_generic(const float* __restrict__ A, const float* __restrict__ B,
-                                                   int M, int N, int K, int m0, int n0, bool interior, bool aligned,
-                                                   SgemmLds<BM, BN, BK, WGM, WGN>& L,
-                                                   const SgemmThread<BM, BN, BK, WGM, WGN>& th,
-                                                   sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
-    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    const int tid = th.tid, nk = (K + BK - 1) / BK;
-    sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
-    auto load_slice = [&](int kt) {
-        const int k0 = kt * BK;
-        const bool fast = interior && aligned && (k0 + BK <= K);
-#pragma unroll
-        for (int r = 0; r < T::A_PER_T; r++) {
-            const int idx = tid + r * T::NT, row = idx / T::KQ, kq = idx % T::KQ;
-            const int gm = m0 + row, gk = k0 + 4 * kq;
-            if (fast) {
-                ra[r] = *reinterpret_cast<const sgpu_f32x4*>(A + (size_t)gm * K + gk);
-            } else {
-                float v[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    v[j] = (gm < M && gk + j < K) ? A[(size_t)gm * K + gk + j] : 0.0f;
-                ra[r] = sgpu_f32x4{v[0], v[1], v[2], v[3]};
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < T::B_PER_T; r++) {
-            const int idx = tid + r * T::NT, kr = idx / T::NQ, nq = idx % T::NQ;
-            const int gk = k0 + kr, gn = n0 + 4 * nq;
-            if (fast) {
-                rb[r] = *reinterpret_cast<const sgpu_f32x4*>(B + (size_t)gk * N + gn);
-            } else {
-                float v[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    v[j] = (gk < K && gn + j < N) ? B[(size_t)gk * N + gn + j] : 0.0f;
-                rb[r] = sgpu_f32x4{v[0], v[1], v[2], v[3]};
-            }
-        }
-    };
-
-    if (nk > 0) {
-        load_slice(0);
-        sgemm_store_slice(L, 0, tid, ra, rb);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int s = kt & 1;
-        if (kt + 1 < nk) load_slice(kt + 1);      // in flight while the MFMAs run
-#pragma unroll
-        for (int ks = 0; ks < BK / 2; ks++) {
-            const int kk = 2 * ks + th.khalf;     // MFMA src layout: lane = i + 32*k
-            float a[T::FM], b[T::FN];
-#pragma unroll
-            for (int i = 0; i < T::FM; i++) a[i] = L.As[s][kk][th.wm * T::WTM + i * 32 + th.l32];
-#pragma unroll
-            for (int j = 0; j < T::FN; j++) b[j] = L.Bs[s][kk][th.wn * T::WTN + j * 32 + th.l32];
-#pragma unroll
-            for (int i = 0; i < T::FM; i++)
-#pragma unroll
-                for (int j = 0; j < T::FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) sgemm_store_slice(L, s ^ 1, tid, ra, rb);
-        __syncthreads();
-    }
-}
-
 // One interior tile with K a multiple of BK (at least two slices) and 16-byte aligned rows:
 // software-pipelined.  Slice kt+1's global loads are issued before slice kt's MFMAs; each
 // k-step's LDS operands are read one step ahead into a second register set, so their
@@ -274,41 +206,118 @@ struct SgemmLdsM {
     float Bs[2][BK][LDBM];
 };
 
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false>
+// MODE 0: interior tile, K whole slices, 16-byte rows: dwordx4 loads, as above.
+// MODE 1 and 2: any tile, any K >= 1, rows of any 4-byte alignment, cdiv(K, BK) slices.
+//   MODE 1 (A tile rows and B slices within 2^31 bytes): consecutive lanes load consecutive
+//   floats (element j of a thread is A row tid/BK + j*NT/BK, k tid%BK; B row tid/BN + j*NT/BN,
+//   column tid%BN) with buffer loads; rows past M or K fall outside the buffer's range and
+//   read as zero, and k >= K or columns >= N are sent outside it (offset 2^31), so no mask
+//   is applied to data.  Floats are written to LDS one each.
+//   MODE 2 (larger operands): dwordx4-shaped map, each float loaded from a clamped
+//   (in-bounds) 64-bit address and zeroed outside A or B when the slice is written to LDS.
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false, int MODE = 0>
 __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, const float* __restrict__ B,
-                                                  int N, int K, int m0, int n0,
+                                                  int M, int N, int K, int m0, int n0,
                                                   SgemmLdsM<BM, BN, BK, WGM, WGN>& L,
                                                   const SgemmThread<BM, BN, BK, WGM, WGN>& th,
                                                   sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
     using T = MfmaTile<BM, BN, BK, WGM, WGN>;
+    constexpr bool MASKED = MODE != 0;
     constexpr int NG = BK / 8;                    // 4-step groups per slice
     static_assert(BK % 8 == 0, "k slice of whole 8-deep groups");
     static_assert(STORE_G >= 0 && STORE_G < NG, "store point inside the slice");
     static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
-    const int tid = th.tid, nk = K / BK;
+    static_assert(MODE != 1 || (T::NT % BK == 0 && T::NT % BN == 0), "lane map: whole rows per round");
+    constexpr int AE = 4 * T::A_PER_T, BE = 4 * T::B_PER_T;   // staged floats per thread
+    constexpr int AR = MODE == 1 ? T::NT / BK : 1, BR = MODE == 1 ? T::NT / BN : 1;
+    constexpr unsigned kOut = 0x80000000u;       // an offset past every MODE-1 buffer range
+    const int tid = th.tid, nk = MASKED ? (K + BK - 1) / BK : K / BK;
     const float* pa = A + (size_t)(m0 + tid / T::KQ) * K + 4 * (tid % T::KQ);
     const float* pb = B + (size_t)(tid / T::NQ) * N + n0 + 4 * (tid % T::NQ);
     const size_t astep = (size_t)(T::NT / T::KQ) * K, bstep_r = (size_t)(T::NT / T::NQ) * N;
     const size_t bstep = (size_t)BK * N;
+    // MODE 1 map and buffers: A from row m0 (range: the tile's valid rows), B from row kt*BK
+    const int ar = tid / BK, ak = tid % BK, bkr = tid / BN, bc = tid % BN;
+    const unsigned a_off0 = (unsigned)(ar * K + ak) * 4u, a_step = (unsigned)(AR * K) * 4u;
+    const unsigned b_off0 = (unsigned)(bkr * N + n0 + bc) * 4u, b_step = (unsigned)(BR * N) * 4u;
+    const bool b_col_ok = n0 + bc < N;
+    const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A + (size_t)m0 * K), (short)0, MODE == 1 ? min(M - m0, BM) * K * 4 : 0, 0x00020000);
+    // MODE 2 map
+    const int ar0 = m0 + tid / T::KQ, ak0 = 4 * (tid % T::KQ);
+    const int bk0 = tid / T::NQ, bn0 = n0 + 4 * (tid % T::NQ);
     sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
+    float sa[AE], sb[BE];
     auto load_slice = [&](int kt) __attribute__((always_inline)) {
+        if constexpr (MODE == 0) {
 #pragma unroll
-        for (int r = 0; r < T::A_PER_T; r++)
-            ra[r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
+            for (int r = 0; r < T::A_PER_T; r++)
+                ra[r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
 #pragma unroll
-        for (int r = 0; r < T::B_PER_T; r++)
-            rb[r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
+            for (int r = 0; r < T::B_PER_T; r++)
+                rb[r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
+        } else if constexpr (MODE == 1) {
+            const unsigned ao = kt * BK + ak < K ? a_off0 + (unsigned)(kt * BK) * 4u : kOut;
+#pragma unroll
+            for (int j = 0; j < AE; j++)
+                sa[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_a, (int)(ao + j * a_step), 0, 0));
+            const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(B + (size_t)kt * BK * N), (short)0, min(K - kt * BK, BK) * N * 4, 0x00020000);
+            const unsigned bo = b_col_ok ? b_off0 : kOut;
+#pragma unroll
+            for (int j = 0; j < BE; j++)
+                sb[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_b, (int)(bo + j * b_step), 0, 0));
+        } else {
+#pragma unroll
+            for (int r = 0; r < T::A_PER_T; r++) {
+                const float* rp = A + (size_t)min(ar0 + r * (T::NT / T::KQ), M - 1) * K;
+#pragma unroll
+                for (int e = 0; e < 4; e++) ra[r][e] = rp[min(kt * BK + ak0 + e, K - 1)];
+            }
+#pragma unroll
+            for (int r = 0; r < T::B_PER_T; r++) {
+                const float* rp = B + (size_t)min(kt * BK + bk0 + r * (T::NT / T::NQ), K - 1) * N;
+#pragma unroll
+                for (int e = 0; e < 4; e++) rb[r][e] = rp[min(bn0 + e, N - 1)];
+            }
+        }
+    };
+    // MODE 2: zero the staged elements of slice kt that lie outside A or B
+    auto mask_slice = [&](int kt) __attribute__((always_inline)) {
+        if constexpr (MODE == 2) {
+#pragma unroll
+            for (int r = 0; r < T::A_PER_T; r++) {
+                const bool row_ok = ar0 + r * (T::NT / T::KQ) < M;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (!(row_ok && kt * BK + ak0 + e < K)) ra[r][e] = 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < T::B_PER_T; r++) {
+                const bool k_ok = kt * BK + bk0 + r * (T::NT / T::NQ) < K;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (!(k_ok && bn0 + e < N)) rb[r][e] = 0.0f;
+            }
+        }
     };
     auto store_slice = [&](int s) __attribute__((always_inline)) {
+        if constexpr (MODE != 1) {
 #pragma unroll
-        for (int r = 0; r < T::A_PER_T; r++) {
-            const int idx = tid + r * T::NT;
-            *reinterpret_cast<sgpu_f32x4*>(&L.As[s][idx / T::KQ][4 * (idx % T::KQ)]) = ra[r];
-        }
+            for (int r = 0; r < T::A_PER_T; r++) {
+                const int idx = tid + r * T::NT;
+                *reinterpret_cast<sgpu_f32x4*>(&L.As[s][idx / T::KQ][4 * (idx % T::KQ)]) = ra[r];
+            }
 #pragma unroll
-        for (int r = 0; r < T::B_PER_T; r++) {
-            const int idx = tid + r * T::NT;
-            *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][idx / T::NQ][4 * (idx % T::NQ)]) = rb[r];
+            for (int r = 0; r < T::B_PER_T; r++) {
+                const int idx = tid + r * T::NT;
+                *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][idx / T::NQ][4 * (idx % T::NQ)]) = rb[r];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < AE; j++) L.As[s][ar + j * AR][ak] = sa[j];
+#pragma unroll
+            for (int j = 0; j < BE; j++) L.Bs[s][bkr + j * BR][bc] = sb[j];
         }
     };
     auto read_group = [&](int s, int g, sgpu_f32x4* a, sgpu_f32x4* b) __attribute__((always_inline)) {
@@ -327,6 +336,10 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     auto slice = [&](int s, int kt_next, auto more_c) __attribute__((always_inline)) {
         constexpr bool more = decltype(more_c)::value;
         constexpr int NMF = 4 * T::FM * T::FN;
+        constexpr int NLD = (MASKED ? 4 : 1) * (T::A_PER_T + T::B_PER_T);   // global loads
+        constexpr int LPM = (NLD + NMF - 1) / NMF;                            // ... per MFMA slot
+        constexpr int NST = (MODE == 1 ? 4 : 1) * (T::A_PER_T + T::B_PER_T);  // LDS writes
+        constexpr int WPM = (NST + NMF / 2 - 1) / (NMF / 2);                  // ... per slot (half group)
         sgpu_f32x4 a[2][T::FM], b[2][T::FN];
         if constexpr (!SPREAD) {
             if (more) load_slice(kt_next);
@@ -349,17 +362,20 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
 #pragma unroll
                     for (int j = 0; j < T::FN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i][t], b[c][j][t], acc[i][j], 0, 0, 0);
-            if (more && g == STORE_G) store_slice(s ^ 1);
+            if (more && g == STORE_G) {
+                if constexpr (MASKED) mask_slice(kt_next);
+                store_slice(s ^ 1);
+            }
             if constexpr (SPREAD) {
 #pragma unroll
                 for (int q = 0; q < NMF; q++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // 1 MFMA
-                    if (more && g == 0 && q < T::A_PER_T + T::B_PER_T)
-                        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);              // 1 global load
+                    if (more && g == 0 && q * LPM < NLD)
+                        __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);            // global loads
                     if (g + 1 < NG && q < T::FM + 4 * T::FN)
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // 1 LDS read
-                    if (more && g == STORE_G && q >= NMF / 2 && q < NMF / 2 + T::A_PER_T + T::B_PER_T)
-                        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);              // 1 LDS write
+                    if (more && g == STORE_G && q >= NMF / 2 && (q - NMF / 2) * WPM < NST)
+                        __builtin_amdgcn_sched_group_barrier(0x200, WPM, 0);            // LDS writes
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -367,6 +383,7 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     };
 
     load_slice(0);
+    if constexpr (MASKED) mask_slice(0);
     store_slice(0);
     __syncthreads();
     for (int kt = 0; kt + 1 < nk; kt++) {
@@ -388,17 +405,16 @@ __device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLds<
 template <int BM, int BN, int BK, int WGM, int WGN>
 __device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLdsU<BM, BN, BK, WGM, WGN>& u) { return u.k; }
 
-// STORE_AT < 0: generic path only.  Otherwise the pipelined path runs on interior-only
-// shapes with the slice store after k-step (LAYOUT 0) or 4-step group (LAYOUT 1, 2) STORE_AT.
+// Whole tiles of a problem with 16-byte rows and K whole slices run the dwordx4 pipeline
+// with the slice store after k-step (LAYOUT 0) or 4-step group (LAYOUT 1, 2) STORE_AT;
 // LAYOUT 0: k-major A staging; 1: m-major A staging; 2: m-major with memory instructions
-// spread one per MFMA.
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT = -1, int LAYOUT = 0>
+// spread one per MFMA.  All other tiles run the masked m-major pipeline.
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT, int LAYOUT>
 __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const float* __restrict__ B,
                                            float* __restrict__ C, int M, int N, int K) {
     using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    using LdsT = typename std::conditional<LAYOUT >= 1, SgemmLdsU<BM, BN, BK, WGM, WGN>,
-                                           SgemmLds<BM, BN, BK, WGM, WGN>>::type;
-    __shared__ __attribute__((aligned(16))) LdsT LU;
+    static_assert(STORE_AT >= 0, "store point");
+    __shared__ __attribute__((aligned(16))) SgemmLdsU<BM, BN, BK, WGM, WGN> LU;
     SgemmLds<BM, BN, BK, WGM, WGN>& L = sgemm_lds_k(LU);
 
     // The tile split assumes exactly NT threads per block; any other block size is rejected
@@ -412,17 +428,18 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
     const bool aligned = ((K & 3) == 0) && ((N & 3) == 0) &&
                          ((((uintptr_t)A) | ((uintptr_t)B)) & 15) == 0;
 
-    // Whole-problem check (uniform): every tile interior, K whole slices, 16-byte rows.  The
-    // pipelined and generic paths get separate tile loops so neither carries the other's
-    // registers.
-    const bool all_fast = STORE_AT >= 0 && aligned && M % BM == 0 && N % BN == 0 &&
-                          K % BK == 0 && K >= 2 * BK;
-    if constexpr (STORE_AT >= 0) {
-        if (all_fast) {
+    // Per tile: interior tiles of a problem with 16-byte rows and K whole slices (at least
+    // two) take the dwordx4 pipeline; every other tile (edges, K tails, unaligned rows) takes
+    // the same pipeline with masked loads (K = 0 writes zeros).  Each kind gets its own tile
+    // loop, so neither carries the other's registers.
+    {
+        const bool kfast = aligned && K % BK == 0 && K >= 2 * BK;
+        if (kfast) {
             for (int t = sgpu_bid(); t < ntiles; t += nb) {
                 int tm, tn;
                 sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
                 const int m0 = tm * BM, n0 = tn * BN;
+                if (m0 + BM > M || n0 + BN > N) continue;
                 sgpu_f32x16 acc[T::FM][T::FN];
 #pragma unroll
                 for (int i = 0; i < T::FM; i++)
@@ -431,28 +448,40 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
                 if constexpr (LAYOUT >= 1)
-                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT == 2>(A, B, N, K, m0, n0, LU.m, th, acc);
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT == 2>(A, B, M, N, K, m0, n0, LU.m, th, acc);
                 else
                     sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
                 sgemm_store_c(C, M, N, m0, n0, true, th, acc);
             }
-            return;
         }
-    }
-    for (int t = sgpu_bid(); t < ntiles; t += nb) {
-        int tm, tn;
-        sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
-        const int m0 = tm * BM, n0 = tn * BN;
-        const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
-        sgpu_f32x16 acc[T::FM][T::FN];
+        constexpr int SG = STORE_AT < BK / 8 ? STORE_AT : 0;      // a group index for the masked path
+        // Buffer-load windows (BM rows of A, BK rows of B) within 2^31 bytes: MODE 1, else 2.
+        // Each mode has its own tile loop (one accumulator set per loop, no merge of the two).
+        const bool win = (long long)BM * K * 4 < 0x7fffffffLL && (long long)BK * N * 4 < 0x7fffffffLL;
+        auto masked_tiles = [&](auto mode_c) __attribute__((always_inline)) {
+            constexpr int MODE = decltype(mode_c)::value;
+            for (int t = sgpu_bid(); t < ntiles; t += nb) {
+                int tm, tn;
+                sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+                const int m0 = tm * BM, n0 = tn * BN;
+                const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
+                if (kfast && interior) continue;
+                sgpu_f32x16 acc[T::FM][T::FN];
 #pragma unroll
-        for (int i = 0; i < T::FM; i++)
+                for (int i = 0; i < T::FM; i++)
 #pragma unroll
-            for (int j = 0; j < T::FN; j++)
+                    for (int j = 0; j < T::FN; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-        sgemm_tile_generic(A, B, M, N, K, m0, n0, interior, aligned, L, th, acc);
-        sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
+                        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+                if (K > 0)
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, SG, LAYOUT == 2, MODE>(A, B, M, N, K, m0, n0, LU.m, th, acc);
+                sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
+            }
+        };
+        if (win)
+            masked_tiles(std::integral_constant<int, 1>{});
+        else
+            masked_tiles(std::integral_constant<int, 2>{});
     }
 }
 
@@ -460,9 +489,9 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 
 extern "C" {
 
-// The three tiled members differ only in tile shape; each takes the pipelined path on
-// interior-only shapes (M, N multiples of the tile, K a multiple of BK, 16-byte rows) and
-// the bounds-checked path otherwise.
+// The tiled members differ only in tile shape and staging; each runs interior tiles of
+// 16-byte-row problems with K a multiple of BK on the dwordx4 pipeline and every other tile
+// on the masked pipeline (edges, K tails, unaligned rows).
 //   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), k-major A
 //                  staging -- small shapes
 //   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks), m-major A staging,
@@ -470,12 +499,12 @@ extern "C" {
 //   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks), m-major A staging,
 //                  spread -- large shapes
 //   sgemm_opt256 : 256x256 tile, BK 32, 4 waves of 128x128 (4x4 blocks), one wave per SIMD
-//                  (104 KB of LDS, 256 accumulator registers): half the LDS operand traffic
+//                  (138 KB of LDS, 256 accumulator registers): half the LDS operand traffic
 //                  per flop of the 64x128 wave tile and 16384 MFMA cycles between barriers --
 //                  shapes whose 256x256 tiles fill the CUs in whole rounds
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<64, 64, 32, 2, 2, 8>(A, B, C, M, N, K);
+    sgemm_mfma<64, 64, 32, 2, 2, 8, 0>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))

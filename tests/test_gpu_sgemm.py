@@ -116,6 +116,21 @@ def test_tile_paths_integer_exact(gpu, fn, M, N, K):
     assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
 
 
+# Shapes whose edge tiles take the clamped-address path: an A tile (BM rows of K floats) or a
+# B slice (BK rows of N floats) of 2^31 bytes or more.  Entries in {-1, 0, 1}: every partial
+# sum is an exact fp32 integer (|sum| <= K < 2^24).
+@pytest.mark.parametrize("fn,M,N,K", [("sgpu_sgemm_tiled", 3, 5, (1 << 23) + 7),
+                                      ("sgpu_sgemm_opt256", 3, 5, (1 << 21) + 3),
+                                      ("sgpu_sgemm_tiled", 2, (1 << 24) + 5, 3)])
+def test_large_operand_windows_integer_exact(gpu, fn, M, N, K):
+    say(f"sgemm {fn} large window {M}x{N}x{K}")
+    rng = np.random.default_rng(K + N)
+    A = rng.integers(-1, 2, (M, K)).astype(np.float32)
+    B = rng.integers(-1, 2, (K, N)).astype(np.float32)
+    C = run_sgemm(gpu, fn, A, B, M, N, K)
+    assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+
+
 @pytest.mark.parametrize("fn", VARIANTS[:3] + ["sgpu_sgemm_opt256"])
 def test_unaligned_pointers(gpu, fn):
     M, N, K = 200, 136, 72
