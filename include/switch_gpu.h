@@ -210,6 +210,7 @@ int sgpu_gpt2_prefill(sgpu_gpt2 *engine, const int *ids, int T, float *logits_ho
  *  FUSED     -- five kernels per layer: LayerNorm+qkv+bias+KV-cache write, attention,
  *               o+bias+residual, LayerNorm+fc+bias+GELU, proj+bias+residual (`fused` ignored)
  *  GRAPH     -- FUSED with the layer stack captured once as a HIP graph and replayed
+ * FUSED and GRAPH need CTX <= 8192 (SGPU_ERR_INVALID_ARG otherwise).
  * No counterpart in the reference beyond the sequence it restates. */
 #define SGPU_GPT2_PATH_REFERENCE 0
 #define SGPU_GPT2_PATH_FUSED 1

@@ -77,6 +77,8 @@ struct sgpu_gpt2 {
     int *d_tokens;                                  /* CTX + 1 greedy ids, by position */
     float *d_amax_v;                                /* argmax partials */
     int *d_amax_i;
+    float *d_attn_ws;                               /* attention chunk partials */
+    unsigned *d_attn_cnt;                           /* per-head chunk counters (kept at zero) */
     hipGraph_t g_layers, g_step;
     hipGraphExec_t ge_layers, ge_step;
 };
@@ -84,11 +86,13 @@ struct sgpu_gpt2 {
 void sgpu_gpt2_destroy(sgpu_gpt2 *e) {
     if (!e) return;
     float *bufs[] = {e->w, e->x, e->ln1, e->qkv, e->att, e->y, e->ln2, e->fc, e->scores, e->probs, e->logits,
-                     e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT, e->d_q, e->d_amax_v};
+                     e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT, e->d_q, e->d_amax_v,
+                     e->d_attn_ws};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) sgpu_free(bufs[i]);
     sgpu_free(e->d_step);
     sgpu_free(e->d_tokens);
     sgpu_free(e->d_amax_i);
+    sgpu_free(e->d_attn_cnt);
     if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
     if (e->g_layers) hipGraphDestroy(e->g_layers);
     if (e->ge_step) hipGraphExecDestroy(e->ge_step);
@@ -143,6 +147,9 @@ int sgpu_gpt2_create(sgpu_gpt2 **out, const sgpu_gpt2_cfg *c, const float *blob)
     TRY(sgpu_malloc((void **)&e->d_step, 4 * sizeof(int)));
     TRY(sgpu_memset_d8(e->d_step, 0, 4 * sizeof(int)));
     TRY(sgpu_malloc((void **)&e->d_tokens, (CTX + 1) * sizeof(int)));
+    TRY(zalloc(&e->d_attn_ws, SGPU_ATTN_WS_FLOATS(c->NH, c->HD)));
+    TRY(sgpu_malloc((void **)&e->d_attn_cnt, (size_t)c->NH * sizeof(unsigned)));
+    TRY(sgpu_memset_d8(e->d_attn_cnt, 0, (size_t)c->NH * sizeof(unsigned)));
 #undef TRY
     *out = e;
     return SGPU_OK;
@@ -189,7 +196,8 @@ static int fused_layers(sgpu_gpt2 *e) {
         const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
         TRY(sgpu_internal_g2_qkv(b + e->L.qkvw, C, 3 * C, e->x, b + e->L.ln1w, b + e->L.ln1b, eps, b + e->L.qkvb,
                                  e->d_q, e->kc[l], e->vc[l], e->d_step, s));
-        TRY(sgpu_internal_dec_attn(e->d_q, e->kc[l], e->vc[l], e->att, e->d_step, c->NH, c->NH, c->HD, 0.125f, s));
+        TRY(sgpu_internal_dec_attn(e->d_q, e->kc[l], e->vc[l], e->att, e->d_step, c->NH, c->NH, c->HD, 0.125f,
+                                   e->d_attn_ws, e->d_attn_cnt, s));
         TRY(sgpu_internal_g2_res(b + e->L.aow, C, C, e->att, b + e->L.aob, e->x, s));
         TRY(sgpu_internal_g2_fc(b + e->L.fcw, C, FC, e->x, b + e->L.ln2w, b + e->L.ln2b, eps, b + e->L.fcb, e->fc, s));
         TRY(sgpu_internal_g2_res(b + e->L.projw, FC, C, e->fc, b + e->L.projb, e->x, s));
@@ -247,6 +255,8 @@ static int run_layers(sgpu_gpt2 *e) {
 
 int sgpu_gpt2_set_path(sgpu_gpt2 *e, int path) {
     if (!e || path < SGPU_GPT2_PATH_REFERENCE || path > SGPU_GPT2_PATH_GRAPH) return SGPU_ERR_INVALID_ARG;
+    /* the fused attention keeps at most 8192 cached positions */
+    if (path != SGPU_GPT2_PATH_REFERENCE && e->cfg.CTX > 8192) return SGPU_ERR_INVALID_ARG;
     e->path = path;
     return SGPU_OK;
 }

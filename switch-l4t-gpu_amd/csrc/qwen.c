@@ -109,6 +109,8 @@ struct sgpu_qwen {
     float *d_q;                                /* rotated q of the fused path */
     float *d_amax_v;                           /* argmax partials */
     int *d_amax_i;
+    float *d_attn_ws;                          /* attention chunk partials */
+    unsigned *d_attn_cnt;                      /* per-head chunk counters (kept at zero) */
     hipGraph_t g_layers, g_step;
     hipGraphExec_t ge_layers, ge_step;
     uint16_t *d_emb, *d_lnfw;
@@ -147,6 +149,8 @@ void sgpu_qwen_destroy(sgpu_qwen *e) {
     sgpu_free(e->d_q);
     sgpu_free(e->d_amax_v);
     sgpu_free(e->d_amax_i);
+    sgpu_free(e->d_attn_ws);
+    sgpu_free(e->d_attn_cnt);
     if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
     if (e->g_layers) hipGraphDestroy(e->g_layers);
     if (e->ge_step) hipGraphExecDestroy(e->ge_step);
@@ -219,6 +223,8 @@ int sgpu_qwen_create(sgpu_qwen **out, const sgpu_qwen_cfg *c, const void *blob) 
     TRY(dalloc((void **)&e->d_q, (size_t)c->NH * c->HD * 4, NULL));
     TRY(dalloc((void **)&e->d_amax_v, SGPU_ARGMAX_PARTS * sizeof(float), NULL));
     TRY(dalloc((void **)&e->d_amax_i, SGPU_ARGMAX_PARTS * sizeof(int), NULL));
+    TRY(dalloc((void **)&e->d_attn_ws, SGPU_ATTN_WS_FLOATS(c->NH, c->HD) * sizeof(float), NULL));
+    TRY(dalloc((void **)&e->d_attn_cnt, (size_t)c->NH * sizeof(unsigned), NULL));
 #undef TRY
     *out = e;
     return SGPU_OK;
@@ -285,7 +291,8 @@ static int fused_layers(sgpu_qwen *e) {
     for (int l = 0; l < c->NL; l++) {
         TRY(sgpu_internal_dec_qkv(e->d_qkvw[l], C, QKVD, e->d_x, e->d_ln1w[l], eps, e->d_qkvb[l], e->d_q, e->d_kc[l],
                                   e->d_vc[l], e->d_cos, e->d_sin, e->d_step, NH, NKV, HD, s));
-        TRY(sgpu_internal_dec_attn(e->d_q, e->d_kc[l], e->d_vc[l], e->d_att, e->d_step, NH, NKV, HD, scale, s));
+        TRY(sgpu_internal_dec_attn(e->d_q, e->d_kc[l], e->d_vc[l], e->d_att, e->d_step, NH, NKV, HD, scale,
+                                   e->d_attn_ws, e->d_attn_cnt, s));
         TRY(sgpu_internal_dec_res(e->d_ow[l], C, C, e->d_att, NULL, e->d_x, s));
         TRY(sgpu_internal_dec_gateup(e->d_gateupw[l], C, FC, e->d_x, e->d_ln2w[l], eps, e->d_down, s));
         TRY(sgpu_internal_dec_res(e->d_downw[l], FC, C, e->d_down, NULL, e->d_x, s));

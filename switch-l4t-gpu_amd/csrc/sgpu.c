@@ -901,14 +901,15 @@ int sgpu_internal_dec_lmhead(const uint16_t *W, int K, int N, const float *x, co
 }
 
 int sgpu_internal_dec_attn(const float *q, const float *kc, const float *vc, float *out, const int *step, int NH,
-                           int NKV, int HD, float scale, void *stream) {
+                           int NKV, int HD, float scale, float *ws, unsigned *cnt, void *stream) {
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
     const int j = HD == 32 ? 0 : HD == 64 ? 1 : HD == 128 ? 2 : -1;
-    if (j < 0 || NKV <= 0 || NH % NKV) return SGPU_ERR_INVALID_ARG;
-    unsigned g[3] = {(unsigned)NH, 1, 1}, b[3] = {256, 1, 1};
-    void *args[] = {(void *)&q, (void *)&kc, (void *)&vc, (void *)&out, (void *)&step, &NH, &NKV, &scale};
+    if (j < 0 || NKV <= 0 || NH <= 0 || NH % NKV || !ws || !cnt) return SGPU_ERR_INVALID_ARG;
+    unsigned g[3] = {(unsigned)NH * SGPU_ATTN_SPLITS, 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&q, (void *)&kc, (void *)&vc, (void *)&out, (void *)&step, &NH, &NKV, &scale,
+                    (void *)&ws, (void *)&cnt};
     return launch(d->dec_attn[j], g, b, stream, args);
 }
 

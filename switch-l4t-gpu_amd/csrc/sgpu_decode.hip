@@ -5,7 +5,8 @@
 // the small steps around it in its prologue or epilogue:
 //   sgpu_dec_qkv_*    RMSNorm(x) -> qkv GEMV + bias -> RoPE on q and k -> q to its buffer,
 //                     k and v straight into the layer's KV cache at `pos`
-//   sgpu_dec_attn     GQA attention for one head per block: scores, softmax, mix
+//   sgpu_dec_attn     GQA attention: blocks per head and position chunk, scores, softmax, mix,
+//                     chunk partials combined by the head's last block
 //   sgpu_dec_res_*    GEMV + residual add in place: x[n] += W[n,:].a (o_proj, down_proj)
 //   sgpu_dec_gateup_* RMSNorm(x) -> gate and up rows of the same output -> SwiGLU
 //   sgpu_dec_lmhead_* final RMSNorm -> tied lm_head GEMV
@@ -138,7 +139,10 @@ struct EpiBiasGelu {
     }
 };
 
-constexpr int kMaxCtx = 8192;   // attention scores kept in LDS (32 KB)
+constexpr int kMaxCtx = 8192;    // longest cache the fused attention takes
+constexpr int kAttnSplits = 32;  // position chunks per head at most (blocks per head in the grid)
+constexpr int kAttnChunk = 256;  // positions per chunk before a second chunk is used
+constexpr int kAttnMaxLen = kMaxCtx / kAttnSplits;   // longest chunk (256): scores kept in LDS
 
 // Block max / sum over 256 threads (4 waves), result in every thread.
 __device__ __forceinline__ float block_max256(float v, float* red) {
@@ -156,23 +160,36 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// One block (256 threads) per query head h; T = pos + 1 cached positions.  Scores: LPT
-// lanes per position (DPL dims each), 256/LPT positions per pass; mix: 256/HD t-slices of HD
-// lanes, eight independent loads in flight per lane.
+// Attention over T = pos + 1 cached positions, block h + NH*c of a grid of NH x kAttnSplits
+// 256-thread blocks: query head h, position chunk c.  T <= kAttnChunk: one chunk per head and
+// block (h, 0) computes the head as a whole (the other blocks exit).  Longer caches are cut
+// into S = ceil(T / kAttnChunk) <= kAttnSplits chunks; each block writes its chunk's partial
+// (max score m, sum of exp(s - m), the exp-weighted sum of V) to ws, and the last of the S
+// blocks of head h to finish (per-head counter in cnt, reset by that block) combines them in
+// chunk order: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max_c m_c.
+// Scores: LPT lanes per position (DPL dims each), 256/LPT positions per pass; mix: 256/HD
+// t-slices of HD lanes, eight independent loads in flight per lane.
 template <int HD>
 __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const float* __restrict__ kc,
                                          const float* __restrict__ vc, float* __restrict__ out,
-                                         const int* __restrict__ step, int NH, int NKV, float scale) {
+                                         const int* __restrict__ step, int NH, int NKV, float scale,
+                                         float* __restrict__ ws, unsigned* __restrict__ cnt) {
     static_assert(HD == 32 || HD == 64 || HD == 128, "head dim");
     constexpr int LPT = HD >= 64 ? HD / 16 : 4;   // lanes per position
     constexpr int DPL = HD / LPT;                  // dims per lane (16 or 8)
     constexpr int PPP = 256 / LPT;                 // positions per pass
     constexpr int SLICES = 256 / HD;
-    __shared__ float sc[kMaxCtx];
+    constexpr int WSTRIDE = HD + 2;                // ws record: o[HD], m, l
+    __shared__ float sc[kAttnMaxLen];
     __shared__ float red[4];
     __shared__ float part[256];
-    const int tid = threadIdx.x, h = blockIdx.x, g = h / (NH / NKV);
-    const int T = step[1] + 1, KVD = NKV * HD;
+    __shared__ int last_s;
+    const int tid = threadIdx.x, h = blockIdx.x % NH, c = blockIdx.x / NH;   // chunk-major: chunk 0 first
+    const int g = h / (NH / NKV);
+    const int T = min(step[1] + 1, kMaxCtx), KVD = NKV * HD;
+    const int S = T <= kAttnChunk ? 1 : min(kAttnSplits, (T + kAttnChunk - 1) / kAttnChunk);
+    if (h >= NH || c >= S) return;                 // block-uniform
+    const int len = (T + S - 1) / S, p0 = c * len, p1 = min(T, p0 + len);   // p0 < p1 (see launcher)
     const float* kg = kc + (size_t)g * HD;
     const float* vg = vc + (size_t)g * HD;
     const int d0 = (tid % LPT) * DPL;
@@ -183,10 +200,10 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
 #pragma unroll
         for (int i = 0; i < 4; i++) qv[e + i] = a[i];
     }
-    for (int tb = 0; tb < T; tb += PPP) {
+    for (int tb = p0; tb < p1; tb += PPP) {
         const int t = tb + tid / LPT;
         float s = 0.0f;
-        if (t < T) {
+        if (t < p1) {
             const float* kr = kg + (size_t)t * KVD + d0;
 #pragma unroll
             for (int e = 0; e < DPL; e += 4) {
@@ -196,14 +213,15 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
             }
         }
         s = sgpu_group_sum<LPT>(s);
-        if (tid % LPT == LPT - 1 && t < T) sc[t] = s * scale;
+        if (tid % LPT == LPT - 1 && t < p1) sc[t - p0] = s * scale;
     }
     __syncthreads();
+    const int n = p1 - p0;
     float m = -1e30f;
-    for (int t = tid; t < T; t += 256) m = fmaxf(m, sc[t]);
+    for (int t = tid; t < n; t += 256) m = fmaxf(m, sc[t]);
     m = block_max256(m, red);
     float sum = 0.0f;
-    for (int t = tid; t < T; t += 256) {
+    for (int t = tid; t < n; t += 256) {
         const float e = expf(sc[t] - m);
         sc[t] = e;
         sum += e;
@@ -212,15 +230,47 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
     const int slice = tid / HD, d = tid % HD;
     float acc = 0.0f;
 #pragma unroll 8
-    for (int t = slice; t < T; t += SLICES) acc = __builtin_fmaf(sc[t], vg[(size_t)t * KVD + d], acc);
+    for (int t = slice; t < n; t += SLICES) acc = __builtin_fmaf(sc[t], vg[(size_t)(p0 + t) * KVD + d], acc);
     part[tid] = acc;
     __syncthreads();
+    float tot = 0.0f;
     if (slice == 0) {
-        float tot = 0.0f;
 #pragma unroll
         for (int s2 = 0; s2 < SLICES; s2++) tot += part[s2 * HD + d];
-        out[(size_t)h * HD + d] = tot / sum;
     }
+    if (S == 1) {
+        if (slice == 0) out[(size_t)h * HD + d] = tot / sum;
+        return;
+    }
+    // Partials go out as device-coherent stores (written through to memory) and are read back
+    // the same way, so no L2 writeback or invalidate is needed: the stores are complete
+    // (waited for) before this block's count reaches the head's counter, and the last block
+    // reads them after seeing the full count.
+    float* rec = ws + ((size_t)h * kAttnSplits + c) * WSTRIDE;
+    if (slice == 0) __hip_atomic_store(rec + d, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+        __hip_atomic_store(rec + HD, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(rec + HD + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores have completed
+    __syncthreads();
+    if (tid == 0) last_s = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __syncthreads();
+    if (!last_s) return;
+    if (slice == 0) {
+        const float* hr = ws + (size_t)h * kAttnSplits * WSTRIDE;
+        auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+        float M = -1e30f;
+        for (int c2 = 0; c2 < S; c2++) M = fmaxf(M, ld(hr + c2 * WSTRIDE + HD));
+        float L = 0.0f, O = 0.0f;
+        for (int c2 = 0; c2 < S; c2++) {
+            const float w = expf(ld(hr + c2 * WSTRIDE + HD) - M);
+            L = __builtin_fmaf(ld(hr + c2 * WSTRIDE + HD + 1), w, L);
+            O = __builtin_fmaf(ld(hr + c2 * WSTRIDE + d), w, O);
+        }
+        out[(size_t)h * HD + d] = O / L;
+    }
+    if (tid == 0) __hip_atomic_store(cnt + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // (value, index) of the first maximum: larger value wins, equal values keep the lower index.
@@ -329,18 +379,21 @@ __global__ void __launch_bounds__(256) sgpu_dec_argmax_final(const float* __rest
 
 __global__ void __launch_bounds__(256) sgpu_dec_attn64(const float* __restrict__ q, const float* __restrict__ kc,
                                                        const float* __restrict__ vc, float* __restrict__ out,
-                                                       const int* __restrict__ step, int NH, int NKV, float scale) {
-    dec_attn<64>(q, kc, vc, out, step, NH, NKV, scale);
+                                                       const int* __restrict__ step, int NH, int NKV, float scale,
+                                                       float* __restrict__ ws, unsigned* __restrict__ cnt) {
+    dec_attn<64>(q, kc, vc, out, step, NH, NKV, scale, ws, cnt);
 }
 __global__ void __launch_bounds__(256) sgpu_dec_attn32(const float* __restrict__ q, const float* __restrict__ kc,
                                                        const float* __restrict__ vc, float* __restrict__ out,
-                                                       const int* __restrict__ step, int NH, int NKV, float scale) {
-    dec_attn<32>(q, kc, vc, out, step, NH, NKV, scale);
+                                                       const int* __restrict__ step, int NH, int NKV, float scale,
+                                                       float* __restrict__ ws, unsigned* __restrict__ cnt) {
+    dec_attn<32>(q, kc, vc, out, step, NH, NKV, scale, ws, cnt);
 }
 __global__ void __launch_bounds__(256) sgpu_dec_attn128(const float* __restrict__ q, const float* __restrict__ kc,
                                                         const float* __restrict__ vc, float* __restrict__ out,
-                                                        const int* __restrict__ step, int NH, int NKV, float scale) {
-    dec_attn<128>(q, kc, vc, out, step, NH, NKV, scale);
+                                                        const int* __restrict__ step, int NH, int NKV, float scale,
+                                                       float* __restrict__ ws, unsigned* __restrict__ cnt) {
+    dec_attn<128>(q, kc, vc, out, step, NH, NKV, scale, ws, cnt);
 }
 
 }  // extern "C"

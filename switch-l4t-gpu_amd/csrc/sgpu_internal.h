@@ -18,8 +18,14 @@ SGPU_HIDDEN int sgpu_internal_dec_res(const uint16_t *W, int K, int N, const flo
                                       void *stream);
 SGPU_HIDDEN int sgpu_internal_dec_lmhead(const uint16_t *W, int K, int N, const float *x, const uint16_t *lnw,
                                          float eps, float *y, void *stream);
+/* Attention runs NH * SGPU_ATTN_SPLITS blocks (position chunks of one head each); ws holds
+ * SGPU_ATTN_WS_FLOATS(NH, HD) floats of chunk partials and cnt NH zero-initialised counters
+ * (each kernel leaves them at zero).  SGPU_ATTN_SPLITS matches kAttnSplits in sgpu_decode.hip. */
+#define SGPU_ATTN_SPLITS 32
+#define SGPU_ATTN_WS_FLOATS(NH, HD) ((size_t)(NH) * SGPU_ATTN_SPLITS * ((HD) + 2))
 SGPU_HIDDEN int sgpu_internal_dec_attn(const float *q, const float *kc, const float *vc, float *out,
-                                       const int *step, int NH, int NKV, int HD, float scale, void *stream);
+                                       const int *step, int NH, int NKV, int HD, float scale, float *ws,
+                                       unsigned *cnt, void *stream);
 SGPU_HIDDEN int sgpu_internal_dec_embed(const uint16_t *emb, int token, int pos, float *x, int C, int *step,
                                         void *stream);
 SGPU_HIDDEN int sgpu_internal_dec_embed_next(const uint16_t *emb, float *x, int C, int *step, void *stream);

@@ -117,6 +117,27 @@ def test_engine_small_teacher_forced(gpu, og, path):
     eng.close()
 
 
+def test_engine_long_context_fused(gpu, og):
+    """400 teacher-forced positions on the fused path: past 256 cached positions the attention
+    cuts each head's cache into chunks and combines their partials; logits track the CPU
+    golden at every checked position."""
+    cfg = dict(SMALL, NL=1, CTX=400)
+    w = unit_gain_weights(gpu, cfg, 29)
+    eng = gpu.Gpt2Engine(gpu.gpt2_cfg(**cfg), w, PATHS["fused"])
+    gold = og.Gpt2Golden(og.gpt2_cfg(**cfg), w, NT)
+    ids = [int(v) for v in np.random.default_rng(8).integers(0, cfg["V"], cfg["CTX"])]
+    for p, t in enumerate(ids):
+        check = p % 25 == 24 or p >= cfg["CTX"] - 2
+        got = eng.forward(t, p, check, 0)
+        want = gold.forward(t, p, check)
+        if not check:
+            continue
+        scale = np.abs(want).max()
+        assert np.abs(got - want).max() <= 1e-4 * scale, (p, np.abs(got - want).max(), scale)
+        assert int(np.argmax(got)) == og.argmax(want)
+    eng.close()
+
+
 @pytest.mark.parametrize("path", ["reference", "fused", "graph"])
 def test_engine_small_generate(gpu, og, path):
     """sgpu_gpt2_generate (device-side argmax and embedding on the fused/graph paths) gives the
