@@ -9,12 +9,13 @@ import pytest
 
 # Kernel names each reference module exports (switch_gpu.cu, gemv.cu, gpt2_kernels.cu,
 # qwen_kernels.cu) and that hosts resolve by name (gpu_workload.c:69-74, gemv_test.c:68-72,
-# gpt2_engine.c:119-128 GEMV subset, qwen_engine.c:148-155).
+# gpt2_engine.c:119-128, qwen_engine.c:148-155); a missing one is fatal to those hosts.
 REFERENCE_KERNELS = {
     "switch_gpu": {"sgemm_tiled", "sgemm_tiled4", "sgemm_opt", "sgemm_naive", "membw_read4",
                    "sgemm_opt256"},   # the last one is an added member (no reference counterpart)
     "gemv": {"gemv", "gemv4", "gemv_warp"},
-    "gpt2_kernels": {"gemv_warp", "gemv_warp_b", "gemv_multi"},
+    "gpt2_kernels": {"gemv_warp", "gemv_warp_b", "gemv_multi", "layernorm", "gelu", "add_bias", "add2",
+                     "attn_scores", "attn_softmax", "attn_mix"},
     "qwen_kernels": {"gemv_h", "rmsnorm", "rope", "swiglu", "attn_scores_gqa", "attn_softmax",
                      "attn_mix_gqa", "add2"},
 }
