@@ -907,7 +907,11 @@ int sgpu_internal_dec_attn(const float *q, const float *kc, const float *vc, flo
     if (!d) return rc;
     const int j = HD == 32 ? 0 : HD == 64 ? 1 : HD == 128 ? 2 : -1;
     if (j < 0 || NKV <= 0 || NH <= 0 || NH % NKV || !ws || !cnt) return SGPU_ERR_INVALID_ARG;
-    unsigned g[3] = {(unsigned)NH * SGPU_ATTN_SPLITS, 1, 1}, b[3] = {256, 1, 1};
+    /* 8 * G * ceil(NKV * splits / 8) blocks: block b is head (b / 8) % G of unit
+     * ((b / 8) / G) * 8 + b % 8 (KV group unit % NKV, chunk unit / NKV); units past
+     * NKV * splits fall at chunk >= splits and exit. */
+    const unsigned G = (unsigned)(NH / NKV), units = (unsigned)NKV * SGPU_ATTN_SPLITS;
+    unsigned g[3] = {8u * G * ((units + 7u) / 8u), 1, 1}, b[3] = {256, 1, 1};
     void *args[] = {(void *)&q, (void *)&kc, (void *)&vc, (void *)&out, (void *)&step, &NH, &NKV, &scale,
                     (void *)&ws, (void *)&cnt};
     return launch(d->dec_attn[j], g, b, stream, args);

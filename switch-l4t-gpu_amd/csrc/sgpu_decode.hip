@@ -160,8 +160,8 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// Attention over T = pos + 1 cached positions, block h + NH*c of a grid of NH x kAttnSplits
-// 256-thread blocks: query head h, position chunk c.  T <= kAttnChunk: one chunk per head and
+// Attention over T = pos + 1 cached positions, one 256-thread block per query head h and
+// position chunk c (the launcher's grid covers NKV x kAttnSplits units of G = NH/NKV heads).  T <= kAttnChunk: one chunk per head and
 // block (h, 0) computes the head as a whole (the other blocks exit).  Longer caches are cut
 // into S = ceil(T / kAttnChunk) <= kAttnSplits chunks; each block writes its chunk's partial
 // (max score m, sum of exp(s - m), the exp-weighted sum of V) to ws, and the last of the S
@@ -184,11 +184,17 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
     __shared__ float red[4];
     __shared__ float part[256];
     __shared__ int last_s;
-    const int tid = threadIdx.x, h = blockIdx.x % NH, c = blockIdx.x / NH;   // chunk-major: chunk 0 first
-    const int g = h / (NH / NKV);
+    // Block b -> XCD b % 8 (blocks are dealt round-robin to the 8 XCDs).  The G query heads
+    // that share KV group g and chunk c get the same b % 8, so the chunk's K and V come from
+    // HBM once into that XCD's L2; units (g, c) are numbered chunk-major so chunk 0 of every
+    // group is dispatched first.
+    const int G = NH / NKV, tid = threadIdx.x;
+    const int xcd = blockIdx.x % 8, i8 = blockIdx.x / 8;
+    const int u = (i8 / G) * 8 + xcd;              // unit (g, c) = (u % NKV, u / NKV)
+    const int g = u % NKV, c = u / NKV, h = g * G + i8 % G;
     const int T = min(step[1] + 1, kMaxCtx), KVD = NKV * HD;
     const int S = T <= kAttnChunk ? 1 : min(kAttnSplits, (T + kAttnChunk - 1) / kAttnChunk);
-    if (h >= NH || c >= S) return;                 // block-uniform
+    if (c >= S) return;                            // block-uniform (c < kAttnSplits, see launcher)
     const int len = (T + S - 1) / S, p0 = c * len, p1 = min(T, p0 + len);   // p0 < p1 (see launcher)
     const float* kg = kc + (size_t)g * HD;
     const float* vg = vc + (size_t)g * HD;
@@ -257,16 +263,33 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
     if (tid == 0) last_s = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
     __syncthreads();
     if (!last_s) return;
-    if (slice == 0) {
+    // All S partials of head h into LDS with one round of device-coherent loads, then
+    // combined in chunk order.
+    __shared__ float stage[kAttnSplits * WSTRIDE];
+    {
         const float* hr = ws + (size_t)h * kAttnSplits * WSTRIDE;
-        auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+        const int nf = S * WSTRIDE;
+        float r[(kAttnSplits * (HD + 2) + 255) / 256];
+#pragma unroll
+        for (int k = 0; k < (kAttnSplits * (HD + 2) + 255) / 256; k++) {
+            const int i = tid + 256 * k;
+            r[k] = i < nf ? __hip_atomic_load(hr + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < (kAttnSplits * (HD + 2) + 255) / 256; k++) {
+            const int i = tid + 256 * k;
+            if (i < nf) stage[i] = r[k];
+        }
+        __syncthreads();
+    }
+    if (slice == 0) {
         float M = -1e30f;
-        for (int c2 = 0; c2 < S; c2++) M = fmaxf(M, ld(hr + c2 * WSTRIDE + HD));
+        for (int c2 = 0; c2 < S; c2++) M = fmaxf(M, stage[c2 * WSTRIDE + HD]);
         float L = 0.0f, O = 0.0f;
         for (int c2 = 0; c2 < S; c2++) {
-            const float w = expf(ld(hr + c2 * WSTRIDE + HD) - M);
-            L = __builtin_fmaf(ld(hr + c2 * WSTRIDE + HD + 1), w, L);
-            O = __builtin_fmaf(ld(hr + c2 * WSTRIDE + d), w, O);
+            const float w = expf(stage[c2 * WSTRIDE + HD] - M);
+            L = __builtin_fmaf(stage[c2 * WSTRIDE + HD + 1], w, L);
+            O = __builtin_fmaf(stage[c2 * WSTRIDE + d], w, O);
         }
         out[(size_t)h * HD + d] = O / L;
     }
