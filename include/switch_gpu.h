@@ -262,9 +262,19 @@ int sgpu_qwen_set_path(sgpu_qwen *engine, int path);
 /* Greedy decode (the reference generation loop, qwen_engine.c:534-548, without its EOT
  * stop): prime with prompt[0..T-1], then n_gen more positions.  out_tokens receives n_gen + 1
  * ids -- the argmax after the prompt and after each generated position, first max winning.
- * On the FUSED/GRAPH paths the argmax runs on the device and the loop never waits for the
- * host; on the REFERENCE path it is the host loop over sgpu_qwen_forward. */
+ * On the FUSED/GRAPH paths the prompt goes through sgpu_qwen_prefill and the argmax runs on
+ * the device, so the loop never waits for the host; on the REFERENCE path it is the host loop
+ * over sgpu_qwen_forward. */
 int sgpu_qwen_generate(sgpu_qwen *engine, const int *prompt, int T, int n_gen, int *out_tokens);
+/* Batched prompt prefill: positions 0..T-1 of ids through every layer together (each layer's
+ * weights stream once per 512 prompt rows: matrix-core GEMMs on the fp16 weights, causal
+ * attention over the cache), filling KV-cache positions 0..T-1; the last row's V logits are
+ * copied to logits_host if it is not NULL.  sgpu_qwen_forward(engine, token, T, ...) then
+ * continues.  Needs the FUSED/GRAPH conditions (any path may be selected).  No counterpart
+ * in the Qwen reference, which primes the cache one position at a time
+ * (qwen_engine.c:526-531); the GPT-2 engine's gpu_prefill (gpt2_engine.c:269-326) is the
+ * model. */
+int sgpu_qwen_prefill(sgpu_qwen *engine, const int *ids, int T, float *logits_host);
 /* Device pointer to the last logits (V floats). */
 const float *sgpu_qwen_device_logits(const sgpu_qwen *engine);
 

@@ -433,8 +433,11 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
 // 256-thread blocks); with one block per tile, block ids are regrouped so each XCD runs a
 // contiguous run of tiles (token tiles fastest: the blocks on one XCD share W panels in its
 // L2).
-template <int FN>
-__device__ __forceinline__ void gemm_nt_mfma(const float* __restrict__ W, const float* __restrict__ X,
+// WT = WF32: fp32 weight rows, 16-byte loads.  WT = WF16: fp16 weight rows (8-byte loads of
+// four codes), converted to fp32 while staged with the exact reference decode (sgpu_h2f), so
+// the MFMAs see the same operands as the CPU golden.
+template <int FN, class WT = WF32>
+__device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict__ W, const float* __restrict__ X,
                                              const float* __restrict__ bias, float* __restrict__ Y,
                                              int K, int N, int T) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -458,14 +461,13 @@ __device__ __forceinline__ void gemm_nt_mfma(const float* __restrict__ W, const 
     for (int tile = bid; tile < ntiles; tile += nb) {
         const int tl = remap ? (tile % 8) * (ntiles / 8) + tile / 8 : tile;
         const int t0 = (tl % ntt) * 32, n0 = (tl / ntt) * 32 * FN;
-        // Row q*8 + lr of the staged block: token rows first, then weight rows.
-        const float* src[NI];
+        // Row q*8 + lr of the staged block: token rows first (q < 4), then weight rows.
+        const float* xsrc[4];
+        const typename WT::elem* wsrc[NI - 4];
 #pragma unroll
-        for (int q = 0; q < NI; q++) {
-            const int r = 8 * q + lr;
-            src[q] = r < 32 ? X + (size_t)min(t0 + r, T - 1) * K + 4 * lq
-                            : W + (size_t)min(n0 + r - 32, N - 1) * K + 4 * lq;
-        }
+        for (int q = 0; q < 4; q++) xsrc[q] = X + (size_t)min(t0 + 8 * q + lr, T - 1) * K + 4 * lq;
+#pragma unroll
+        for (int q = 4; q < NI; q++) wsrc[q - 4] = W + (size_t)min(n0 + 8 * q + lr - 32, N - 1) * K + 4 * lq;
 
         f32x16 acc[FN];
 #pragma unroll
@@ -478,7 +480,17 @@ __device__ __forceinline__ void gemm_nt_mfma(const float* __restrict__ W, const 
             const bool ok = k0 + 4 * lq < K;                // K % 4 == 0: whole quads
             const sgpu_f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int q = 0; q < NI; q++) g[q] = ok ? *reinterpret_cast<const sgpu_f32x4*>(src[q] + k0) : z;
+            for (int q = 0; q < 4; q++) g[q] = ok ? *reinterpret_cast<const sgpu_f32x4*>(xsrc[q] + k0) : z;
+#pragma unroll
+            for (int q = 4; q < NI; q++) {
+                if constexpr (sizeof(typename WT::elem) == 4) {
+                    g[q] = ok ? *reinterpret_cast<const sgpu_f32x4*>(wsrc[q - 4] + k0) : z;
+                } else {
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 h = ok ? *reinterpret_cast<const u32x2*>(wsrc[q - 4] + k0) : u32x2{0u, 0u};
+                    g[q] = sgpu_f32x4{sgpu_h2f_lo(h[0]), sgpu_h2f_hi(h[0]), sgpu_h2f_lo(h[1]), sgpu_h2f_hi(h[1])};
+                }
+            }
         };
         auto chunk = [&](bool more, int cn) __attribute__((always_inline)) {
 #pragma unroll

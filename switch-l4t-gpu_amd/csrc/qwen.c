@@ -111,6 +111,8 @@ struct sgpu_qwen {
     int *d_amax_i;
     float *d_attn_ws;                          /* attention chunk partials */
     unsigned *d_attn_cnt;                      /* per-head chunk counters (kept at zero) */
+    int *d_pf_ids;                             /* batched prefill: prompt ids and row buffers */
+    float *d_pf_x, *d_pf_xn, *d_pf_qkv, *d_pf_att, *d_pf_y, *d_pf_g;
     hipGraph_t g_layers, g_step;
     hipGraphExec_t ge_layers, ge_step;
     uint16_t *d_emb, *d_lnfw;
@@ -151,6 +153,9 @@ void sgpu_qwen_destroy(sgpu_qwen *e) {
     sgpu_free(e->d_amax_i);
     sgpu_free(e->d_attn_ws);
     sgpu_free(e->d_attn_cnt);
+    sgpu_free(e->d_pf_ids);
+    float *pf[] = {e->d_pf_x, e->d_pf_xn, e->d_pf_qkv, e->d_pf_att, e->d_pf_y, e->d_pf_g};
+    for (size_t i = 0; i < sizeof pf / sizeof pf[0]; i++) sgpu_free(pf[i]);
     if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
     if (e->g_layers) hipGraphDestroy(e->g_layers);
     if (e->ge_step) hipGraphExecDestroy(e->ge_step);
@@ -373,6 +378,72 @@ int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *
     return logits_to_host(e, logits_host);
 }
 
+/* ---- batched prompt prefill: the prompt's rows go through each layer together, so each
+ * layer's weights stream once per chunk of up to PF_ROWS rows instead of once per position ---- */
+#define PF_ROWS 512
+
+static int pf_alloc(sgpu_qwen *e) {
+    if (e->d_pf_x) return SGPU_OK;
+    const sgpu_qwen_cfg *c = &e->cfg;
+    const size_t R = PF_ROWS, C = (size_t)c->C, FC = (size_t)c->FC, Q = (size_t)e->L.qkvd;
+    const size_t ybig = 2 * FC > C ? 2 * FC : C;
+    int rc;
+    if ((rc = dalloc((void **)&e->d_pf_ids, (size_t)c->CTX * sizeof(int), NULL)) ||
+        (rc = dalloc((void **)&e->d_pf_xn, R * C * 4, NULL)) || (rc = dalloc((void **)&e->d_pf_qkv, R * Q * 4, NULL)) ||
+        (rc = dalloc((void **)&e->d_pf_att, R * C * 4, NULL)) || (rc = dalloc((void **)&e->d_pf_y, R * ybig * 4, NULL)) ||
+        (rc = dalloc((void **)&e->d_pf_g, R * FC * 4, NULL)) || (rc = dalloc((void **)&e->d_pf_x, R * C * 4, NULL)))
+        return rc;
+    return SGPU_OK;
+}
+
+/* Positions 0..T-1 of the prompt into the KV caches, the last row's logits into d_logits and
+ * the step record {ids[T-1], T-1} (so the on-device greedy loop continues from position T). */
+static int prefill_rows(sgpu_qwen *e, const int *ids, int T) {
+    const sgpu_qwen_cfg *c = &e->cfg;
+    const int C = c->C, NH = c->NH, NKV = c->NKV, HD = c->HD, FC = c->FC, QKVD = e->L.qkvd;
+    const float eps = c->eps, scale = (float)(1.0 / sqrt((double)HD));
+    void *s = (void *)e->stream;
+    int rc;
+    if ((rc = pf_alloc(e))) return rc;
+    hipError_t he = hipMemcpyAsync(e->d_pf_ids, ids, (size_t)T * sizeof(int), hipMemcpyHostToDevice, e->stream);
+    if (he != hipSuccess) return (int)he;
+#define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+    int Tc = 0;
+    for (int c0 = 0; c0 < T; c0 += PF_ROWS) {
+        Tc = T - c0 < PF_ROWS ? T - c0 : PF_ROWS;
+        TRY(sgpu_internal_pf_embed(e->d_emb, e->d_pf_ids + c0, Tc, e->d_pf_x, C, s));
+        for (int l = 0; l < c->NL; l++) {
+            TRY(sgpu_rmsnorm(e->d_pf_x, e->d_ln1w[l], e->d_pf_xn, C, eps, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_qkvw[l], e->d_pf_xn, e->d_qkvb[l], e->d_pf_qkv, C, QKVD, Tc, s));
+            TRY(sgpu_internal_pf_qkv_post(e->d_pf_qkv, Tc, c0, e->d_cos, e->d_sin, e->d_kc[l], e->d_vc[l], NH, NKV,
+                                          HD, s));
+            TRY(sgpu_internal_pf_attn(e->d_pf_qkv, e->d_kc[l], e->d_vc[l], e->d_pf_att, Tc, c0, NH, NKV, HD, scale, s));
+            TRY(sgpu_internal_pf_gemm(e->d_ow[l], e->d_pf_att, NULL, e->d_pf_y, C, C, Tc, s));
+            TRY(sgpu_add2(e->d_pf_x, e->d_pf_y, e->d_pf_x, Tc * C, s));
+            TRY(sgpu_rmsnorm(e->d_pf_x, e->d_ln2w[l], e->d_pf_xn, C, eps, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_gateupw[l], e->d_pf_xn, NULL, e->d_pf_y, C, 2 * FC, Tc, s));
+            TRY(sgpu_internal_pf_swiglu(e->d_pf_y, e->d_pf_g, FC, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_downw[l], e->d_pf_g, NULL, e->d_pf_y, FC, C, Tc, s));
+            TRY(sgpu_add2(e->d_pf_x, e->d_pf_y, e->d_pf_x, Tc * C, s));
+        }
+    }
+    TRY(sgpu_internal_dec_lmhead(e->d_emb, C, c->V, e->d_pf_x + (size_t)(Tc - 1) * C, e->d_lnfw, eps, e->d_logits, s));
+#undef TRY
+    const int st[2] = {ids[T - 1], T - 1};
+    he = hipMemcpyAsync(e->d_step, st, sizeof st, hipMemcpyHostToDevice, e->stream);
+    if (he != hipSuccess) return (int)he;
+    return sgpu_stream_synchronize(s);
+}
+
+int sgpu_qwen_prefill(sgpu_qwen *e, const int *ids, int T, float *logits_host) {
+    if (!e || !ids || T <= 0 || T > e->cfg.CTX || !fused_ok(&e->cfg)) return SGPU_ERR_INVALID_ARG;
+    for (int p = 0; p < T; p++)
+        if (ids[p] < 0 || ids[p] >= e->cfg.V) return SGPU_ERR_INVALID_ARG;
+    int rc = prefill_rows(e, ids, T);
+    if (rc || !logits_host) return rc;
+    return sgpu_memcpy_dtoh(logits_host, e->d_logits, (size_t)e->cfg.V * sizeof(float));
+}
+
 int sgpu_qwen_generate(sgpu_qwen *e, const int *prompt, int T, int n_gen, int *out_tokens) {
     if (!e || !prompt || !out_tokens || T <= 0 || n_gen < 0) return SGPU_ERR_INVALID_ARG;
     const sgpu_qwen_cfg *c = &e->cfg;
@@ -395,8 +466,7 @@ int sgpu_qwen_generate(sgpu_qwen *e, const int *prompt, int T, int n_gen, int *o
         free(logits);
         return rc;
     }
-    for (int p = 0; p < T; p++)
-        if ((rc = sgpu_qwen_forward(e, prompt[p], p, p == T - 1, NULL))) return rc;
+    if ((rc = prefill_rows(e, prompt, T))) return rc;
     if ((rc = sgpu_internal_dec_argmax(e->d_logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
                                        (void *)e->stream)))
         return rc;

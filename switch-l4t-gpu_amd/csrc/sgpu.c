@@ -94,6 +94,7 @@ typedef struct {
     hipFunction_t dec[NDECFAM][NDEC_ALL];
     hipFunction_t dec_attn[3], dec_embed, dec_embed_next, dec_argmax_part, dec_argmax_final;
     hipFunction_t dec_g2embed, dec_g2embed_next;
+    hipFunction_t pf_embed, pf_gemm, pf_qkv_post, pf_attn[3], pf_swiglu;
 } devstate;
 
 static devstate g_dev[SGPU_MAX_DEVICES];
@@ -169,6 +170,19 @@ static int load_device(int dev) {
             hipModuleGetFunction(&d->dec_argmax_final, d->mod[MOD_DECODE], "sgpu_dec_argmax_final") != hipSuccess ||
             hipModuleGetFunction(&d->dec_g2embed, d->mod[MOD_DECODE], "sgpu_dec_g2embed") != hipSuccess ||
             hipModuleGetFunction(&d->dec_g2embed_next, d->mod[MOD_DECODE], "sgpu_dec_g2embed_next") != hipSuccess) {
+            rc = SGPU_ERR_NO_KERNEL;
+            goto out;
+        }
+        const char *pattn[3] = {"sgpu_pf_attn32", "sgpu_pf_attn64", "sgpu_pf_attn128"};
+        for (int j = 0; j < 3; j++)
+            if (hipModuleGetFunction(&d->pf_attn[j], d->mod[MOD_DECODE], pattn[j]) != hipSuccess) {
+                rc = SGPU_ERR_NO_KERNEL;
+                goto out;
+            }
+        if (hipModuleGetFunction(&d->pf_embed, d->mod[MOD_DECODE], "sgpu_pf_embed") != hipSuccess ||
+            hipModuleGetFunction(&d->pf_gemm, d->mod[MOD_DECODE], "sgpu_pf_gemm") != hipSuccess ||
+            hipModuleGetFunction(&d->pf_qkv_post, d->mod[MOD_DECODE], "sgpu_pf_qkv_post") != hipSuccess ||
+            hipModuleGetFunction(&d->pf_swiglu, d->mod[MOD_DECODE], "sgpu_pf_swiglu") != hipSuccess) {
             rc = SGPU_ERR_NO_KERNEL;
             goto out;
         }
@@ -948,6 +962,68 @@ int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, 
     unsigned g2[3] = {1, 1, 1};
     void *a2[] = {(void *)&part_v, (void *)&part_i, &np, (void *)&step, (void *)&out};
     return launch(d->dec_argmax_final, g2, b, stream, a2);
+}
+
+/* ---- batched prompt prefill (sgpu_decode.hip sgpu_pf_*) ---- */
+int sgpu_internal_pf_embed(const uint16_t *emb, const int *ids, int T, float *x, int C, void *stream) {
+    if (!emb || !ids || !x || T <= 0 || C <= 0) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid((int)umin((unsigned)((long long)T * C), 0x7fffffffu)), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&emb, (void *)&ids, &T, (void *)&x, &C};
+    return launch(d->pf_embed, g, b, stream, args);
+}
+
+int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, float *Y, int K, int N, int T,
+                          void *stream) {
+    if (!W || !X || !Y || K <= 0 || N <= 0 || T <= 0 || K % 4 || ((uintptr_t)W & 7) || ((uintptr_t)X & 15))
+        return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    const long long tiles = (long long)cdiv(T, 32) * cdiv(N, 32);
+    unsigned g[3] = {(unsigned)(tiles < 0x7fffffffLL ? tiles : 0x7fffffffLL), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T};
+    return launch(d->pf_gemm, g, b, stream, args);
+}
+
+int sgpu_internal_pf_qkv_post(float *qkv, int T, int pos0, const float *cosT, const float *sinT, float *kc,
+                              float *vc, int NH, int NKV, int HD, void *stream) {
+    if (!qkv || !cosT || !sinT || !kc || !vc || T <= 0 || pos0 < 0 || NH <= 0 || NKV <= 0 || HD <= 0 || HD % 2)
+        return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    const long long per = (long long)(NH + NKV) * (HD / 2) + (long long)NKV * HD;
+    unsigned g[3] = {(unsigned)elem_grid((int)umin((unsigned)(T * per), 0x7fffffffu)), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&qkv, &T, &pos0, (void *)&cosT, (void *)&sinT, (void *)&kc, (void *)&vc, &NH, &NKV, &HD};
+    return launch(d->pf_qkv_post, g, b, stream, args);
+}
+
+int sgpu_internal_pf_attn(const float *qkv, const float *kc, const float *vc, float *out, int T, int pos0, int NH,
+                          int NKV, int HD, float scale, void *stream) {
+    const int j = HD == 32 ? 0 : HD == 64 ? 1 : HD == 128 ? 2 : -1;
+    if (j < 0 || !qkv || !kc || !vc || !out || T <= 0 || T > 65535 || pos0 < 0 || pos0 + T > 8192 || NKV <= 0 ||
+        NH <= 0 || NH % NKV)
+        return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    int QKVD = (NH + 2 * NKV) * HD;
+    unsigned g[3] = {(unsigned)NH, (unsigned)T, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&qkv, (void *)&kc, (void *)&vc, (void *)&out, &pos0, &NH, &NKV, &scale, &QKVD};
+    return launch(d->pf_attn[j], g, b, stream, args);
+}
+
+int sgpu_internal_pf_swiglu(const float *Y, float *G, int FC, int T, void *stream) {
+    if (!Y || !G || FC <= 0 || T <= 0) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    unsigned g[3] = {(unsigned)elem_grid((int)umin((unsigned)((long long)T * FC), 0x7fffffffu)), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&Y, (void *)&G, &FC, &T};
+    return launch(d->pf_swiglu, g, b, stream, args);
 }
 
 /* ---- GPT-2 fused decode (sgpu_decode.hip, fp32 weights) ---- */

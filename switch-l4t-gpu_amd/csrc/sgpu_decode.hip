@@ -160,49 +160,25 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// Attention over T = pos + 1 cached positions, one 256-thread block per query head h and
-// position chunk c (the launcher's grid covers NKV x kAttnSplits units of G = NH/NKV heads).  T <= kAttnChunk: one chunk per head and
-// block (h, 0) computes the head as a whole (the other blocks exit).  Longer caches are cut
-// into S = ceil(T / kAttnChunk) <= kAttnSplits chunks; each block writes its chunk's partial
-// (max score m, sum of exp(s - m), the exp-weighted sum of V) to ws, and the last of the S
-// blocks of head h to finish (per-head counter in cnt, reset by that block) combines them in
-// chunk order: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max_c m_c.
-// Scores: LPT lanes per position (DPL dims each), 256/LPT positions per pass; mix: 256/HD
-// t-slices of HD lanes, eight independent loads in flight per lane.
+// One query head over cached positions p0..p1-1 (p1 - p0 <= the length of sc): scores in
+// sc, block max m and sum of exp(s - m) returned in every thread, and the exp-weighted sum of
+// V returned in the lanes tid < HD (dim tid).  Scores: LPT lanes per position (DPL dims each),
+// 256/LPT positions per pass; mix: 256/HD t-slices of HD lanes, eight independent loads in
+// flight per lane.
 template <int HD>
-__device__ __forceinline__ void dec_attn(const float* __restrict__ q, const float* __restrict__ kc,
-                                         const float* __restrict__ vc, float* __restrict__ out,
-                                         const int* __restrict__ step, int NH, int NKV, float scale,
-                                         float* __restrict__ ws, unsigned* __restrict__ cnt) {
-    static_assert(HD == 32 || HD == 64 || HD == 128, "head dim");
+__device__ __forceinline__ float attn_chunk(const float* __restrict__ qh, const float* __restrict__ kg,
+                                            const float* __restrict__ vg, int KVD, int p0, int p1, float scale,
+                                            float* sc, float* red, float* part, float& m_out, float& sum_out) {
     constexpr int LPT = HD >= 64 ? HD / 16 : 4;   // lanes per position
     constexpr int DPL = HD / LPT;                  // dims per lane (16 or 8)
     constexpr int PPP = 256 / LPT;                 // positions per pass
     constexpr int SLICES = 256 / HD;
-    constexpr int WSTRIDE = HD + 2;                // ws record: o[HD], m, l
-    __shared__ float sc[kAttnMaxLen];
-    __shared__ float red[4];
-    __shared__ float part[256];
-    __shared__ int last_s;
-    // Block b -> XCD b % 8 (blocks are dealt round-robin to the 8 XCDs).  The G query heads
-    // that share KV group g and chunk c get the same b % 8, so the chunk's K and V come from
-    // HBM once into that XCD's L2; units (g, c) are numbered chunk-major so chunk 0 of every
-    // group is dispatched first.
-    const int G = NH / NKV, tid = threadIdx.x;
-    const int xcd = blockIdx.x % 8, i8 = blockIdx.x / 8;
-    const int u = (i8 / G) * 8 + xcd;              // unit (g, c) = (u % NKV, u / NKV)
-    const int g = u % NKV, c = u / NKV, h = g * G + i8 % G;
-    const int T = min(step[1] + 1, kMaxCtx), KVD = NKV * HD;
-    const int S = T <= kAttnChunk ? 1 : min(kAttnSplits, (T + kAttnChunk - 1) / kAttnChunk);
-    if (c >= S) return;                            // block-uniform (c < kAttnSplits, see launcher)
-    const int len = (T + S - 1) / S, p0 = c * len, p1 = min(T, p0 + len);   // p0 < p1 (see launcher)
-    const float* kg = kc + (size_t)g * HD;
-    const float* vg = vc + (size_t)g * HD;
+    const int tid = threadIdx.x;
     const int d0 = (tid % LPT) * DPL;
     float qv[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; e += 4) {
-        const sgpu_f32x4 a = *reinterpret_cast<const sgpu_f32x4*>(q + (size_t)h * HD + d0 + e);
+        const sgpu_f32x4 a = *reinterpret_cast<const sgpu_f32x4*>(qh + d0 + e);
 #pragma unroll
         for (int i = 0; i < 4; i++) qv[e + i] = a[i];
     }
@@ -244,6 +220,45 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
 #pragma unroll
         for (int s2 = 0; s2 < SLICES; s2++) tot += part[s2 * HD + d];
     }
+    m_out = m;
+    sum_out = sum;
+    return tot;
+}
+
+// Attention over T = pos + 1 cached positions, one 256-thread block per query head h and
+// position chunk c (the launcher's grid covers NKV x kAttnSplits units of G = NH/NKV heads).  T <= kAttnChunk: one chunk per head and
+// block (h, 0) computes the head as a whole (the other blocks exit).  Longer caches are cut
+// into S = ceil(T / kAttnChunk) <= kAttnSplits chunks; each block writes its chunk's partial
+// (max score m, sum of exp(s - m), the exp-weighted sum of V) to ws, and the last of the S
+// blocks of head h to finish (per-head counter in cnt, reset by that block) combines them in
+// chunk order: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M), M = max_c m_c.
+template <int HD>
+__device__ __forceinline__ void dec_attn(const float* __restrict__ q, const float* __restrict__ kc,
+                                         const float* __restrict__ vc, float* __restrict__ out,
+                                         const int* __restrict__ step, int NH, int NKV, float scale,
+                                         float* __restrict__ ws, unsigned* __restrict__ cnt) {
+    static_assert(HD == 32 || HD == 64 || HD == 128, "head dim");
+    constexpr int WSTRIDE = HD + 2;                // ws record: o[HD], m, l
+    __shared__ float sc[kAttnMaxLen];
+    __shared__ float red[4];
+    __shared__ float part[256];
+    __shared__ int last_s;
+    // Block b -> XCD b % 8 (blocks are dealt round-robin to the 8 XCDs).  The G query heads
+    // that share KV group g and chunk c get the same b % 8, so the chunk's K and V come from
+    // HBM once into that XCD's L2; units (g, c) are numbered chunk-major so chunk 0 of every
+    // group is dispatched first.
+    const int G = NH / NKV, tid = threadIdx.x;
+    const int xcd = blockIdx.x % 8, i8 = blockIdx.x / 8;
+    const int u = (i8 / G) * 8 + xcd;              // unit (g, c) = (u % NKV, u / NKV)
+    const int g = u % NKV, c = u / NKV, h = g * G + i8 % G;
+    const int T = min(step[1] + 1, kMaxCtx), KVD = NKV * HD;
+    const int S = T <= kAttnChunk ? 1 : min(kAttnSplits, (T + kAttnChunk - 1) / kAttnChunk);
+    if (c >= S) return;                            // block-uniform (c < kAttnSplits, see launcher)
+    const int len = (T + S - 1) / S, p0 = c * len, p1 = min(T, p0 + len);   // p0 < p1 (see launcher)
+    float m, sum;
+    const float tot = attn_chunk<HD>(q + (size_t)h * HD, kc + (size_t)g * HD, vc + (size_t)g * HD, KVD, p0, p1,
+                                     scale, sc, red, part, m, sum);
+    const int slice = tid / HD, d = tid % HD;
     if (S == 1) {
         if (slice == 0) out[(size_t)h * HD + d] = tot / sum;
         return;
@@ -307,6 +322,24 @@ __device__ __forceinline__ void amax_block256(float& bv, int& bi, float* sv, int
     bv = sv[0];
     bi = si[0];
     for (int i = 1; i < 4; i++) amax_merge(bv, bi, sv[i], si[i]);
+}
+
+// Causal attention for prompt rows: block (h, t) is query head h of prompt row t (position
+// pos0 + t, q rotated in place in the row's qkv vector of length QKVD), over cached positions
+// 0..pos0+t; output row t of out (NH*HD floats per row).
+template <int HD>
+__device__ __forceinline__ void pf_attn(const float* __restrict__ qkv, const float* __restrict__ kc,
+                                        const float* __restrict__ vc, float* __restrict__ out, int pos0, int NH,
+                                        int NKV, float scale, int QKVD) {
+    __shared__ float sc[kMaxCtx];
+    __shared__ float red[4];
+    __shared__ float part[256];
+    const int h = blockIdx.x, t = blockIdx.y, KVD = NKV * HD, g = h / (NH / NKV);
+    const int n = min(pos0 + t + 1, kMaxCtx);
+    float m, sum;
+    const float tot = attn_chunk<HD>(qkv + (size_t)t * QKVD + (size_t)h * HD, kc + (size_t)g * HD,
+                                     vc + (size_t)g * HD, KVD, 0, n, scale, sc, red, part, m, sum);
+    if (threadIdx.x < HD) out[(size_t)t * NH * HD + (size_t)h * HD + threadIdx.x] = tot / sum;
 }
 
 }  // namespace
@@ -397,6 +430,89 @@ __global__ void __launch_bounds__(256) sgpu_dec_argmax_final(const float* __rest
         if (idx == 0x7fffffff) idx = 0;
         step[0] = idx;
         if (out) out[step[1] + 1] = idx;
+    }
+}
+
+// ---- batched prompt prefill (T rows at positions pos0..pos0+T-1) ----
+
+// x[t] = h2f(emb[ids[t]]) for the T rows.
+__global__ void sgpu_pf_embed(const uint16_t* __restrict__ emb, const int* __restrict__ ids, int T,
+                              float* __restrict__ x, int C) {
+    const long long total = (long long)T * C;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += (long long)gridDim.x * blockDim.x) {
+        const int t = (int)(i / C), k = (int)(i % C);
+        x[i] = sgpu_h2f(emb[(size_t)ids[t] * C + k]);
+    }
+}
+
+// Y[t][n] = sum_k X[t][k] * h2f(W[n][k]) + bias?[n] on the fp32 matrix cores (one block per
+// 32-token x 32-row tile, grid-stride over tiles; blockDim 256, K % 4 == 0, 16-byte X rows).
+__global__ void __launch_bounds__(256) sgpu_pf_gemm(const uint16_t* __restrict__ W, const float* __restrict__ X,
+                                                    const float* __restrict__ bias, float* __restrict__ Y, int K,
+                                                    int N, int T) {
+    if (blockDim.x != 256) return;
+    sgpu::gemm_nt_mfma<1, WF16>(W, X, bias, Y, K, N, T);
+}
+
+// Per prompt row t (position pos0 + t) of the qkv matrix (rows of QKVD = (NH + 2*NKV)*HD):
+// RoPE on the q heads in place, RoPE on the k heads into the key cache, v into the value
+// cache (qwen_engine.c:227-230 order and rotation, the rope kernel's arithmetic).
+__global__ void sgpu_pf_qkv_post(float* __restrict__ qkv, int T, int pos0, const float* __restrict__ cosT,
+                                 const float* __restrict__ sinT, float* __restrict__ kc, float* __restrict__ vc,
+                                 int NH, int NKV, int HD) {
+#pragma clang fp contract(off)
+    const int hd2 = HD / 2, KVD = NKV * HD, QKVD = (NH + 2 * NKV) * HD;
+    const int per = (NH + NKV) * hd2 + KVD;          // work items per row: q pairs, k pairs, v
+    const long long total = (long long)T * per;
+    for (long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x; idx < total;
+         idx += (long long)gridDim.x * blockDim.x) {
+        const int t = (int)(idx / per), r = (int)(idx % per), pos = pos0 + t;
+        float* row = qkv + (size_t)t * QKVD;
+        if (r < (NH + NKV) * hd2) {
+            const int hh = r / hd2, i = r % hd2;     // heads 0..NH-1 are q, NH.. are k
+            const float a = row[hh * HD + i], b = row[hh * HD + hd2 + i];
+            const float c = cosT[(size_t)pos * hd2 + i], sn = sinT[(size_t)pos * hd2 + i];
+            const float o0 = a * c - b * sn, o1 = a * sn + b * c;
+            if (hh < NH) {
+                row[hh * HD + i] = o0;
+                row[hh * HD + hd2 + i] = o1;
+            } else {
+                float* kr = kc + (size_t)pos * KVD + (hh - NH) * HD;
+                kr[i] = o0;
+                kr[hd2 + i] = o1;
+            }
+        } else {
+            const int j = r - (NH + NKV) * hd2;
+            vc[(size_t)pos * KVD + j] = row[(NH + NKV) * HD + j];
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) sgpu_pf_attn64(const float* __restrict__ qkv, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, float* __restrict__ out, int pos0,
+                                                      int NH, int NKV, float scale, int QKVD) {
+    pf_attn<64>(qkv, kc, vc, out, pos0, NH, NKV, scale, QKVD);
+}
+__global__ void __launch_bounds__(256) sgpu_pf_attn32(const float* __restrict__ qkv, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, float* __restrict__ out, int pos0,
+                                                      int NH, int NKV, float scale, int QKVD) {
+    pf_attn<32>(qkv, kc, vc, out, pos0, NH, NKV, scale, QKVD);
+}
+__global__ void __launch_bounds__(256) sgpu_pf_attn128(const float* __restrict__ qkv, const float* __restrict__ kc,
+                                                       const float* __restrict__ vc, float* __restrict__ out, int pos0,
+                                                       int NH, int NKV, float scale, int QKVD) {
+    pf_attn<128>(qkv, kc, vc, out, pos0, NH, NKV, scale, QKVD);
+}
+
+// G[t][i] = silu(Y[t][i]) * Y[t][FC + i] for gate|up rows of 2*FC (the swiglu kernel's
+// arithmetic, qwen_kernels.cu:119-126).
+__global__ void sgpu_pf_swiglu(const float* __restrict__ Y, float* __restrict__ G, int FC, int T) {
+#pragma clang fp contract(off)
+    const long long total = (long long)T * FC;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total; i += (long long)gridDim.x * blockDim.x) {
+        const int t = (int)(i / FC), k = (int)(i % FC);
+        const float gv = Y[(size_t)t * 2 * FC + k];
+        G[i] = (gv / (1.0f + expf(-gv))) * Y[(size_t)t * 2 * FC + FC + k];
     }
 }
 

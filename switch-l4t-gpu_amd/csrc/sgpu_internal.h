@@ -33,6 +33,18 @@ SGPU_HIDDEN int sgpu_internal_dec_embed_next(const uint16_t *emb, float *x, int 
 #define SGPU_ARGMAX_PARTS 256
 SGPU_HIDDEN int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
                                          void *stream);
+/* Batched prompt prefill of the Qwen engine (qwen.c sgpu_qwen_prefill): row embedding, the
+ * fp16-weight matrix-core GEMM Y[T][N] = X[T][K] W[N][K]^T + bias, RoPE of q in place and
+ * of k into the key cache with v into the value cache, causal attention of T prompt rows
+ * (positions pos0..pos0+T-1, pos0 + T <= 8192), and row SwiGLU over gate|up rows of 2*FC. */
+SGPU_HIDDEN int sgpu_internal_pf_embed(const uint16_t *emb, const int *ids, int T, float *x, int C, void *stream);
+SGPU_HIDDEN int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, float *Y, int K, int N,
+                                      int T, void *stream);
+SGPU_HIDDEN int sgpu_internal_pf_qkv_post(float *qkv, int T, int pos0, const float *cosT, const float *sinT,
+                                          float *kc, float *vc, int NH, int NKV, int HD, void *stream);
+SGPU_HIDDEN int sgpu_internal_pf_attn(const float *qkv, const float *kc, const float *vc, float *out, int T,
+                                      int pos0, int NH, int NKV, int HD, float scale, void *stream);
+SGPU_HIDDEN int sgpu_internal_pf_swiglu(const float *Y, float *G, int FC, int T, void *stream);
 /* GPT-2 fused decode (fp32 weights), see gpt2.c. */
 SGPU_HIDDEN int sgpu_internal_g2_qkv(const float *W, int K, int N, const float *x, const float *lnw,
                                      const float *lnb, float eps, const float *bias, float *q, float *kc,

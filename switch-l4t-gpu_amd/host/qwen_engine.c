@@ -7,7 +7,7 @@
  *
  * Usage: qwen_engine (--weights FILE | --random SEED) [--ids FILE | --prompt-random N]
  *                    [--gen N] [--greedy] [--serve] [--json] [--write-weights FILE]
- *                    [--path reference|fused|graph]
+ *                    [--path reference|fused|graph] [--batch-prefill]
  *   --weights        flat file in the qwen_engine.c:8-16 layout (conv_qwen.py writer)
  *   --random SEED    random-init model: every fp16 tensor N(0, 0.02), RoPE theta 1e6 tables
  *   --ids FILE       u32 count + u32 ids (qwen_engine.c:477-486)
@@ -17,6 +17,8 @@
  *   --write-weights F  write the model (loaded or random-init) as a flat file in the same
  *                    layout and exit without touching the device (the writer role of
  *                    conv_qwen.py:63-99)
+ *   --batch-prefill  prime the cache with all prompt positions in one batched pass
+ *                    (sgpu_qwen_prefill) instead of one position at a time
  *   --path P         reference: the gpu_forward launch sequence (qwen_engine.c:205-269);
  *                    fused: five kernels per layer; graph (default): those replayed as a HIP
  *                    graph.  Same tokens on every path.
@@ -93,7 +95,7 @@ int main(int argc, char **argv) {
     setvbuf(stdout, NULL, _IONBF, 0);
     const char *weights = NULL, *ids_file = NULL, *write_weights = NULL;
     long long seed = -1;
-    int n_gen = 24, prompt_random = 0, serve = 0, json = 0, path = SGPU_QWEN_PATH_GRAPH;
+    int n_gen = 24, prompt_random = 0, serve = 0, json = 0, batch = 0, path = SGPU_QWEN_PATH_GRAPH;
     for (int i = 1; i < argc; i++) {
         if (!strcmp(argv[i], "--weights") && i + 1 < argc) weights = argv[++i];
         else if (!strcmp(argv[i], "--random") && i + 1 < argc) seed = atoll(argv[++i]);
@@ -104,6 +106,7 @@ int main(int argc, char **argv) {
         else if (!strcmp(argv[i], "--greedy")) { /* always greedy */ }
         else if (!strcmp(argv[i], "--serve")) serve = 1;
         else if (!strcmp(argv[i], "--json")) json = 1;
+        else if (!strcmp(argv[i], "--batch-prefill")) batch = 1;
         else if (!strcmp(argv[i], "--path") && i + 1 < argc) {
             const char *v = argv[++i];
             if (!strcmp(v, "reference")) path = SGPU_QWEN_PATH_REFERENCE;
@@ -180,7 +183,10 @@ int main(int argc, char **argv) {
     fprintf(log, "prompt: %d token(s)\n", total);
 
     double tp = now_s();
-    for (int p = 0; p < total; p++) CHK(sgpu_qwen_forward(eng, ids[p], p, p == total - 1, logits));
+    if (batch)
+        CHK(sgpu_qwen_prefill(eng, ids, total, logits));
+    else
+        for (int p = 0; p < total; p++) CHK(sgpu_qwen_forward(eng, ids[p], p, p == total - 1, logits));
     double prime_s = now_s() - tp;
     fprintf(log, "primed %d prompt token(s) in %.1f ms\n", total, prime_s * 1e3);
 

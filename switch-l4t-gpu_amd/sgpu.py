@@ -111,6 +111,7 @@ _SIGS = {
     "sgpu_qwen_device_logits": (_P, [_P]),
     "sgpu_qwen_set_path": (_I, [_P, _I]),
     "sgpu_qwen_generate": (_I, [_P, _P, _I, _I, _P]),
+    "sgpu_qwen_prefill": (_I, [_P, _P, _I, _P]),
     "sgpu_gen_sgemm_inputs": (None, [_P, _P, _S, ct.c_uint]),
     "sgpu_frand": (_F, [ct.POINTER(ct.c_uint64)]),
     "sgpu_gen_uniform": (None, [_P, _S, ct.POINTER(ct.c_uint64), _F]),
@@ -328,6 +329,12 @@ class QwenEngine:
         call("sgpu_qwen_forward", self.h, token, pos, int(want_logits),
              self.logits.ctypes.data if want_logits else None)
         return self.logits if want_logits else None
+
+    def prefill(self, ids) -> np.ndarray:
+        """Positions 0..len(ids)-1 in one batched pass; logits of the last row."""
+        a = np.ascontiguousarray(ids, np.int32)
+        call("sgpu_qwen_prefill", self.h, a.ctypes.data, a.size, self.logits.ctypes.data)
+        return self.logits
 
     def close(self):
         if self.h:

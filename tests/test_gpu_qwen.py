@@ -153,6 +153,46 @@ def test_engine_long_context_fused(gpu, og, case):
     eng.close()
 
 
+# Batched prefill (sgpu_qwen_prefill): the last prompt row's logits, then five decoded
+# positions that read the cache the prefill wrote, against the CPU golden run position by
+# position.  Prompts past 512 rows are prefilled in chunks that attend to earlier chunks
+# through the cache.
+PREFILL = [dict(cfg=SMALL, T=1), dict(cfg=SMALL, T=7), dict(cfg=SMALL, T=40),
+           dict(cfg=dict(V=300, C=128, NL=2, NH=4, NKV=2, HD=32, FC=256, CTX=1100), T=1030),
+           dict(cfg=dict(V=300, C=256, NL=1, NH=2, NKV=1, HD=128, FC=512, CTX=600), T=520)]
+
+
+@pytest.mark.parametrize("case", PREFILL, ids=["t1", "t7", "t40", "chunked-hd32", "chunked-hd128"])
+def test_engine_prefill_matches_golden(gpu, og, case):
+    cfg, T = case["cfg"], case["T"]
+    say(f"qwen prefill T={T} cfg={cfg}")
+    blob = gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=51, std=0.15)
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob, PATHS["fused"])
+    gold = og.QwenGolden(og.qwen_cfg(**cfg), blob, NT)
+    ids = [int(v) for v in np.random.default_rng(T).integers(0, cfg["V"], T + 5)]
+    got = eng.prefill(ids[:T]).copy()
+    for p in range(T):
+        want = gold.forward(ids[p], p, p == T - 1)
+    rows = [(T - 1, got, want)]
+    for p in range(T, T + 5):
+        rows.append((p, eng.forward(ids[p], p, True).copy(), gold.forward(ids[p], p, True)))
+    for p, g, w in rows:
+        scale = np.abs(w).max()
+        assert np.abs(g - w).max() <= 1e-4 * scale, (p, np.abs(g - w).max(), scale)
+        assert int(np.argmax(g)) == og.argmax(w), p
+    eng.close()
+
+
+def test_engine_prefill_rejects_bad_ids(gpu):
+    cfg = SMALL
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=3), PATHS["fused"])
+    with pytest.raises(gpu.SgpuError):
+        eng.prefill([1, cfg["V"]])
+    with pytest.raises(gpu.SgpuError):
+        eng.prefill([1] * (cfg["CTX"] + 1))
+    eng.close()
+
+
 @pytest.mark.parametrize("path", ["reference", "graph"])
 def test_engine_small_generate(gpu, og, path):
     """sgpu_qwen_generate (on-device argmax loop for the graph path) gives the CPU golden's
@@ -231,14 +271,14 @@ def test_engine_full_greedy_token_identical(gpu, og):
 def test_engine_cli_json(gpu):
     exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
     runs = {}
-    for path in ("reference", "graph"):
-        out = subprocess.run([exe, "--random", "7", "--prompt-random", "8", "--gen", "6", "--json", "--path", path],
-                             capture_output=True, text=True, timeout=300)
+    for path, extra in (("reference", []), ("graph", []), ("graph", ["--batch-prefill"])):
+        out = subprocess.run([exe, "--random", "7", "--prompt-random", "8", "--gen", "6", "--json", "--path", path]
+                             + extra, capture_output=True, text=True, timeout=300)
         assert out.returncode == 0, out.stderr
         d = json.loads(out.stdout.strip().splitlines()[-1])
         assert d["done"] and d["tok_s"] > 0
-        runs[path] = d["ids"]
-    assert runs["reference"] == runs["graph"]
+        runs[path + "".join(extra)] = d["ids"]
+    assert runs["reference"] == runs["graph"] == runs["graph--batch-prefill"]
 
 
 def test_engine_serve_protocol(gpu):
