@@ -53,7 +53,7 @@ static int argmax(const float *v, int n) {
     return b;
 }
 
-static void serve_loop(sgpu_qwen *eng, const sgpu_qwen_cfg *cfg, float *logits) {
+static void serve_loop(sgpu_qwen *eng, const sgpu_qwen_cfg *cfg, float *logits, int batch) {
     const int CTX = cfg->CTX;
     int *buf = malloc(sizeof(int) * (size_t)CTX);
     uint32_t *tmp = malloc(sizeof(uint32_t) * (size_t)CTX * 2);
@@ -69,7 +69,10 @@ static void serve_loop(sgpu_qwen *eng, const sgpu_qwen_cfg *cfg, float *logits) 
         if (fread(&maxg, 4, 1, stdin) != 1) break;
         if (T == 0) { uint32_t z = 0; fwrite(&z, 4, 1, stdout); fflush(stdout); continue; }
         if (maxg > (uint32_t)CTX - T - 2) maxg = (uint32_t)CTX - T - 2;
-        for (uint32_t p = 0; p < T; p++) CHK(sgpu_qwen_forward(eng, buf[p], (int)p, p == T - 1, logits));
+        if (batch)
+            CHK(sgpu_qwen_prefill(eng, buf, (int)T, logits));
+        else
+            for (uint32_t p = 0; p < T; p++) CHK(sgpu_qwen_forward(eng, buf[p], (int)p, p == T - 1, logits));
         int total = (int)T;
         int nxt = argmax(logits, cfg->V);
         buf[total++] = nxt;
@@ -152,7 +155,7 @@ int main(int argc, char **argv) {
     free(blob);
     float *logits = malloc(sizeof(float) * (size_t)cfg.V);
     if (serve) {
-        serve_loop(eng, &cfg, logits);
+        serve_loop(eng, &cfg, logits, batch);
         sgpu_qwen_destroy(eng);
         return 0;
     }

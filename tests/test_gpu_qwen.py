@@ -291,14 +291,19 @@ def test_engine_serve_protocol(gpu):
     exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
     reqs = [([5, 17, 9000, 151000, 42], 6), ([123] * 3 + [7], 4)]
     payload = b"".join(struct.pack(f"<I{len(ids)}II", len(ids), *ids, g) for ids, g in reqs)
-    out = subprocess.run([exe, "--random", "7", "--serve"], input=payload, capture_output=True, timeout=300)
-    assert out.returncode == 0, out.stderr.decode()
-    buf, off, got = out.stdout, 0, []
-    for _ in reqs:
-        (m,) = struct.unpack_from("<I", buf, off)
-        got.append(list(struct.unpack_from(f"<{m}I", buf, off + 4)))
-        off += 4 + 4 * m
-    assert off == len(buf)
+    answers = []
+    for extra in ([], ["--batch-prefill"]):
+        out = subprocess.run([exe, "--random", "7", "--serve"] + extra, input=payload, capture_output=True,
+                             timeout=300)
+        assert out.returncode == 0, out.stderr.decode()
+        buf, off, got = out.stdout, 0, []
+        for _ in reqs:
+            (m,) = struct.unpack_from("<I", buf, off)
+            got.append(list(struct.unpack_from(f"<{m}I", buf, off + 4)))
+            off += 4 + 4 * m
+        assert off == len(buf)
+        answers.append(got)
+    assert answers[0] == answers[1]
     cfg = gpu.qwen_default_cfg()
     eng = gpu.QwenEngine(cfg, gpu.qwen_random_blob(cfg, seed=7, std=0.02), 2)
     for (ids, g), resp in zip(reqs, got):
