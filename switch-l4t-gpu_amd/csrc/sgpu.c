@@ -508,6 +508,12 @@ static void pick_tuned(const devstate *d, int K, int N, int vec, int *li, int *s
         if (g_segs[j] >= s) { *li = best_l; *si = j; return; }
 }
 
+/* Grid cap of the persistent tuned GEMVs (blocks per CU), reached only by lm_head-sized row
+ * counts.  Measured on the lm_head shapes with rotating weight copies: fp16 [151936 x 896]
+ * peaks at 18 blocks per CU (86.2% of HBM; 84.0% at 8), fp32 [50257 x 768] at 4 (81.5%;
+ * 80.3% at 8) -- its lanes keep 1.7x more bytes in flight. */
+static unsigned gemv_blocks_per_cu(int is_h) { return is_h ? 18u : 4u; }
+
 static int gemv_launch(int generic_kid, int is_h, const void *W, const float *x, const float *bias, float *y,
                        int K, int N, void *stream) {
     if (K < 0 || N < 0) return SGPU_ERR_INVALID_ARG;
@@ -523,7 +529,7 @@ static int gemv_launch(int generic_kid, int is_h, const void *W, const float *x,
     const int aligned = ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0;
     if (li >= 0 && aligned) {
         const int teams = 256 / g_lpr[li];
-        unsigned g[3] = {umin(cdiv(N, teams), (unsigned)d->cus * 8u), 1, 1}, b[3] = {256, 1, 1};
+        unsigned g[3] = {umin(cdiv(N, teams), (unsigned)d->cus * gemv_blocks_per_cu(is_h)), 1, 1}, b[3] = {256, 1, 1};
         return launch(is_h ? d->gemv_h[li][si] : d->gemv_f32[li][si], g, b, stream, args);
     }
     unsigned g[3], b[3];
@@ -870,7 +876,9 @@ static int dec_launch_team(devstate *d, int fam, int K, int nteams, void **args,
     const int j = dec_pick(d, K, nteams, n_entries, dec_vec(fam));
     if (j < 0) return SGPU_ERR_INVALID_ARG;
     const unsigned teams = 256u / (unsigned)g_dec_cfg[j][0];
-    unsigned g[3] = {umin(cdiv(nteams, teams), (unsigned)d->cus * 8u), 1, 1}, b[3] = {256, 1, 1};
+    /* the fp16 lm_head runs the measured 16-lane, 7-segment configuration; the rest keep 8 */
+    const unsigned per_cu = fam == DEC_LMHEAD ? gemv_blocks_per_cu(1) : 8u;
+    unsigned g[3] = {umin(cdiv(nteams, teams), (unsigned)d->cus * per_cu), 1, 1}, b[3] = {256, 1, 1};
     return launch(d->dec[fam][j], g, b, stream, args);
 }
 
