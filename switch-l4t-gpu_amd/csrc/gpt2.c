@@ -311,12 +311,13 @@ int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *
     return want_logits ? logits_out(e, e->x, logits_host) : SGPU_OK;
 }
 
-int sgpu_gpt2_prefill(sgpu_gpt2 *e, const int *ids, int T, float *logits_host) {
-    if (!e || !ids) return SGPU_ERR_INVALID_ARG;
+/* gpu_prefill's layer loop: all T prompt rows through each layer, cache positions 0..T-1
+ * filled, the final rows left in xT.  Attention: the reference's per-row launches (k/v copies,
+ * scores, softmax, mix for each row), or -- with the cache within 8192 positions -- two
+ * strided copies of every row's k and v into the caches and one launch of the batched causal
+ * attention (one block per head and row, same arithmetic as the fused decode attention). */
+static int prefill_layers(sgpu_gpt2 *e, const int *ids, int T) {
     const sgpu_gpt2_cfg *c = &e->cfg;
-    if (T <= 0 || T > c->CTX) return SGPU_ERR_INVALID_ARG;
-    for (int t = 0; t < T; t++)
-        if (ids[t] < 0 || ids[t] >= c->V) return SGPU_ERR_INVALID_ARG;
     const int C = c->C, FC = c->FC;
     const float eps = c->eps, scale = 0.125f;
     void *s = (void *)e->stream;
@@ -329,13 +330,24 @@ int sgpu_gpt2_prefill(sgpu_gpt2 *e, const int *ids, int T, float *logits_host) {
         const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
         TRY(sgpu_layernorm(e->xT, b + e->L.ln1w, b + e->L.ln1b, e->ln1T, C, eps, T, s));
         TRY(sgpu_gemv_multi(b + e->L.qkvw, e->ln1T, b + e->L.qkvb, e->qkvT, C, 3 * C, T, s));
-        for (int t = 0; t < T; t++) {     /* causal attention, one query row at a time */
-            const float *qrow = e->qkvT + (size_t)t * 3 * C;
-            TRY(sgpu_memcpy_dtod_async(e->kc[l] + (size_t)t * C, qrow + C, (size_t)C * 4, s));
-            TRY(sgpu_memcpy_dtod_async(e->vc[l] + (size_t)t * C, qrow + 2 * C, (size_t)C * 4, s));
-            TRY(sgpu_gpt2_attn_scores(qrow, e->kc[l], e->scores, t + 1, scale, s));
-            TRY(sgpu_gpt2_attn_softmax(e->scores, e->probs, t + 1, s));
-            TRY(sgpu_gpt2_attn_mix(e->probs, e->vc[l], e->attT + (size_t)t * C, t + 1, s));
+        if (T <= 8192) {
+            const size_t row = (size_t)C * 4, qrow = 3 * row;
+            hipError_t he = hipMemcpy2DAsync(e->kc[l], row, e->qkvT + C, qrow, row, (size_t)T, hipMemcpyDeviceToDevice,
+                                             e->stream);
+            if (he == hipSuccess)
+                he = hipMemcpy2DAsync(e->vc[l], row, e->qkvT + 2 * C, qrow, row, (size_t)T, hipMemcpyDeviceToDevice,
+                                      e->stream);
+            if (he != hipSuccess) return (int)he;
+            TRY(sgpu_internal_pf_attn(e->qkvT, e->kc[l], e->vc[l], e->attT, T, 0, c->NH, c->NH, c->HD, scale, s));
+        } else {
+            for (int t = 0; t < T; t++) {     /* causal attention, one query row at a time */
+                const float *qrow = e->qkvT + (size_t)t * 3 * C;
+                TRY(sgpu_memcpy_dtod_async(e->kc[l] + (size_t)t * C, qrow + C, (size_t)C * 4, s));
+                TRY(sgpu_memcpy_dtod_async(e->vc[l] + (size_t)t * C, qrow + 2 * C, (size_t)C * 4, s));
+                TRY(sgpu_gpt2_attn_scores(qrow, e->kc[l], e->scores, t + 1, scale, s));
+                TRY(sgpu_gpt2_attn_softmax(e->scores, e->probs, t + 1, s));
+                TRY(sgpu_gpt2_attn_mix(e->probs, e->vc[l], e->attT + (size_t)t * C, t + 1, s));
+            }
         }
         TRY(sgpu_gemv_multi(b + e->L.aow, e->attT, b + e->L.aob, e->yT, C, C, T, s));
         TRY(sgpu_add2(e->xT, e->yT, e->xT, T * C, s));
@@ -346,7 +358,17 @@ int sgpu_gpt2_prefill(sgpu_gpt2 *e, const int *ids, int T, float *logits_host) {
         TRY(sgpu_add2(e->xT, e->yT, e->xT, T * C, s));
     }
 #undef TRY
-    return logits_out(e, e->xT + (size_t)(T - 1) * C, logits_host);
+    return SGPU_OK;
+}
+
+int sgpu_gpt2_prefill(sgpu_gpt2 *e, const int *ids, int T, float *logits_host) {
+    if (!e || !ids) return SGPU_ERR_INVALID_ARG;
+    const sgpu_gpt2_cfg *c = &e->cfg;
+    if (T <= 0 || T > c->CTX) return SGPU_ERR_INVALID_ARG;
+    for (int t = 0; t < T; t++)
+        if (ids[t] < 0 || ids[t] >= c->V) return SGPU_ERR_INVALID_ARG;
+    int rc = prefill_layers(e, ids, T);
+    return rc ? rc : logits_out(e, e->xT + (size_t)(T - 1) * c->C, logits_host);
 }
 
 int sgpu_gpt2_generate(sgpu_gpt2 *e, const int *prompt, int T, int n_gen, int *out_tokens) {
@@ -371,8 +393,15 @@ int sgpu_gpt2_generate(sgpu_gpt2 *e, const int *prompt, int T, int n_gen, int *o
         free(logits);
         return rc;
     }
-    for (int p = 0; p < T; p++)
-        if ((rc = forward_fused(e, prompt[p], p, p == T - 1, NULL))) return rc;
+    /* the prompt in one batched pass; the last row through the fused lm_head, and the step
+     * record {prompt[T-1], T-1} so the on-device loop continues at position T */
+    if ((rc = prefill_layers(e, prompt, T))) return rc;
+    if ((rc = sgpu_memcpy_dtod_async(e->x, e->xT + (size_t)(T - 1) * c->C, (size_t)c->C * 4, (void *)e->stream)) ||
+        (rc = fused_lm_head(e)))
+        return rc;
+    const int st[2] = {prompt[T - 1], T - 1};
+    hipError_t hs = hipMemcpyAsync(e->d_step, st, sizeof st, hipMemcpyHostToDevice, e->stream);
+    if (hs != hipSuccess) return (int)hs;
     if ((rc = sgpu_internal_dec_argmax(e->logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
                                        (void *)e->stream)))
         return rc;
