@@ -108,7 +108,7 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
-/* The sgemm_opt256 member alone (any shape; bounds-checked path off whole tiles).  No
+/* The sgemm_opt256 member alone (any shape; masked loads on edge tiles).  No
  * counterpart in the reference: an added member of the same family, with the same
  * (A, B, C, M, N, K) symbol arguments, for hosts that launch members by name. */
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream);

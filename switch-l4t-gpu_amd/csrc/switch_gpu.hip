@@ -127,7 +127,8 @@ __device__ __forceinline__ void sgemm_store_c(float* __restrict__ C, int M, int 
 // k-step's LDS operands are read one step ahead into a second register set, so their
 // latency runs under the previous step's MFMAs; slice kt+1 is written to the idle LDS buffer
 // after MFMA step STORE_AT of slice kt, once its loads have had that long to land.  One
-// barrier per slice.  Same MFMA sequence per accumulator as the generic path.
+// barrier per slice.  (Edge tiles of the same member run the m-major masked pipeline, whose
+// k order inside each 8-deep group differs, so their sums round independently of these.)
 template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT>
 __device__ __forceinline__ void sgemm_tile_fast(const float* __restrict__ A, const float* __restrict__ B,
                                                 int N, int K, int m0, int n0,
@@ -434,26 +435,6 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
     // loop, so neither carries the other's registers.
     {
         const bool kfast = aligned && K % BK == 0 && K >= 2 * BK;
-        if (kfast) {
-            for (int t = sgpu_bid(); t < ntiles; t += nb) {
-                int tm, tn;
-                sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
-                const int m0 = tm * BM, n0 = tn * BN;
-                if (m0 + BM > M || n0 + BN > N) continue;
-                sgpu_f32x16 acc[T::FM][T::FN];
-#pragma unroll
-                for (int i = 0; i < T::FM; i++)
-#pragma unroll
-                    for (int j = 0; j < T::FN; j++)
-#pragma unroll
-                        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-                if constexpr (LAYOUT >= 1)
-                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT == 2>(A, B, M, N, K, m0, n0, LU.m, th, acc);
-                else
-                    sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
-                sgemm_store_c(C, M, N, m0, n0, true, th, acc);
-            }
-        }
         constexpr int SG = STORE_AT < BK / 8 ? STORE_AT : 0;      // a group index for the masked path
         // Buffer-load windows (BM rows of A, BK rows of B) within 2^31 bytes: MODE 1, else 2.
         // Each mode has its own tile loop (one accumulator set per loop, no merge of the two).
@@ -478,10 +459,32 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                 sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
             }
         };
+        // Masked tiles first, then interior tiles: with this order the interior loop's code
+        // measured 7% faster on sgemm_tiled4 at 4096^3 (1% on sgemm_opt).
         if (win)
             masked_tiles(std::integral_constant<int, 1>{});
         else
             masked_tiles(std::integral_constant<int, 2>{});
+        if (kfast) {
+            for (int t = sgpu_bid(); t < ntiles; t += nb) {
+                int tm, tn;
+                sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+                const int m0 = tm * BM, n0 = tn * BN;
+                if (m0 + BM > M || n0 + BN > N) continue;
+                sgpu_f32x16 acc[T::FM][T::FN];
+#pragma unroll
+                for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                    for (int j = 0; j < T::FN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+                if constexpr (LAYOUT >= 1)
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT == 2>(A, B, M, N, K, m0, n0, LU.m, th, acc);
+                else
+                    sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
+                sgemm_store_c(C, M, N, m0, n0, true, th, acc);
+            }
+        }
     }
 }
 
