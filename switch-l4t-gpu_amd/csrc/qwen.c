@@ -382,17 +382,25 @@ int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *
  * layer's weights stream once per chunk of up to PF_ROWS rows instead of once per position ---- */
 #define PF_ROWS 512
 
+/* Allocated on the first prefill and kept; a failed call leaves the buffers it did get in
+ * place (freed with the engine) and the next call allocates only the missing ones. */
 static int pf_alloc(sgpu_qwen *e) {
-    if (e->d_pf_x) return SGPU_OK;
     const sgpu_qwen_cfg *c = &e->cfg;
     const size_t R = PF_ROWS, C = (size_t)c->C, FC = (size_t)c->FC, Q = (size_t)e->L.qkvd;
     const size_t ybig = 2 * FC > C ? 2 * FC : C;
-    int rc;
-    if ((rc = dalloc((void **)&e->d_pf_ids, (size_t)c->CTX * sizeof(int), NULL)) ||
-        (rc = dalloc((void **)&e->d_pf_xn, R * C * 4, NULL)) || (rc = dalloc((void **)&e->d_pf_qkv, R * Q * 4, NULL)) ||
-        (rc = dalloc((void **)&e->d_pf_att, R * C * 4, NULL)) || (rc = dalloc((void **)&e->d_pf_y, R * ybig * 4, NULL)) ||
-        (rc = dalloc((void **)&e->d_pf_g, R * FC * 4, NULL)) || (rc = dalloc((void **)&e->d_pf_x, R * C * 4, NULL)))
-        return rc;
+    struct { void **p; size_t bytes; } need[] = {
+        {(void **)&e->d_pf_ids, (size_t)c->CTX * sizeof(int)}, {(void **)&e->d_pf_x, R * C * 4},
+        {(void **)&e->d_pf_xn, R * C * 4}, {(void **)&e->d_pf_qkv, R * Q * 4}, {(void **)&e->d_pf_att, R * C * 4},
+        {(void **)&e->d_pf_y, R * ybig * 4}, {(void **)&e->d_pf_g, R * FC * 4}};
+    for (size_t i = 0; i < sizeof need / sizeof need[0]; i++) {
+        if (*need[i].p) continue;
+        int rc = dalloc(need[i].p, need[i].bytes, NULL);
+        if (rc) {                      /* allocated but not cleared: give it back */
+            sgpu_free(*need[i].p);
+            *need[i].p = NULL;
+            return rc;
+        }
+    }
     return SGPU_OK;
 }
 
