@@ -16,8 +16,9 @@
 // fp32 accumulate; no reduced-precision xf32).  A block of 64*WGM*WGN threads owns a BMxBN
 // tile of C; each wave owns a (BM/WGM)x(BN/WGN) sub-tile held as 32x32 MFMA blocks.
 // A and B k-slices of depth BK are staged through LDS, double-buffered (one barrier per
-// slice): A either k-major with a 2-float row pad or m-major with a 4-float pad, B row-major
-// with a pad.  Tiles are walked with a grid-stride loop over a linear tile index, so any
+// slice; in the large members it sits before the slice's last MFMA group, so the next
+// slice's first operand reads overlap that group): A either k-major with a 2-float row pad
+// or m-major with a 4-float pad, B row-major with a pad.  Tiles are walked with a grid-stride loop over a linear tile index, so any
 // grid of 64*WGM*WGN-thread blocks is correct (surplus blocks exit); with one block per tile
 // the index is remapped so each XCD (blocks are dealt round-robin to the 8 XCDs) works on a
 // compact group of tiles that shares A and B panels in its own L2.
@@ -216,7 +217,7 @@ struct SgemmLdsM {
 //   is applied to data.  Floats are written to LDS one each.
 //   MODE 2 (larger operands): dwordx4-shaped map, each float loaded from a clamped
 //   (in-bounds) 64-bit address and zeroed outside A or B when the slice is written to LDS.
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false, int MODE = 0>
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false, int MODE = 0, bool EARLY = false>
 __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, const float* __restrict__ B,
                                                   int M, int N, int K, int m0, int n0,
                                                   SgemmLdsM<BM, BN, BK, WGM, WGN>& L,
@@ -227,6 +228,7 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     constexpr int NG = BK / 8;                    // 4-step groups per slice
     static_assert(BK % 8 == 0, "k slice of whole 8-deep groups");
     static_assert(STORE_G >= 0 && STORE_G < NG, "store point inside the slice");
+    static_assert(!EARLY || (STORE_G < NG - 1 && NG % 2 == 0), "early barrier: store before the last group");
     static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
     static_assert(MODE != 1 || (T::NT % BK == 0 && T::NT % BN == 0), "lane map: whole rows per round");
     constexpr int AE = 4 * T::A_PER_T, BE = 4 * T::B_PER_T;   // staged floats per thread
@@ -334,6 +336,12 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     // SPREAD: the slice's memory instructions (next slice's global loads in group 0, next
     // group's LDS reads, the slice store in group STORE_G) are dealt out one per MFMA instead
     // of issued in bursts, so the MFMA stream never waits behind a full memory queue.
+    // EARLY: the slice's barrier sits before its last group instead of after it, and that
+    // group's MFMAs run under the LDS reads of the next slice's first group (the next slice
+    // was stored at group STORE_G < NG-1; every read of this slice's buffer except the last
+    // group's was issued, and waited for, before the barrier), so no LDS latency is exposed
+    // between slices.
+    sgpu_f32x4 a[2][T::FM], b[2][T::FN];
     auto slice = [&](int s, int kt_next, auto more_c) __attribute__((always_inline)) {
         constexpr bool more = decltype(more_c)::value;
         constexpr int NMF = 4 * T::FM * T::FN;
@@ -341,20 +349,25 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
         constexpr int LPM = (NLD + NMF - 1) / NMF;                            // ... per MFMA slot
         constexpr int NST = (MODE == 1 ? 4 : 1) * (T::A_PER_T + T::B_PER_T);  // LDS writes
         constexpr int WPM = (NST + NMF / 2 - 1) / (NMF / 2);                  // ... per slot (half group)
-        sgpu_f32x4 a[2][T::FM], b[2][T::FN];
         if constexpr (!SPREAD) {
             if (more) load_slice(kt_next);
             __builtin_amdgcn_sched_barrier(0);
         }
-        read_group(s, 0, a[0], b[0]);
+        if constexpr (!EARLY) read_group(s, 0, a[0], b[0]);
         if constexpr (SPREAD) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
             const int c = g & 1;
+            constexpr bool rd_next = EARLY && more;    // last group reads the next slice's group 0
+            if (rd_next && g == NG - 1) {
+                __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+            }
             if constexpr (SPREAD) {
                 if (more && g == 0) load_slice(kt_next);
             }
             if (g + 1 < NG) read_group(s, g + 1, a[c ^ 1], b[c ^ 1]);
+            else if (rd_next) read_group(s ^ 1, 0, a[c ^ 1], b[c ^ 1]);
             if constexpr (!SPREAD) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < 4; t++)
@@ -373,7 +386,7 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // 1 MFMA
                     if (more && g == 0 && q * LPM < NLD)
                         __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);            // global loads
-                    if (g + 1 < NG && q < T::FM + 4 * T::FN)
+                    if ((g + 1 < NG || rd_next) && q < T::FM + 4 * T::FN)
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // 1 LDS read
                     if (more && g == STORE_G && q >= NMF / 2 && (q - NMF / 2) * WPM < NST)
                         __builtin_amdgcn_sched_group_barrier(0x200, WPM, 0);            // LDS writes
@@ -387,9 +400,10 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     if constexpr (MASKED) mask_slice(0);
     store_slice(0);
     __syncthreads();
+    if constexpr (EARLY) read_group(0, 0, a[0], b[0]);
     for (int kt = 0; kt + 1 < nk; kt++) {
         slice(kt & 1, kt + 1, std::true_type{});
-        __syncthreads();
+        if constexpr (!EARLY) __syncthreads();
     }
     slice((nk - 1) & 1, 0, std::false_type{});
     __syncthreads();
@@ -407,9 +421,11 @@ template <int BM, int BN, int BK, int WGM, int WGN>
 __device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLdsU<BM, BN, BK, WGM, WGN>& u) { return u.k; }
 
 // Whole tiles of a problem with 16-byte rows and K whole slices run the dwordx4 pipeline
-// with the slice store after k-step (LAYOUT 0) or 4-step group (LAYOUT 1, 2) STORE_AT;
+// with the slice store after k-step (LAYOUT 0) or 4-step group (LAYOUT 1-3) STORE_AT;
 // LAYOUT 0: k-major A staging; 1: m-major A staging; 2: m-major with memory instructions
-// spread one per MFMA.  All other tiles run the masked m-major pipeline.
+// spread one per MFMA; 3: as 2, with each slice's barrier moved before its last group.
+// All other tiles run the masked m-major pipeline (spread for LAYOUT 2 and 3, barrier at
+// the end of the slice).
 template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT, int LAYOUT>
 __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const float* __restrict__ B,
                                            float* __restrict__ C, int M, int N, int K) {
@@ -455,7 +471,8 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
                 if (K > 0)
-                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, SG, LAYOUT == 2, MODE>(A, B, M, N, K, m0, n0, LU.m, th, acc);
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, SG, LAYOUT >= 2, MODE, false>(
+                        A, B, M, N, K, m0, n0, LU.m, th, acc);
                 sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
             }
         };
@@ -479,7 +496,8 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
                 if constexpr (LAYOUT >= 1)
-                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT == 2>(A, B, M, N, K, m0, n0, LU.m, th, acc);
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT >= 2, 0, LAYOUT == 3>(
+                        A, B, M, N, K, m0, n0, LU.m, th, acc);
                 else
                     sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
                 sgemm_store_c(C, M, N, m0, n0, true, th, acc);
@@ -498,9 +516,9 @@ extern "C" {
 //   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), k-major A
 //                  staging -- small shapes
 //   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks), m-major A staging,
-//                  memory instructions spread over the MFMA stream
+//                  memory instructions spread over the MFMA stream, early slice barrier
 //   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks), m-major A staging,
-//                  spread -- large shapes
+//                  spread, early slice barrier -- large shapes
 //   sgemm_opt256 : 256x256 tile, BK 32, 4 waves of 128x128 (4x4 blocks), one wave per SIMD
 //                  (138 KB of LDS, 256 accumulator registers): half the LDS operand traffic
 //                  per flop of the 64x128 wave tile and 16384 MFMA cycles between barriers --
@@ -512,17 +530,17 @@ sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __r
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 128, 32, 2, 2, 3, 2>(A, B, C, M, N, K);
+    sgemm_mfma<128, 128, 32, 2, 2, 1, 3>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_opt(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 256, 16, 2, 2, 0, 2>(A, B, C, M, N, K);
+    sgemm_mfma<128, 256, 16, 2, 2, 0, 3>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sgemm_opt256(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<256, 256, 32, 2, 2, 1, 2>(A, B, C, M, N, K);
+    sgemm_mfma<256, 256, 32, 2, 2, 1, 3>(A, B, C, M, N, K);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:
