@@ -10,6 +10,10 @@ timed steps between device synchronisations.  Inputs are resident in HBM before 
 Secondary figures measured in the same run (same JSON line):
   gemv   -- fp16-weight GEMV on the Qwen2.5-0.5B lm_head shape [151936 x 896], rotating
             four weight copies (1.09 GB) so every launch streams from HBM, not the MALL
+  sgemm_sweep -- sgpu_sgemm_opt at 256^3 .. 4096^3 and the ragged 1023x1025x997
+  gemv_shapes -- every GPT-2 (fp32) and Qwen2.5-0.5B (fp16) projection shape
+  Both report the time per launch replayed from a recorded graph (rates are computed from it)
+  and per launch from a host loop of ctypes calls (which adds the host's submission cost).
   decode -- random-init Qwen2.5-0.5B-architecture decode, 32-token prompt, 128 greedy tokens
 The CPU baseline is the oracle's serial-order SGEMM (row-parallel over the host cores) on a
 bounded sample of rows of the same 4096^3 problem.
@@ -96,6 +100,127 @@ def bench_gemv_lm_head(reps=100, copies=4, warm=1000):
     us = ev.elapsed_ms() * 1e3 / (reps * copies)
     algo_bytes = 2.0 * N * K + 4.0 * K + 4.0 * N
     return dict(us=us, bytes=algo_bytes, gbps=algo_bytes / (us * 1e-6) / 1e9, err=err, copies=copies)
+
+
+SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+                (1023, 1025, 997)]
+GEMV_SHAPES = [("fp32", "gpt2 qkv", 2304, 768), ("fp32", "gpt2 attn-out", 768, 768), ("fp32", "gpt2 fc", 3072, 768),
+               ("fp32", "gpt2 proj", 768, 3072), ("fp32", "gpt2 lm_head", 50257, 768),
+               ("fp16", "qwen q", 896, 896), ("fp16", "qwen k/v", 128, 896), ("fp16", "qwen o", 896, 896),
+               ("fp16", "qwen gate/up", 4864, 896), ("fp16", "qwen down", 896, 4864),
+               ("fp16", "qwen lm_head", 151936, 896)]
+ROTATE_BYTES = 600e6     # weight copies rotated per shape, up to 64: past the 256 MB MALL where that fits
+
+
+def bench_sgemm_sweep(reps=100, warm=50):
+    """sgpu_sgemm_opt over the SGEMM size sweep (square 256..4096 and the ragged 1023x1025x997),
+    reference-generator inputs; HIP-event time per launch after warm-up, normwise error of
+    sampled rows against a float64 product."""
+    out = []
+    for M, N, K in SWEEP_SHAPES:
+        A, B = sgpu.gen_sgemm_inputs(max(M * K, K * N), 42)
+        A, B = A[:M * K], B[:K * N]
+        dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((M, N))
+        run = lambda: sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+        run()
+        sgpu.synchronize()
+        C = dC.to_host()
+        rows = np.linspace(0, M - 1, 8).astype(int)
+        ref = A.reshape(M, K)[rows].astype(np.float64) @ B.reshape(K, N).astype(np.float64)
+        err = float(np.abs(C[rows] - ref).max() / np.abs(ref).max())
+        ev = sgpu.Events()
+        for _ in range(warm):
+            run()
+        ev.record_start(None)
+        for _ in range(reps):
+            run()
+        ev.record_stop(None)
+        us = ev.elapsed_ms() * 1e3 / reps
+        # the same launches recorded once and replayed: no host submission cost per launch
+        st = sgpu.Stream()
+        per_graph = 10
+        with sgpu.Graph(st) as g:
+            for _ in range(per_graph):
+                sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
+        for _ in range(max(1, warm // per_graph)):
+            g.launch()
+        ev.record_start(st.h)
+        for _ in range(max(1, reps // per_graph)):
+            g.launch()
+        ev.record_stop(st.h)
+        us_g = ev.elapsed_ms() * 1e3 / (max(1, reps // per_graph) * per_graph)
+        g.close()
+        st.close()
+        tf = 2.0 * M * N * K / (us_g * 1e-6) / 1e12
+        out.append({"M": M, "N": N, "K": K, "us_in_graph": round(us_g, 2), "us_host_loop": round(us, 2),
+                    "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MATRIX_TFLOPS, 4), "normwise_err": err})
+        for d in (dA, dB, dC):
+            d.close()
+    return out
+
+
+def bench_gemv_shapes(reps=50, warm=100):
+    """The per-projection GEMV shapes of both decoders: GPT-2 fp32 through sgpu_gemv_warp_b
+    (zero bias, the engine's call), Qwen fp16 through sgpu_gemv_h.  Weights N(0, 0.02), x N(0, 1);
+    copies of W are rotated so consecutive launches read different memory."""
+    out = []
+    st = 7
+    for wt, name, N, K in GEMV_SHAPES:
+        Wf, st = sgpu.gen_normal(N * K, st, 0.0, 0.02)
+        x, st = sgpu.gen_normal(K, st, 0.0, 1.0)
+        W = sgpu.f32_to_f16(Wf) if wt == "fp16" else Wf
+        del Wf
+        wbytes = W.nbytes
+        copies = int(max(2, min(64, np.ceil(ROTATE_BYTES / wbytes))))
+        dWs = [sgpu.DeviceArray.from_host(W) for _ in range(copies)]
+        dx, dy = sgpu.DeviceArray.from_host(x), sgpu.DeviceArray(N)
+        dz = sgpu.DeviceArray.from_host(np.zeros(N, np.float32)) if wt == "fp32" else None
+        if wt == "fp32":
+            run = lambda i, st=None: sgpu.call("sgpu_gemv_warp_b", dWs[i % copies].ptr, dx.ptr, dz.ptr, dy.ptr,
+                                               K, N, st)
+        else:
+            run = lambda i, st=None: sgpu.call("sgpu_gemv_h", dWs[i % copies].ptr, dx.ptr, None, dy.ptr, K, N, st)
+        run(0)
+        sgpu.synchronize()
+        y = dy.to_host()
+        rows = np.arange(0, N, max(1, N // 64))
+        Wd = (W.reshape(N, K)[rows].view(np.float16).astype(np.float64) if wt == "fp16"
+              else W.reshape(N, K)[rows].astype(np.float64))
+        if wt == "fp16":
+            Wd[np.abs(Wd) < 2.0 ** -14] = 0.0     # the h2f contract flushes fp16 subnormals
+        ref = Wd @ x.astype(np.float64)
+        err = float(np.abs(y[rows] - ref).max() / np.abs(ref).max())
+        ev = sgpu.Events()
+        for i in range(warm):
+            run(i)
+        ev.record_start(None)
+        for i in range(reps * copies):
+            run(i)
+        ev.record_stop(None)
+        us = ev.elapsed_ms() * 1e3 / (reps * copies)
+        # in-graph: one launch per weight copy recorded once, the graph replayed
+        strm = sgpu.Stream()
+        with sgpu.Graph(strm) as g:
+            for i in range(copies):
+                run(i, strm.h)
+        for _ in range(max(1, warm // copies)):
+            g.launch()
+        ev.record_start(strm.h)
+        for _ in range(reps):
+            g.launch()
+        ev.record_stop(strm.h)
+        us_g = ev.elapsed_ms() * 1e3 / (reps * copies)
+        g.close()
+        strm.close()
+        algo = wbytes + 4.0 * K + 4.0 * N + (4.0 * N if wt == "fp32" else 0.0)
+        gbps = algo / (us_g * 1e-6) / 1e9
+        out.append({"shape": [N, K], "name": name, "weights": wt, "us_in_graph": round(us_g, 3),
+                    "us_host_loop": round(us, 3), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
+                    "rotated_mb": round(copies * wbytes / 1e6, 1), "normwise_err": err})
+        for d in dWs + [dx, dy] + ([dz] if dz is not None else []):
+            d.close()
+        del dWs
+    return out
 
 
 def host_loop_tok_s(eng, ids, gen):
@@ -265,6 +390,10 @@ def main():
     gv = bench_gemv_lm_head()
     log(f"gemv_h lm_head: {gv['us']:.1f} us, {gv['gbps']:.0f} GB/s ({gv['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), "
         f"err {gv['err']:.2e}")
+    sweep = bench_sgemm_sweep()
+    log("sgemm sweep (in-graph): " + ", ".join(f"{r['M']}x{r['N']}x{r['K']} {r['tflops']:.1f} TF" for r in sweep))
+    gshapes = bench_gemv_shapes()
+    log("gemv shapes (in-graph): " + ", ".join(f"{r['name']} {r['us_in_graph']:.2f} us" for r in gshapes))
     dec = g2 = None
     if not args.no_decode:
         dec = bench_decode()
@@ -304,6 +433,8 @@ def main():
                               "unit": "GB/s", "frac": round(gv["gbps"] / PEAK_HBM_GBPS, 4),
                               "traffic": traffic.get("gemv_h_lm_head")},
                  "weight_copies_rotated": gv["copies"], "normwise_err": gv["err"]},
+        "sgemm_sweep": sweep,
+        "gemv_shapes": gshapes,
         "decode": None if dec is None else {
             "model": "Qwen2.5-0.5B architecture, random-init N(0,0.02) fp16 weights",
             "tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4),

@@ -75,6 +75,21 @@ int sgpu_memset_d8(void *dst, int value, size_t bytes);              /* synchron
 int sgpu_synchronize(void);                                          /* cuCtxSynchronize */
 int sgpu_stream_synchronize(void *stream);
 
+/* Streams and recorded launch sequences.  A caller that issues the same launches many times
+ * (a serving loop, a benchmark of a short kernel) records them once on a stream made here and
+ * replays them with one call: every sgpu_* launcher that takes a stream can be recorded, and
+ * recorded launches do not run until the graph is launched.  Recording is thread-local: other
+ * threads' HIP work is unaffected, while the recording thread must not call the synchronous
+ * sgpu_* functions (copies, fills, synchronize) until sgpu_graph_end.  Streams are created at
+ * the default priority.  No reference counterpart (the reference launches one kernel per
+ * host call). */
+int sgpu_stream_create(void **stream);
+int sgpu_stream_destroy(void *stream);
+int sgpu_graph_begin(void *stream);                 /* stream must not be NULL */
+int sgpu_graph_end(void *stream, void **graph);     /* instantiated; *graph NULL on error */
+int sgpu_graph_launch(void *graph, void *stream);
+int sgpu_graph_destroy(void *graph);
+
 /* Timing with HIP events on a stream (the reference times with CLOCK_MONOTONIC around a
  * synchronised batch, gpu_workload.c:133-139; events time the stream itself). */
 int sgpu_event_create(void **event);
@@ -104,7 +119,8 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * 128x128; one output per thread).  sgpu_sgemm_opt is the tuned entry: it launches the
  * member (sgemm_opt256 256x256, sgemm_opt 128x256, sgemm_tiled4 128x128 or sgemm_tiled
  * 64x64 tiles) whose busiest CU has the least work: ceil(tiles / CUs) tiles times the
- * tile's area over the member's sustained rate. */
+ * tile's area over the member's sustained rate; problems with fewer 64x64 tiles than half
+ * the CUs, and small ones whose K is not a multiple of 32, go to sgemm_splitk instead. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
@@ -112,6 +128,14 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
  * counterpart in the reference: an added member of the same family, with the same
  * (A, B, C, M, N, K) symbol arguments, for hosts that launch members by name. */
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+/* The sgemm_splitk member: 64x64 tiles with K split S ways (S >= 1; reduced so that every
+ * split holds at least one 32-deep slice), each (tile, split) a block.  Every split writes its
+ * partial tile to a library-owned per-device workspace (32 MB, allocated by sgpu_init) and the
+ * last split of a tile sums all S partials in split order, so results do not depend on
+ * arrival order.  Rejects problems needing more than 16384 tiles or S x tiles x 4096 floats
+ * of workspace (SGPU_ERR_INVALID_ARG).  Launches on one device that overlap in time share
+ * the workspace and must not run concurrently.  No counterpart in the reference. */
+int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream);
 int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 
 /* Read-bandwidth probe, membw_read4 (switch_gpu.cu:41-54; launched gpu_workload.c:210-213):

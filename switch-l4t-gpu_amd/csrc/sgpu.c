@@ -44,7 +44,7 @@ static const struct {
 
 /* Every kernel the launchers use: (module, symbol). */
 enum {
-    K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_NAIVE, K_MEMBW,
+    K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_NAIVE, K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI,
     K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
     K_EMBED_H,
@@ -56,7 +56,8 @@ static const struct {
     const char *sym;
 } g_kern[NKERN] = {
     {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
-    {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_naive"}, {MOD_SWITCH, "membw_read4"},
+    {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_splitk"}, {MOD_SWITCH, "sgemm_naive"},
+    {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"},
     {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
@@ -95,9 +96,19 @@ typedef struct {
     hipFunction_t dec_attn[3], dec_embed, dec_embed_next, dec_argmax_part, dec_argmax_final;
     hipFunction_t dec_g2embed, dec_g2embed_next;
     hipFunction_t pf_embed, pf_gemm, pf_qkv_post, pf_attn[3], pf_swiglu;
+    float *sk_ws;          /* split-K partial tiles, SK_WS_FLOATS */
+    unsigned *sk_cnt;      /* split-K arrival counters, SK_MAX_TILES, zero between launches */
 } devstate;
 
 static devstate g_dev[SGPU_MAX_DEVICES];
+
+/* Split-K member (sgemm_splitk): 64x64 tiles, slices of 32; workspace for S x tiles partial
+ * tiles of 4096 floats (32 MB: 4 splits of 512 tiles, the most the dispatch rule picks) and
+ * one counter per tile. */
+#define SK_TILE 64
+#define SK_BK 32
+#define SK_WS_FLOATS (8u << 20)
+#define SK_MAX_TILES 16384u
 static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
 
 const char *sgpu_error_string(int status) {
@@ -186,6 +197,19 @@ static int load_device(int dev) {
             rc = SGPU_ERR_NO_KERNEL;
             goto out;
         }
+    }
+    /* split-K workspace: allocated once per device, counters zeroed once (every launch
+     * leaves them at zero) */
+    e = hipMalloc((void **)&d->sk_ws, SK_WS_FLOATS * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&d->sk_cnt, SK_MAX_TILES * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(d->sk_cnt, 0, SK_MAX_TILES * sizeof(unsigned));
+    if (e != hipSuccess) {
+        hipFree(d->sk_ws);
+        hipFree(d->sk_cnt);
+        d->sk_ws = NULL;
+        d->sk_cnt = NULL;
+        rc = (int)e;
+        goto out;
     }
     d->ready = 1;
 out:
@@ -292,6 +316,49 @@ int sgpu_synchronize(void) {
 }
 int sgpu_stream_synchronize(void *stream) {
     HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    return SGPU_OK;
+}
+
+int sgpu_stream_create(void **stream) {
+    if (!stream) return SGPU_ERR_INVALID_ARG;
+    *stream = NULL;
+    hipStream_t st;
+    HIPCHK(hipStreamCreate(&st));               /* default priority */
+    *stream = (void *)st;
+    return SGPU_OK;
+}
+int sgpu_stream_destroy(void *stream) {
+    if (!stream) return SGPU_OK;
+    HIPCHK(hipStreamDestroy((hipStream_t)stream));
+    return SGPU_OK;
+}
+
+/* Recorded launch sequences: stream capture in thread-local mode, instantiated at the end. */
+int sgpu_graph_begin(void *stream) {
+    if (!stream) return SGPU_ERR_INVALID_ARG;     /* the null stream cannot be captured */
+    HIPCHK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return SGPU_OK;
+}
+int sgpu_graph_end(void *stream, void **graph) {
+    if (!stream || !graph) return SGPU_ERR_INVALID_ARG;
+    *graph = NULL;
+    hipGraph_t g = NULL;
+    HIPCHK(hipStreamEndCapture((hipStream_t)stream, &g));
+    hipGraphExec_t ge = NULL;
+    hipError_t e = hipGraphInstantiate(&ge, g, NULL, NULL, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return (int)e;
+    *graph = (void *)ge;
+    return SGPU_OK;
+}
+int sgpu_graph_launch(void *graph, void *stream) {
+    if (!graph) return SGPU_ERR_INVALID_ARG;
+    HIPCHK(hipGraphLaunch((hipGraphExec_t)graph, (hipStream_t)stream));
+    return SGPU_OK;
+}
+int sgpu_graph_destroy(void *graph) {
+    if (!graph) return SGPU_OK;
+    HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph));
     return SGPU_OK;
 }
 
@@ -458,6 +525,59 @@ static int sgemm_pick(int M, int N, int cus) {
     return best;
 }
 
+/* sgemm_splitk: S k-splits of every 64x64 tile.  The count is reduced so that every split
+ * holds at least one 32-deep slice (per = cdiv(nk, S) slices each, cdiv(nk, per) splits). */
+static int sk_splits(int K, int S) {
+    const int nk = cdiv(K, SK_BK);
+    if (S > nk) S = nk;
+    const int per = cdiv(nk, S);
+    return cdiv(nk, per);
+}
+static int splitk_fits(int M, int N, int S) {
+    const long long tiles = (long long)cdiv(M, SK_TILE) * cdiv(N, SK_TILE);
+    return tiles <= SK_MAX_TILES && (unsigned long long)S * tiles * SK_TILE * SK_TILE <= SK_WS_FLOATS;
+}
+static int splitk_launch(devstate *d, const float *A, const float *B, float *C, int M, int N, int K, int S,
+                         void *stream) {
+    const long long tiles = (long long)cdiv(M, SK_TILE) * cdiv(N, SK_TILE);
+    if (!splitk_fits(M, N, S)) return SGPU_ERR_INVALID_ARG;
+    unsigned g[3] = {(unsigned)(tiles * S), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {&A, &B, &C, &M, &N, &K, &S, &d->sk_ws, &d->sk_cnt};
+    return launch(d->fn[K_SGEMM_SPLITK], g, b, stream, args);
+}
+int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream) {
+    if (M < 0 || N < 0 || K < 0 || S < 1) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    S = K > 0 ? sk_splits(K, S) : 1;
+    if (!splitk_fits(M, N, S)) return SGPU_ERR_INVALID_ARG;
+    if (!C || (K > 0 && (!A || !B))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    return splitk_launch(d, A, B, C, M, N, K, S, stream);
+}
+/* When sgpu_sgemm_opt splits K (measured, warm, srand inputs: 512^3 13.0 -> 9.9 us at S = 4,
+ * 1023x1025x997 41.6 -> 33.3 us at S = 4; 1024^3 and larger gain nothing): with fewer 64x64
+ * tiles than half the CUs, into about CUs / tiles splits (a power of two, at most 8); with a K
+ * tail (every unsplit tile on the masked pipeline) and at most two tiles per CU, into 4 (the
+ * splits before the tail run the dwordx4 pipeline).  Splits keep at least two slices.
+ * Returns 1 for no split. */
+static int splitk_pick(int M, int N, int K, int cus) {
+    const long long tiles = (long long)cdiv(M, SK_TILE) * cdiv(N, SK_TILE);
+    const int nk = cdiv(K, SK_BK);
+    int S = 1;
+    if (tiles * 2 <= cus) {
+        const long long r = cus / tiles;
+        while (S < 8 && S * 2 <= r) S *= 2;
+    } else if (K % SK_BK && tiles <= 2LL * cus) {
+        S = 4;
+    }
+    if (S > nk / 2) S = nk / 2;
+    if (S < 2) return 1;
+    S = sk_splits(K, S);
+    return splitk_fits(M, N, S) ? S : 1;
+}
+
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
     if (M == 0 || N == 0) return SGPU_OK;
@@ -465,6 +585,8 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    const int S = K > 0 ? splitk_pick(M, N, K, d->cus) : 1;
+    if (S > 1) return splitk_launch(d, A, B, C, M, N, K, S, stream);
     const int m = sgemm_pick(M, N, d->cus);
     return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }

@@ -5,7 +5,8 @@
 //   sgemm_tiled, sgemm_tiled4, sgemm_opt : (const float*A, const float*B, float*C, int M, int N, int K)
 //   sgemm_naive                          : same arguments, one output per thread
 //   membw_read4                          : (const float4*buf, float*out, int n4, int iters)
-// plus sgemm_opt256, a larger-tile member with the same arguments.
+// plus sgemm_opt256, a larger-tile member with the same arguments, and sgemm_splitk
+//   (A, B, C, M, N, K, int S, float* ws, unsigned* cnt), the 64x64 tile with K split S ways.
 //
 // C = A*B, fp32, row-major (A: MxK stride K, B: KxN stride N, C: MxN stride N), overwrite
 // (alpha 1, beta 0).  Unlike the reference kernels, every shape is accepted: interior tiles
@@ -18,10 +19,12 @@
 // A and B k-slices of depth BK are staged through LDS, double-buffered (one barrier per
 // slice; in the large members it sits before the slice's last MFMA group, so the next
 // slice's first operand reads overlap that group): A either k-major with a 2-float row pad
-// or m-major with a 4-float pad, B row-major with a pad.  Tiles are walked with a grid-stride loop over a linear tile index, so any
-// grid of 64*WGM*WGN-thread blocks is correct (surplus blocks exit); with one block per tile
-// the index is remapped so each XCD (blocks are dealt round-robin to the 8 XCDs) works on a
-// compact group of tiles that shares A and B panels in its own L2.
+// or m-major with a 4-float pad, B row-major with a pad.  Tiles are walked with a grid-stride
+// loop over a linear tile index, so any grid of 64*WGM*WGN-thread blocks is correct (surplus
+// blocks exit); with one block per tile the index is remapped so each XCD (blocks are dealt
+// round-robin to the 8 XCDs) works on a compact group of tiles that shares A and B panels in
+// its own L2.  sgemm_splitk walks (tile, k-split) units the same way and sums a tile's splits
+// in the last split to finish.
 #include <type_traits>
 
 #include "sgpu_device.h"
@@ -132,7 +135,7 @@ __device__ __forceinline__ void sgemm_store_c(float* __restrict__ C, int M, int 
 // k order inside each 8-deep group differs, so their sums round independently of these.)
 template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT>
 __device__ __forceinline__ void sgemm_tile_fast(const float* __restrict__ A, const float* __restrict__ B,
-                                                int N, int K, int m0, int n0,
+                                                int N, int K, int lda, int m0, int n0,
                                                 SgemmLds<BM, BN, BK, WGM, WGN>& L,
                                                 const SgemmThread<BM, BN, BK, WGM, WGN>& th,
                                                 sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
@@ -143,9 +146,9 @@ __device__ __forceinline__ void sgemm_tile_fast(const float* __restrict__ A, con
     static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
     // Load round r of a thread reads A row (tid/KQ + r*NT/KQ) and B row (tid/NQ + r*NT/NQ):
     // one base pointer each plus wave-uniform strides.
-    const float* pa = A + (size_t)(m0 + tid / T::KQ) * K + 4 * (tid % T::KQ);
+    const float* pa = A + (size_t)(m0 + tid / T::KQ) * lda + 4 * (tid % T::KQ);
     const float* pb = B + (size_t)(tid / T::NQ) * N + n0 + 4 * (tid % T::NQ);
-    const size_t astep = (size_t)(T::NT / T::KQ) * K, bstep_r = (size_t)(T::NT / T::NQ) * N;
+    const size_t astep = (size_t)(T::NT / T::KQ) * lda, bstep_r = (size_t)(T::NT / T::NQ) * N;
     const size_t bstep = (size_t)BK * N;
     sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
     auto load_slice = [&](int kt) __attribute__((always_inline)) {
@@ -219,7 +222,7 @@ struct SgemmLdsM {
 //   (in-bounds) 64-bit address and zeroed outside A or B when the slice is written to LDS.
 template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false, int MODE = 0, bool EARLY = false>
 __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, const float* __restrict__ B,
-                                                  int M, int N, int K, int m0, int n0,
+                                                  int M, int N, int K, int lda, int m0, int n0,
                                                   SgemmLdsM<BM, BN, BK, WGM, WGN>& L,
                                                   const SgemmThread<BM, BN, BK, WGM, WGN>& th,
                                                   sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
@@ -235,17 +238,17 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     constexpr int AR = MODE == 1 ? T::NT / BK : 1, BR = MODE == 1 ? T::NT / BN : 1;
     constexpr unsigned kOut = 0x80000000u;       // an offset past every MODE-1 buffer range
     const int tid = th.tid, nk = MASKED ? (K + BK - 1) / BK : K / BK;
-    const float* pa = A + (size_t)(m0 + tid / T::KQ) * K + 4 * (tid % T::KQ);
+    const float* pa = A + (size_t)(m0 + tid / T::KQ) * lda + 4 * (tid % T::KQ);
     const float* pb = B + (size_t)(tid / T::NQ) * N + n0 + 4 * (tid % T::NQ);
-    const size_t astep = (size_t)(T::NT / T::KQ) * K, bstep_r = (size_t)(T::NT / T::NQ) * N;
+    const size_t astep = (size_t)(T::NT / T::KQ) * lda, bstep_r = (size_t)(T::NT / T::NQ) * N;
     const size_t bstep = (size_t)BK * N;
     // MODE 1 map and buffers: A from row m0 (range: the tile's valid rows), B from row kt*BK
     const int ar = tid / BK, ak = tid % BK, bkr = tid / BN, bc = tid % BN;
-    const unsigned a_off0 = (unsigned)(ar * K + ak) * 4u, a_step = (unsigned)(AR * K) * 4u;
+    const unsigned a_off0 = (unsigned)(ar * lda + ak) * 4u, a_step = (unsigned)(AR * lda) * 4u;
     const unsigned b_off0 = (unsigned)(bkr * N + n0 + bc) * 4u, b_step = (unsigned)(BR * N) * 4u;
     const bool b_col_ok = n0 + bc < N;
     const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(A + (size_t)m0 * K), (short)0, MODE == 1 ? min(M - m0, BM) * K * 4 : 0, 0x00020000);
+        (void*)(A + (size_t)m0 * lda), (short)0, MODE == 1 ? min(M - m0, BM) * lda * 4 : 0, 0x00020000);
     // MODE 2 map
     const int ar0 = m0 + tid / T::KQ, ak0 = 4 * (tid % T::KQ);
     const int bk0 = tid / T::NQ, bn0 = n0 + 4 * (tid % T::NQ);
@@ -273,7 +276,7 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
         } else {
 #pragma unroll
             for (int r = 0; r < T::A_PER_T; r++) {
-                const float* rp = A + (size_t)min(ar0 + r * (T::NT / T::KQ), M - 1) * K;
+                const float* rp = A + (size_t)min(ar0 + r * (T::NT / T::KQ), M - 1) * lda;
 #pragma unroll
                 for (int e = 0; e < 4; e++) ra[r][e] = rp[min(kt * BK + ak0 + e, K - 1)];
             }
@@ -426,9 +429,10 @@ __device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLdsU
 // spread one per MFMA; 3: as 2, with each slice's barrier moved before its last group.
 // All other tiles run the masked m-major pipeline (spread for LAYOUT 2 and 3, barrier at
 // the end of the slice).
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT, int LAYOUT>
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT, int LAYOUT, bool SPLIT = false>
 __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const float* __restrict__ B,
-                                           float* __restrict__ C, int M, int N, int K) {
+                                           float* __restrict__ C, int M, int N, int K, int S = 1,
+                                           float* __restrict__ ws = nullptr, unsigned* __restrict__ cnt = nullptr) {
     using T = MfmaTile<BM, BN, BK, WGM, WGN>;
     static_assert(STORE_AT >= 0, "store point");
     __shared__ __attribute__((aligned(16))) SgemmLdsU<BM, BN, BK, WGM, WGN> LU;
@@ -441,28 +445,92 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN, ntiles = ntm * ntn;
     const int nb = sgpu_nblocks();
-    const bool remap = (nb == ntiles) && (ntiles % kXcds == 0);
+    const bool remap = !SPLIT && (nb == ntiles) && (ntiles % kXcds == 0);
     const bool aligned = ((K & 3) == 0) && ((N & 3) == 0) &&
                          ((((uintptr_t)A) | ((uintptr_t)B)) & 15) == 0;
+    // Work units: (tile, k-split) pairs, split-major.  Split s covers slices [s*per, (s+1)*per)
+    // of the cdiv(K, BK) slices; every split of a tile holds at least one slice (the launcher
+    // chooses S so), and the last one may end in a partial slice.
+    const int nsplit = SPLIT ? S : 1;
+    const int per = SPLIT ? ((K + BK - 1) / BK + nsplit - 1) / nsplit : 0;
+    const int nunits = ntiles * nsplit;
+    auto unit = [&](int u, int& m0, int& n0, int& k0, int& kext) __attribute__((always_inline)) {
+        int tm, tn;
+        sgemm_tile_coords(SPLIT ? u % ntiles : u, ntm, ntn, remap, tm, tn);
+        m0 = tm * BM;
+        n0 = tn * BN;
+        k0 = SPLIT ? (u / ntiles) * per * BK : 0;
+        kext = SPLIT ? min(K - k0, per * BK) : K;
+    };
+    // A unit's result: with one split, straight to C; with several, each split's partial
+    // tile goes out as device-coherent stores (written through to memory, waited for before
+    // the tile's counter is incremented) and the last split to arrive sums all S partials in
+    // split order -- the same order whichever block is last -- and writes C.
+    __shared__ int last_s;
+    auto finish = [&](int u, int m0, int n0, bool interior, sgpu_f32x16 (&acc)[T::FM][T::FN]) __attribute__((always_inline)) {
+        if constexpr (SPLIT) {
+            if (nsplit > 1) {
+                const int t = u % ntiles, sp = u / ntiles;
+                constexpr int TILE = BM * BN;
+                float* rec = ws + (size_t)(sp * ntiles + t) * TILE + th.tid;
+#pragma unroll
+                for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                    for (int j = 0; j < T::FN; j++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            __hip_atomic_store(rec + ((i * T::FN + j) * 16 + r) * T::NT, acc[i][j][r], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores have completed
+                __syncthreads();
+                if (th.tid == 0)
+                    last_s = __hip_atomic_fetch_add(cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                             (unsigned)(nsplit - 1);
+                __syncthreads();
+                if (!last_s) return;
+                sgpu_f32x16 sum[T::FM][T::FN];
+                for (int s2 = 0; s2 < nsplit; s2++) {
+                    const float* src = ws + (size_t)(s2 * ntiles + t) * TILE + th.tid;
+#pragma unroll
+                    for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                        for (int j = 0; j < T::FN; j++)
+#pragma unroll
+                            for (int r = 0; r < 16; r++) {
+                                const float v = s2 == sp ? acc[i][j][r]
+                                                         : __hip_atomic_load(src + ((i * T::FN + j) * 16 + r) * T::NT,
+                                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                sum[i][j][r] = s2 == 0 ? v : sum[i][j][r] + v;
+                            }
+                }
+                sgemm_store_c(C, M, N, m0, n0, interior, th, sum);
+                if (th.tid == 0) __hip_atomic_store(cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+        }
+        sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
+    };
 
-    // Per tile: interior tiles of a problem with 16-byte rows and K whole slices (at least
-    // two) take the dwordx4 pipeline; every other tile (edges, K tails, unaligned rows) takes
-    // the same pipeline with masked loads (K = 0 writes zeros).  Each kind gets its own tile
-    // loop, so neither carries the other's registers.
+    // Per unit: interior tiles of a problem with 16-byte rows and a k range of whole slices
+    // (at least two) take the dwordx4 pipeline; every other unit (edges, K tails, unaligned
+    // rows) takes the same pipeline with masked loads (K = 0 writes zeros).  Each kind gets
+    // its own loop, so neither carries the other's registers.
     {
-        const bool kfast = aligned && K % BK == 0 && K >= 2 * BK;
+        const bool kfast_k = aligned && K % BK == 0 && K >= 2 * BK;
+        auto kfast = [&](int kext) __attribute__((always_inline)) {
+            return SPLIT ? aligned && kext % BK == 0 && kext >= 2 * BK : kfast_k;
+        };
         constexpr int SG = STORE_AT < BK / 8 ? STORE_AT : 0;      // a group index for the masked path
         // Buffer-load windows (BM rows of A, BK rows of B) within 2^31 bytes: MODE 1, else 2.
-        // Each mode has its own tile loop (one accumulator set per loop, no merge of the two).
+        // Each mode has its own loop (one accumulator set per loop, no merge of the two).
         const bool win = (long long)BM * K * 4 < 0x7fffffffLL && (long long)BK * N * 4 < 0x7fffffffLL;
         auto masked_tiles = [&](auto mode_c) __attribute__((always_inline)) {
             constexpr int MODE = decltype(mode_c)::value;
-            for (int t = sgpu_bid(); t < ntiles; t += nb) {
-                int tm, tn;
-                sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
-                const int m0 = tm * BM, n0 = tn * BN;
+            for (int u = sgpu_bid(); u < nunits; u += nb) {
+                int m0, n0, k0, kext;
+                unit(u, m0, n0, k0, kext);
                 const bool interior = (m0 + BM <= M) && (n0 + BN <= N);
-                if (kfast && interior) continue;
+                if (kfast(kext) && interior) continue;
                 sgpu_f32x16 acc[T::FM][T::FN];
 #pragma unroll
                 for (int i = 0; i < T::FM; i++)
@@ -470,24 +538,23 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                     for (int j = 0; j < T::FN; j++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-                if (K > 0)
+                if (kext > 0)
                     sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, SG, LAYOUT >= 2, MODE, false>(
-                        A, B, M, N, K, m0, n0, LU.m, th, acc);
-                sgemm_store_c(C, M, N, m0, n0, interior, th, acc);
+                        A + k0, B + (size_t)k0 * N, M, N, kext, K, m0, n0, LU.m, th, acc);
+                finish(u, m0, n0, interior, acc);
             }
         };
-        // Masked tiles first, then interior tiles: with this order the interior loop's code
+        // Masked units first, then interior ones: with this order the interior loop's code
         // measured 7% faster on sgemm_tiled4 at 4096^3 (1% on sgemm_opt).
         if (win)
             masked_tiles(std::integral_constant<int, 1>{});
         else
             masked_tiles(std::integral_constant<int, 2>{});
-        if (kfast) {
-            for (int t = sgpu_bid(); t < ntiles; t += nb) {
-                int tm, tn;
-                sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
-                const int m0 = tm * BM, n0 = tn * BN;
-                if (m0 + BM > M || n0 + BN > N) continue;
+        if (SPLIT ? aligned : kfast_k) {
+            for (int u = sgpu_bid(); u < nunits; u += nb) {
+                int m0, n0, k0, kext;
+                unit(u, m0, n0, k0, kext);
+                if (m0 + BM > M || n0 + BN > N || !kfast(kext)) continue;
                 sgpu_f32x16 acc[T::FM][T::FN];
 #pragma unroll
                 for (int i = 0; i < T::FM; i++)
@@ -497,10 +564,11 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
                 if constexpr (LAYOUT >= 1)
                     sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT >= 2, 0, LAYOUT == 3>(
-                        A, B, M, N, K, m0, n0, LU.m, th, acc);
+                        A + k0, B + (size_t)k0 * N, M, N, kext, K, m0, n0, LU.m, th, acc);
                 else
-                    sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A, B, N, K, m0, n0, L, th, acc);
-                sgemm_store_c(C, M, N, m0, n0, true, th, acc);
+                    sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A + k0, B + (size_t)k0 * N, N, kext, K, m0, n0, L,
+                                                                    th, acc);
+                finish(u, m0, n0, true, acc);
             }
         }
     }
@@ -541,6 +609,15 @@ sgemm_opt(const float* __restrict__ A, const float* __restrict__ B, float* __res
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sgemm_opt256(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_mfma<256, 256, 32, 2, 2, 1, 3>(A, B, C, M, N, K);
+}
+
+// sgemm_splitk: the 64x64 tile with K split S ways: blocks are (tile, split) units, so a
+// problem with fewer tiles than CUs still spreads over the chip.  ws holds S*ntiles*4096
+// floats of partial tiles, cnt one zero-initialised counter per tile (left at zero again).
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+sgemm_splitk(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
+             int S, float* __restrict__ ws, unsigned* __restrict__ cnt) {
+    sgemm_mfma<64, 64, 32, 2, 2, 1, 3, true>(A, B, C, M, N, K, S, ws, cnt);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:

@@ -72,8 +72,15 @@ _SIGS = {
     "sgpu_sgemm_tiled4": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_opt": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_opt256": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "sgpu_sgemm_splitk": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_sgemm_naive": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_membw_read4": (_I, [_P, _P, _I, _I, ct.POINTER(_I), _P]),
+    "sgpu_stream_create": (_I, [_P]),
+    "sgpu_stream_destroy": (_I, [_P]),
+    "sgpu_graph_begin": (_I, [_P]),
+    "sgpu_graph_end": (_I, [_P, _P]),
+    "sgpu_graph_launch": (_I, [_P, _P]),
+    "sgpu_graph_destroy": (_I, [_P]),
     "sgpu_gemv": (_I, [_P, _P, _P, _I, _I, _P]),
     "sgpu_gemv4": (_I, [_P, _P, _P, _I, _I, _P]),
     "sgpu_gemv_warp": (_I, [_P, _P, _P, _I, _I, _P]),
@@ -208,6 +215,67 @@ class DeviceArray:
         if getattr(self, "ptr", None):
             lib().sgpu_free(self.ptr)
             self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Stream:
+    """A HIP stream at the default priority (sgpu_stream_create)."""
+
+    def __init__(self):
+        h = ct.c_void_p()
+        call("sgpu_stream_create", ct.byref(h))
+        self.h = h.value
+
+    def synchronize(self):
+        call("sgpu_stream_synchronize", self.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().sgpu_stream_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Graph:
+    """Launches recorded on a Stream and replayed as one graph launch:
+
+        with Graph(stream) as g:
+            call("sgpu_gemv_h", ..., stream.h)     # recorded, not run
+        g.launch()
+    """
+
+    def __init__(self, stream: Stream):
+        self.stream, self.h = stream, None
+
+    def __enter__(self):
+        call("sgpu_graph_begin", self.stream.h)
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = ct.c_void_p()
+        rc = lib().sgpu_graph_end(self.stream.h, ct.byref(h))
+        if exc_type is None:
+            check(rc, "sgpu_graph_end")
+        self.h = h.value
+        return False
+
+    def launch(self):
+        call("sgpu_graph_launch", self.h, self.stream.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().sgpu_graph_destroy(self.h)
+            self.h = None
 
     def __del__(self):
         try:

@@ -12,7 +12,7 @@ import pytest
 # gpt2_engine.c:119-128, qwen_engine.c:148-155); a missing one is fatal to those hosts.
 REFERENCE_KERNELS = {
     "switch_gpu": {"sgemm_tiled", "sgemm_tiled4", "sgemm_opt", "sgemm_naive", "membw_read4",
-                   "sgemm_opt256"},   # the last one is an added member (no reference counterpart)
+                   "sgemm_opt256", "sgemm_splitk"},   # the last two are added members (no reference counterpart)
     "gemv": {"gemv", "gemv4", "gemv_warp"},
     "gpt2_kernels": {"gemv_warp", "gemv_warp_b", "gemv_multi", "layernorm", "gelu", "add_bias", "add2",
                      "attn_scores", "attn_softmax", "attn_mix"},
@@ -110,6 +110,17 @@ def test_argument_errors_before_device(sg):
     assert L.sgpu_qwen_generate(None, None, 1, 1, None) == sg.SGPU_ERR_INVALID_ARG
     assert L.sgpu_gpt2_generate(None, None, 1, 1, None) == sg.SGPU_ERR_INVALID_ARG
     assert L.sgpu_gpt2_forward(None, 0, 0, 1, None, 0) == sg.SGPU_ERR_INVALID_ARG
+    # split-K: bad split counts and problems past the workspace are rejected up front
+    assert L.sgpu_sgemm_splitk(None, None, None, 64, 64, 64, 0, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_splitk(None, None, None, 4096, 4096, 4096, 2, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_splitk(None, None, None, 0, 64, 64, 2, None) == 0
+    # streams and recorded launch sequences: NULL handles
+    assert L.sgpu_stream_create(None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_stream_destroy(None) == 0
+    assert L.sgpu_graph_begin(None) == sg.SGPU_ERR_INVALID_ARG      # the null stream cannot record
+    assert L.sgpu_graph_end(None, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_graph_launch(None, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_graph_destroy(None) == 0
 
 
 def test_gemv_multi_geometry_follows_the_token_rule(sg):

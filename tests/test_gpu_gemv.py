@@ -65,6 +65,49 @@ def test_qwen_shapes_fp16(gpu, og, N, K):
     assert np.all(np.abs(y - ref) <= 1e-3 * np.abs(ref) + 1e-3 * m)
 
 
+def test_recorded_launches_replay(gpu, og):
+    """GEMV (fp16 and fp32 weights) and SGEMM launches recorded once on a stream and replayed:
+    every replay, with new inputs copied in between (host work and synchronisation between
+    the replays), gives the same bits as the same launches run directly."""
+    say("graph replay gemv_h + gemv_warp_b + sgemm_opt")
+    N, K, M = 896, 4864, 64
+    Wh = gpu.f32_to_f16(gpu.gen_normal(N * K, 3, 0.0, 0.02)[0])
+    Wf, s = gpu.gen_normal(N * K, 5, 0.0, 0.02)
+    bias, s = gpu.gen_normal(N, s, 0.0, 0.1)
+    A, s = gpu.gen_normal(M * K, s, 0.0, 1.0)
+    dWh, dWf, db, dA = (gpu.DeviceArray.from_host(a) for a in (Wh, Wf, bias, A))
+    dx, dyh, dyf, dC = gpu.DeviceArray(K), gpu.DeviceArray(N), gpu.DeviceArray(N), gpu.DeviceArray((M, N))
+
+    def launches(st):
+        gpu.call("sgpu_gemv_h", dWh.ptr, dx.ptr, None, dyh.ptr, K, N, st)
+        gpu.call("sgpu_gemv_warp_b", dWf.ptr, dx.ptr, db.ptr, dyf.ptr, K, N, st)
+        # C[M x N] = A[M x K] * Wf viewed as [K x N]
+        gpu.call("sgpu_sgemm_opt", dA.ptr, dWf.ptr, dC.ptr, M, N, K, st)
+
+    st = gpu.Stream()
+    with gpu.Graph(st) as g:
+        launches(st.h)
+    for rep in range(4):
+        x, s = gpu.gen_normal(K, 100 + rep, 0.0, 1.0)
+        gpu.call("sgpu_memcpy_htod", dx.ptr, x.ctypes.data, K * 4)
+        for d in (dyh, dyf, dC):
+            d.fill_bytes(0xFF)
+        launches(None)
+        gpu.synchronize()
+        want = [d.to_host() for d in (dyh, dyf, dC)]
+        for d in (dyh, dyf, dC):
+            d.fill_bytes(0xFF)
+        g.launch()
+        st.synchronize()
+        got = [d.to_host() for d in (dyh, dyf, dC)]
+        for w, h in zip(want, got):
+            assert np.array_equal(w.view(np.uint32), h.view(np.uint32)), rep
+        ref = og.gemv_h_fbias(Wh, x, None, K, N, NT)
+        assert np.abs(got[0] - ref).max() / np.abs(ref).max() <= 1e-3
+    g.close()
+    st.close()
+
+
 EDGE = [(1, 1), (5, 3), (64, 4), (63, 8), (1000, 63), (7, 896), (300, 4864), (33, 5000), (4, 8200), (2, 40000)]
 
 

@@ -131,6 +131,47 @@ def test_large_operand_windows_integer_exact(gpu, fn, M, N, K):
     assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
 
 
+# (M, N, K, S): even and uneven splits, K tails (a partial last slice), edge tiles, one tile
+# with many splits, and S above the slice count (reduced to one slice per split).
+SPLITK_CASES = [(512, 512, 512, 1), (512, 512, 512, 2), (512, 512, 512, 4), (512, 512, 512, 8),
+                (1023, 1025, 997, 4), (100, 70, 3000, 8), (64, 64, 8192, 16), (257, 511, 1030, 3),
+                (130, 260, 40, 5), (33, 17, 96, 64)]
+
+
+@pytest.mark.parametrize("M,N,K,S", SPLITK_CASES)
+def test_splitk_integer_exact(gpu, M, N, K, S):
+    """Every split count gives the exact product on integer inputs, on two calls in a row
+    (each launch leaves its tile counters at zero for the next)."""
+    say(f"sgemm splitk integer {M}x{N}x{K} S={S}")
+    rng = np.random.default_rng(M * 7 + N + K + S)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    for _ in range(2):
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, S, None)
+        gpu.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+
+
+def test_splitk_reference_generator_and_unaligned(gpu, og):
+    """Reference-generator inputs within the normwise bar of the oracle, with A starting one
+    float past a 16-byte boundary (every unit on the masked pipeline)."""
+    M, N, K = 300, 200, 1500
+    say(f"sgemm splitk srand unaligned {M}x{N}x{K}")
+    A, B = gpu.gen_sgemm_inputs(max(M * K, K * N), 42)
+    A, B = A[:M * K], B[:K * N]
+    dA = gpu.DeviceArray(M * K + 1)
+    gpu.call("sgpu_memcpy_htod", dA.offset(1), A.ctypes.data, M * K * 4)
+    dB, dC = gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    gpu.call("sgpu_sgemm_splitk", dA.offset(1), dB.ptr, dC.ptr, M, N, K, 6, None)
+    gpu.synchronize()
+    C = dC.to_host().reshape(M, N)
+    ref = og.sgemm(A, B, M, N, K).astype(np.float64)
+    assert np.abs(C - ref).max() / np.abs(ref).max() <= 1e-4
+
+
 @pytest.mark.parametrize("fn", VARIANTS[:3] + ["sgpu_sgemm_opt256"])
 def test_unaligned_pointers(gpu, fn):
     M, N, K = 200, 136, 72
