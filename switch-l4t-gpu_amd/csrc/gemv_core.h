@@ -436,10 +436,17 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
 // WT = WF32: fp32 weight rows, 16-byte loads.  WT = WF16: fp16 weight rows (8-byte loads of
 // four codes), converted to fp32 while staged with the exact reference decode (sgpu_h2f), so
 // the MFMAs see the same operands as the CPU golden.
-template <int FN, class WT = WF32>
+// SPLIT: blocks are (tile, k-split) units, split-major; split s takes chunks
+// [s*nch/S, (s+1)*nch/S) and its four waves divide those.  Each unit's block-summed partial
+// tile goes to ws with device-coherent stores (written through to memory, waited for) before
+// the unit counts in on cnt[tile]; the last split of a tile sums the S partials in split
+// order (deterministic), adds the bias, writes Y and resets the counter.  ws holds
+// S * ntiles * 1024 * FN floats, cnt one zeroed counter per tile.
+template <int FN, class WT = WF32, bool SPLIT = false>
 __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict__ W, const float* __restrict__ X,
                                              const float* __restrict__ bias, float* __restrict__ Y,
-                                             int K, int N, int T) {
+                                             int K, int N, int T, int S = 1, float* __restrict__ ws = nullptr,
+                                             unsigned* __restrict__ cnt = nullptr) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     constexpr int NW = 4;                                   // waves per block (K split)
     constexpr int R = 32 * (1 + FN);                        // staged rows per wave: tokens, then W
@@ -452,13 +459,17 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
     const int lr = lane >> 3, lq = lane & 7;                // coalesced: row in 8-row group, quad
     const int ntt = (T + 31) / 32, ntn = (N + 32 * FN - 1) / (32 * FN), ntiles = ntt * ntn;
     const int nch = (K + 31) / 32;
-    const int c0 = wave * nch / NW, c1 = (wave + 1) * nch / NW;
+    const int nsplit = SPLIT ? S : 1;
     const int nb = gridDim.x * gridDim.y;
     const int bid = blockIdx.x + blockIdx.y * gridDim.x;
-    const bool remap = (nb == ntiles) && (ntiles % 8 == 0);
+    const bool remap = nsplit == 1 && (nb == ntiles) && (ntiles % 8 == 0);
     float (*st)[P] = stage[wave];
+    __shared__ int last_s;
 
-    for (int tile = bid; tile < ntiles; tile += nb) {
+    for (int unit = bid; unit < ntiles * nsplit; unit += nb) {
+        const int tile = SPLIT ? unit % ntiles : unit, sp = SPLIT ? unit / ntiles : 0;
+        const int uc0 = sp * nch / nsplit, uc1 = (sp + 1) * nch / nsplit;
+        const int c0 = uc0 + wave * (uc1 - uc0) / NW, c1 = uc0 + (wave + 1) * (uc1 - uc0) / NW;
         const int tl = remap ? (tile % 8) * (ntiles / 8) + tile / 8 : tile;
         const int t0 = (tl % ntt) * 32, n0 = (tl / ntt) * 32 * FN;
         // Row q*8 + lr of the staged block: token rows first (q < 4), then weight rows.
@@ -526,6 +537,51 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
         // summing the NW partials in wave order.  D layout: lane l, acc r -> token
         // 8*(r/4) + 4*(l/32) + r%4, row l%32.
         constexpr int RPW = 16 / NW;
+        float v[FN][RPW];
+#pragma unroll
+        for (int f = 0; f < FN; f++)
+#pragma unroll
+            for (int rr = 0; rr < RPW; rr++) {
+                const int r = RPW * wave + rr;
+                v[f][rr] = red(0, 16 * f + r);
+#pragma unroll
+                for (int w = 1; w < NW; w++) v[f][rr] += red(w, 16 * f + r);
+            }
+        if (SPLIT && nsplit > 1) {
+            // This thread's values: (f, rr) at ws + unit record + (f*RPW + rr)*256 + tid.
+            constexpr int REC = 1024 * FN;
+            float* rec = ws + (size_t)(sp * ntiles + tile) * REC + tid;
+#pragma unroll
+            for (int f = 0; f < FN; f++)
+#pragma unroll
+                for (int rr = 0; rr < RPW; rr++)
+                    __hip_atomic_store(rec + (f * RPW + rr) * 256, v[f][rr], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores have completed
+            __syncthreads();
+            if (tid == 0)
+                last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (unsigned)(nsplit - 1);
+            __syncthreads();
+            if (!last_s) continue;                  // block-uniform; staging is free again
+            float sum[FN][RPW];
+            for (int s2 = 0; s2 < nsplit; s2++) {
+                const float* src = ws + (size_t)(s2 * ntiles + tile) * REC + tid;
+#pragma unroll
+                for (int f = 0; f < FN; f++)
+#pragma unroll
+                    for (int rr = 0; rr < RPW; rr++) {
+                        const float o = s2 == sp ? v[f][rr]
+                                                 : __hip_atomic_load(src + (f * RPW + rr) * 256, __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT);
+                        sum[f][rr] = s2 == 0 ? o : sum[f][rr] + o;
+                    }
+            }
+#pragma unroll
+            for (int f = 0; f < FN; f++)
+#pragma unroll
+                for (int rr = 0; rr < RPW; rr++) v[f][rr] = sum[f][rr];
+            if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
 #pragma unroll
         for (int f = 0; f < FN; f++) {
             const int n = n0 + 32 * f + i;
@@ -533,11 +589,8 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
 #pragma unroll
             for (int rr = 0; rr < RPW; rr++) {
                 const int r = RPW * wave + rr;
-                float v = red(0, 16 * f + r);
-#pragma unroll
-                for (int w = 1; w < NW; w++) v += red(w, 16 * f + r);
                 const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (t < T && n < N) Y[(size_t)t * N + n] = v + bv;
+                if (t < T && n < N) Y[(size_t)t * N + n] = v[f][rr] + bv;
             }
         }
         __syncthreads();                          // staging is reused by the next tile

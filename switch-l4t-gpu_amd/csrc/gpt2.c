@@ -79,6 +79,8 @@ struct sgpu_gpt2 {
     int *d_amax_i;
     float *d_attn_ws;                               /* attention chunk partials */
     unsigned *d_attn_cnt;                           /* per-head chunk counters (kept at zero) */
+    float *d_split_ws;                              /* prefill GEMM k-split partials */
+    unsigned *d_split_cnt;                          /* ... and per-tile counters (kept at zero) */
     hipGraph_t g_layers, g_step;
     hipGraphExec_t ge_layers, ge_step;
 };
@@ -87,12 +89,13 @@ void sgpu_gpt2_destroy(sgpu_gpt2 *e) {
     if (!e) return;
     float *bufs[] = {e->w, e->x, e->ln1, e->qkv, e->att, e->y, e->ln2, e->fc, e->scores, e->probs, e->logits,
                      e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT, e->d_q, e->d_amax_v,
-                     e->d_attn_ws};
+                     e->d_attn_ws, e->d_split_ws};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) sgpu_free(bufs[i]);
     sgpu_free(e->d_step);
     sgpu_free(e->d_tokens);
     sgpu_free(e->d_amax_i);
     sgpu_free(e->d_attn_cnt);
+    sgpu_free(e->d_split_cnt);
     if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
     if (e->g_layers) hipGraphDestroy(e->g_layers);
     if (e->ge_step) hipGraphExecDestroy(e->ge_step);
@@ -150,6 +153,9 @@ int sgpu_gpt2_create(sgpu_gpt2 **out, const sgpu_gpt2_cfg *c, const float *blob)
     TRY(zalloc(&e->d_attn_ws, SGPU_ATTN_WS_FLOATS(c->NH, c->HD)));
     TRY(sgpu_malloc((void **)&e->d_attn_cnt, (size_t)c->NH * sizeof(unsigned)));
     TRY(sgpu_memset_d8(e->d_attn_cnt, 0, (size_t)c->NH * sizeof(unsigned)));
+    TRY(zalloc(&e->d_split_ws, SGPU_NT_WS_FLOATS));
+    TRY(sgpu_malloc((void **)&e->d_split_cnt, SGPU_NT_CNT * sizeof(unsigned)));
+    TRY(sgpu_memset_d8(e->d_split_cnt, 0, SGPU_NT_CNT * sizeof(unsigned)));
 #undef TRY
     *out = e;
     return SGPU_OK;
@@ -329,7 +335,8 @@ static int prefill_layers(sgpu_gpt2 *e, const int *ids, int T) {
     for (int l = 0; l < c->NL; l++) {
         const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
         TRY(sgpu_layernorm(e->xT, b + e->L.ln1w, b + e->L.ln1b, e->ln1T, C, eps, T, s));
-        TRY(sgpu_gemv_multi(b + e->L.qkvw, e->ln1T, b + e->L.qkvb, e->qkvT, C, 3 * C, T, s));
+        TRY(sgpu_internal_gemv_multi(b + e->L.qkvw, e->ln1T, b + e->L.qkvb, e->qkvT, C, 3 * C, T,
+            e->d_split_ws, e->d_split_cnt, s));
         if (T <= 8192) {
             const size_t row = (size_t)C * 4, qrow = 3 * row;
             hipError_t he = hipMemcpy2DAsync(e->kc[l], row, e->qkvT + C, qrow, row, (size_t)T, hipMemcpyDeviceToDevice,
@@ -349,12 +356,15 @@ static int prefill_layers(sgpu_gpt2 *e, const int *ids, int T) {
                 TRY(sgpu_gpt2_attn_mix(e->probs, e->vc[l], e->attT + (size_t)t * C, t + 1, s));
             }
         }
-        TRY(sgpu_gemv_multi(b + e->L.aow, e->attT, b + e->L.aob, e->yT, C, C, T, s));
+        TRY(sgpu_internal_gemv_multi(b + e->L.aow, e->attT, b + e->L.aob, e->yT, C, C, T,
+            e->d_split_ws, e->d_split_cnt, s));
         TRY(sgpu_add2(e->xT, e->yT, e->xT, T * C, s));
         TRY(sgpu_layernorm(e->xT, b + e->L.ln2w, b + e->L.ln2b, e->ln2T, C, eps, T, s));
-        TRY(sgpu_gemv_multi(b + e->L.fcw, e->ln2T, b + e->L.fcb, e->fcT, C, FC, T, s));
+        TRY(sgpu_internal_gemv_multi(b + e->L.fcw, e->ln2T, b + e->L.fcb, e->fcT, C, FC, T,
+            e->d_split_ws, e->d_split_cnt, s));
         TRY(sgpu_gelu(e->fcT, e->fcT, T * FC, s));
-        TRY(sgpu_gemv_multi(b + e->L.projw, e->fcT, b + e->L.projb, e->yT, FC, C, T, s));
+        TRY(sgpu_internal_gemv_multi(b + e->L.projw, e->fcT, b + e->L.projb, e->yT, FC, C, T,
+            e->d_split_ws, e->d_split_cnt, s));
         TRY(sgpu_add2(e->xT, e->yT, e->xT, T * C, s));
     }
 #undef TRY

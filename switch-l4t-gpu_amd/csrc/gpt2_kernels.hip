@@ -59,6 +59,18 @@ __global__ void __launch_bounds__(256) gemv_multi(const float* __restrict__ W, c
         sgpu::gemv_multi_f32<16>(W, X, bias, Y, K, N, T);
 }
 
+// gemv_multi with each 32x32 tile's K split S ways across blocks (grid = tiles * S): the
+// matrix-core path for problems with too few tiles to fill the CUs.  Same operand
+// conditions as gemv_multi's matrix-core path (checked by the launcher); ws holds
+// S * tiles * 1024 floats, cnt one zeroed counter per tile (left at zero).
+__global__ void __launch_bounds__(256) gemv_multi_splitk(const float* __restrict__ W, const float* __restrict__ X,
+                                                         const float* __restrict__ bias, float* __restrict__ Y,
+                                                         int K, int N, int T, int S, float* __restrict__ ws,
+                                                         unsigned* __restrict__ cnt) {
+    if (blockDim.x != 256) return;
+    sgpu::gemm_nt_mfma<1, sgpu::WF32, true>(W, X, bias, Y, K, N, T, S, ws, cnt);
+}
+
 // y = (x - mean) / sqrt(var + eps) * w + b per row (grid = rows), with the two-pass
 // mean/variance of the CPU golden (gpt2_engine.c:331-339).
 __global__ void __launch_bounds__(1024) layernorm(const float* __restrict__ x, const float* __restrict__ w,

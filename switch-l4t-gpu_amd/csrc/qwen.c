@@ -111,6 +111,8 @@ struct sgpu_qwen {
     int *d_amax_i;
     float *d_attn_ws;                          /* attention chunk partials */
     unsigned *d_attn_cnt;                      /* per-head chunk counters (kept at zero) */
+    float *d_split_ws;                         /* prefill GEMM k-split partials */
+    unsigned *d_split_cnt;                     /* ... and per-tile counters (kept at zero) */
     int *d_pf_ids;                             /* batched prefill: prompt ids and row buffers */
     float *d_pf_x, *d_pf_xn, *d_pf_qkv, *d_pf_att, *d_pf_y, *d_pf_g;
     hipGraph_t g_layers, g_step;
@@ -153,6 +155,8 @@ void sgpu_qwen_destroy(sgpu_qwen *e) {
     sgpu_free(e->d_amax_i);
     sgpu_free(e->d_attn_ws);
     sgpu_free(e->d_attn_cnt);
+    sgpu_free(e->d_split_ws);
+    sgpu_free(e->d_split_cnt);
     sgpu_free(e->d_pf_ids);
     float *pf[] = {e->d_pf_x, e->d_pf_xn, e->d_pf_qkv, e->d_pf_att, e->d_pf_y, e->d_pf_g};
     for (size_t i = 0; i < sizeof pf / sizeof pf[0]; i++) sgpu_free(pf[i]);
@@ -230,6 +234,8 @@ int sgpu_qwen_create(sgpu_qwen **out, const sgpu_qwen_cfg *c, const void *blob) 
     TRY(dalloc((void **)&e->d_amax_i, SGPU_ARGMAX_PARTS * sizeof(int), NULL));
     TRY(dalloc((void **)&e->d_attn_ws, SGPU_ATTN_WS_FLOATS(c->NH, c->HD) * sizeof(float), NULL));
     TRY(dalloc((void **)&e->d_attn_cnt, (size_t)c->NH * sizeof(unsigned), NULL));
+    TRY(dalloc((void **)&e->d_split_ws, (size_t)SGPU_NT_WS_FLOATS * sizeof(float), NULL));
+    TRY(dalloc((void **)&e->d_split_cnt, (size_t)SGPU_NT_CNT * sizeof(unsigned), NULL));
 #undef TRY
     *out = e;
     return SGPU_OK;
@@ -422,16 +428,20 @@ static int prefill_rows(sgpu_qwen *e, const int *ids, int T) {
         TRY(sgpu_internal_pf_embed(e->d_emb, e->d_pf_ids + c0, Tc, e->d_pf_x, C, s));
         for (int l = 0; l < c->NL; l++) {
             TRY(sgpu_rmsnorm(e->d_pf_x, e->d_ln1w[l], e->d_pf_xn, C, eps, Tc, s));
-            TRY(sgpu_internal_pf_gemm(e->d_qkvw[l], e->d_pf_xn, e->d_qkvb[l], e->d_pf_qkv, C, QKVD, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_qkvw[l], e->d_pf_xn, e->d_qkvb[l], e->d_pf_qkv, C, QKVD, Tc,
+                e->d_split_ws, e->d_split_cnt, s));
             TRY(sgpu_internal_pf_qkv_post(e->d_pf_qkv, Tc, c0, e->d_cos, e->d_sin, e->d_kc[l], e->d_vc[l], NH, NKV,
                                           HD, s));
             TRY(sgpu_internal_pf_attn(e->d_pf_qkv, e->d_kc[l], e->d_vc[l], e->d_pf_att, Tc, c0, NH, NKV, HD, scale, s));
-            TRY(sgpu_internal_pf_gemm(e->d_ow[l], e->d_pf_att, NULL, e->d_pf_y, C, C, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_ow[l], e->d_pf_att, NULL, e->d_pf_y, C, C, Tc,
+                e->d_split_ws, e->d_split_cnt, s));
             TRY(sgpu_add2(e->d_pf_x, e->d_pf_y, e->d_pf_x, Tc * C, s));
             TRY(sgpu_rmsnorm(e->d_pf_x, e->d_ln2w[l], e->d_pf_xn, C, eps, Tc, s));
-            TRY(sgpu_internal_pf_gemm(e->d_gateupw[l], e->d_pf_xn, NULL, e->d_pf_y, C, 2 * FC, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_gateupw[l], e->d_pf_xn, NULL, e->d_pf_y, C, 2 * FC, Tc,
+                e->d_split_ws, e->d_split_cnt, s));
             TRY(sgpu_internal_pf_swiglu(e->d_pf_y, e->d_pf_g, FC, Tc, s));
-            TRY(sgpu_internal_pf_gemm(e->d_downw[l], e->d_pf_g, NULL, e->d_pf_y, FC, C, Tc, s));
+            TRY(sgpu_internal_pf_gemm(e->d_downw[l], e->d_pf_g, NULL, e->d_pf_y, FC, C, Tc,
+                e->d_split_ws, e->d_split_cnt, s));
             TRY(sgpu_add2(e->d_pf_x, e->d_pf_y, e->d_pf_x, Tc * C, s));
         }
     }

@@ -45,7 +45,7 @@ static const struct {
 /* Every kernel the launchers use: (module, symbol). */
 enum {
     K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_NAIVE, K_MEMBW,
-    K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI,
+    K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK,
     K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
     K_EMBED_H,
     K_LAYERNORM, K_GELU, K_ADD_BIAS, K_G2_SCORES, K_G2_SOFTMAX, K_G2_MIX,
@@ -59,7 +59,7 @@ static const struct {
     {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_splitk"}, {MOD_SWITCH, "sgemm_naive"},
     {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
-    {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"},
+    {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
     {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
     {MOD_QWEN, "attn_scores_gqa"}, {MOD_QWEN, "attn_softmax"}, {MOD_QWEN, "attn_mix_gqa"},
     {MOD_QWEN, "add2"},
@@ -679,18 +679,49 @@ int sgpu_gemv_h(const uint16_t *W, const float *x, const float *bias, float *y, 
     return gemv_launch(K_GEMV_H, 1, W, x, bias, y, K, N, stream);
 }
 
-int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N, int T,
-                    void *stream) {
+/* K splits for the batched matrix-core GEMM (32-token x 32-row tiles): with fewer tiles than
+ * CUs, about two units per CU, each split keeping at least four 32-deep chunks (one per
+ * wave), at most 16 splits, within SGPU_NT_WS_FLOATS of partials.  1 = no split. */
+static int nt_splits(int T, int N, int K, int cus) {
+    const long long tiles = (long long)cdiv(T, 32) * cdiv(N, 32);
+    const int nch = cdiv(K, 32);
+    if (tiles >= cus || tiles > (long long)SGPU_NT_CNT) return 1;
+    long long S = 2LL * cus / tiles;
+    if (S > nch / 4) S = nch / 4;
+    if (S > 16) S = 16;
+    while (S > 1 && S * tiles * 1024 > (long long)SGPU_NT_WS_FLOATS) S--;
+    return S < 1 ? 1 : (int)S;
+}
+
+int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N, int T,
+                             float *ws, unsigned *cnt, void *stream) {
     if (K < 0 || N < 0 || T < 0) return SGPU_ERR_INVALID_ARG;
     if (N == 0 || T == 0) return SGPU_OK;
     if (!Y || (K > 0 && (!W || !X))) return SGPU_ERR_INVALID_ARG;
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    /* Too few 32x32 tiles to fill the CUs: split each tile's K over blocks (matrix-core path
+     * conditions: whole aligned quads and at least 4 tokens). */
+    const int mfma_ok = K > 0 && K % 4 == 0 && !(((uintptr_t)W | (uintptr_t)X) & 15) && T >= 4;
+    const int S = (mfma_ok && ws && cnt) ? nt_splits(T, N, K, d->cus) : 1;
+    if (S > 1) {
+        const long long tiles = (long long)cdiv(T, 32) * cdiv(N, 32);
+        unsigned g[3] = {(unsigned)(tiles * S), 1, 1}, b[3] = {256, 1, 1};
+        void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T, (void *)&S, &ws, &cnt};
+        return launch(d->fn[K_GEMV_MULTI_SPLITK], g, b, stream, args);
+    }
     unsigned g[3], b[3];
     geometry(d, "gemv_multi", T, N, K, g, b);
     void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T};
     return launch(d->fn[K_GEMV_MULTI], g, b, stream, args);
+}
+
+int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N, int T,
+                    void *stream) {
+    int rc;
+    devstate *d = (N > 0 && T > 0 && K >= 0) ? cur(&rc) : NULL;
+    return sgpu_internal_gemv_multi(W, X, bias, Y, K, N, T, d ? d->sk_ws : NULL, d ? d->sk_cnt : NULL, stream);
 }
 
 /* ---- Qwen support kernels ---- */
@@ -1106,15 +1137,16 @@ int sgpu_internal_pf_embed(const uint16_t *emb, const int *ids, int T, float *x,
 }
 
 int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, float *Y, int K, int N, int T,
-                          void *stream) {
+                          float *ws, unsigned *cnt, void *stream) {
     if (!W || !X || !Y || K <= 0 || N <= 0 || T <= 0 || K % 4 || ((uintptr_t)W & 7) || ((uintptr_t)X & 15))
         return SGPU_ERR_INVALID_ARG;
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
-    const long long tiles = (long long)cdiv(T, 32) * cdiv(N, 32);
-    unsigned g[3] = {(unsigned)(tiles < 0x7fffffffLL ? tiles : 0x7fffffffLL), 1, 1}, b[3] = {256, 1, 1};
-    void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T};
+    const int S = (ws && cnt) ? nt_splits(T, N, K, d->cus) : 1;
+    const long long units = (long long)cdiv(T, 32) * cdiv(N, 32) * S;
+    unsigned g[3] = {(unsigned)(units < 0x7fffffffLL ? units : 0x7fffffffLL), 1, 1}, b[3] = {256, 1, 1};
+    void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T, (void *)&S, &ws, &cnt};
     return launch(d->pf_gemm, g, b, stream, args);
 }
 

@@ -39,7 +39,15 @@ SGPU_HIDDEN int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, i
  * (positions pos0..pos0+T-1, pos0 + T <= 8192), and row SwiGLU over gate|up rows of 2*FC. */
 SGPU_HIDDEN int sgpu_internal_pf_embed(const uint16_t *emb, const int *ids, int T, float *x, int C, void *stream);
 SGPU_HIDDEN int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, float *Y, int K, int N,
-                                      int T, void *stream);
+                                      int T, float *ws, unsigned *cnt, void *stream);
+/* gemv_multi with an explicit split-K workspace (NULL: never split). */
+SGPU_HIDDEN int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N,
+                                         int T, float *ws, unsigned *cnt, void *stream);
+/* Split-K workspace of the batched matrix-core GEMMs (sgpu_internal_pf_gemm,
+ * sgpu_internal_gemv_multi): SGPU_NT_WS_FLOATS floats of partial tiles and SGPU_NT_CNT
+ * counters, zeroed once (every launch leaves them at zero). */
+#define SGPU_NT_WS_FLOATS (1u << 20)
+#define SGPU_NT_CNT 1024u
 SGPU_HIDDEN int sgpu_internal_pf_qkv_post(float *qkv, int T, int pos0, const float *cosT, const float *sinT,
                                           float *kc, float *vc, int NH, int NKV, int HD, void *stream);
 SGPU_HIDDEN int sgpu_internal_pf_attn(const float *qkv, const float *kc, const float *vc, float *out, int T,

@@ -162,8 +162,9 @@ def test_gemv_multi(gpu, og, T, with_bias):
 
 
 # (K, N, T): matrix-core path (32-token x 32-row tiles) with ragged token/row tiles, K tails
-# inside a 32-deep chunk, K shorter than the four-wave split, the GPT-2 shapes, and both
-# sides of the token-count switch to the vector path (T < 4, or T <= 8 with K > 1024).
+# inside a 32-deep chunk, K shorter than the four-wave split, the GPT-2 shapes, the vector
+# path (T < 4, unaligned rows), and shapes with fewer tiles than CUs, whose tiles' K is split
+# across blocks (the launcher's rule: up to 16 splits of at least four 32-deep chunks).
 MULTI_SHAPES = [(768, 2304, 128), (772, 100, 33), (64, 65, 1), (3072, 768, 64), (40, 1000, 300),
                 (768, 2048, 512), (36, 37, 31), (768, 50257, 3), (4, 7, 5), (3072, 3072, 257),
                 (64, 100, 3), (64, 100, 4), (1028, 40, 8), (1028, 40, 9), (1024, 40, 8)]
@@ -180,10 +181,12 @@ def test_gemv_multi_integer_shapes(gpu, K, N, T):
     db = gpu.DeviceArray.from_host(bias)
     dY = gpu.DeviceArray((T, N))
     dY.fill_bytes(0xFF)
-    gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, db.ptr, dY.ptr, K, N, T, None)
-    gpu.synchronize()
     want = (X @ W.T + bias.astype(np.int64)).astype(np.float32)    # |sum| < 2^24: exact
-    assert np.array_equal(dY.to_host(), want)
+    for _ in range(2):                         # split tiles leave their counters at zero
+        dY.fill_bytes(0xFF)
+        gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, db.ptr, dY.ptr, K, N, T, None)
+        gpu.synchronize()
+        assert np.array_equal(dY.to_host(), want)
 
 
 def test_gemv_multi_unaligned_rows_take_vector_path(gpu):
