@@ -317,9 +317,11 @@ def cpu_baseline(n, target_s=1.5):
 
 def pmc_probe():
     """One launch each of: add2 over 64 Mi floats (a plain elementwise kernel whose HBM
-    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), sgpu_sgemm_opt
-    4096^3 (sgemm_opt256) and the lm_head gemv_h.  Run under `rocprofv3 --pmc FETCH_SIZE` and again with
-    WRITE_SIZE; prints the algorithmic bytes of each launch as one JSON line."""
+    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration) and the lm_head
+    gemv_h, and ten back-to-back launches of sgpu_sgemm_opt 4096^3 (sgemm_opt256; per-dispatch
+    counters are averaged).  Run under `rocprofv3 --pmc FETCH_SIZE`, again with WRITE_SIZE,
+    and with the MFMA-busy counters; prints the algorithmic bytes of each launch as one JSON
+    line."""
     n = 64 << 20
     a = sgpu.DeviceArray(n)
     b = sgpu.DeviceArray(n)
@@ -334,7 +336,8 @@ def pmc_probe():
     A, B = sgpu.gen_sgemm_inputs(N4 * N4, 42)
     dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((N4, N4))
     sgpu.synchronize()
-    sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, N4, N4, N4, None)
+    for _ in range(10):
+        sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, N4, N4, N4, None)
     sgpu.synchronize()
     del dA, dB, dC
     N, K = 151936, 896
@@ -356,6 +359,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the SGEMM size sweep and GEMV shape legs (they replay recorded graphs)")
     ap.add_argument("--pmc-probe", action="store_true", help="one launch per measured kernel, for rocprofv3 --pmc")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (for profiling it)")
     ap.add_argument("--decode-path", choices=["reference", "fused", "graph"], default="graph")
@@ -390,10 +395,12 @@ def main():
     gv = bench_gemv_lm_head()
     log(f"gemv_h lm_head: {gv['us']:.1f} us, {gv['gbps']:.0f} GB/s ({gv['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), "
         f"err {gv['err']:.2e}")
-    sweep = bench_sgemm_sweep()
-    log("sgemm sweep (in-graph): " + ", ".join(f"{r['M']}x{r['N']}x{r['K']} {r['tflops']:.1f} TF" for r in sweep))
-    gshapes = bench_gemv_shapes()
-    log("gemv shapes (in-graph): " + ", ".join(f"{r['name']} {r['us_in_graph']:.2f} us" for r in gshapes))
+    sweep = gshapes = None
+    if not args.no_sweep:
+        sweep = bench_sgemm_sweep()
+        log("sgemm sweep (in-graph): " + ", ".join(f"{r['M']}x{r['N']}x{r['K']} {r['tflops']:.1f} TF" for r in sweep))
+        gshapes = bench_gemv_shapes()
+        log("gemv shapes (in-graph): " + ", ".join(f"{r['name']} {r['us_in_graph']:.2f} us" for r in gshapes))
     dec = g2 = None
     if not args.no_decode:
         dec = bench_decode()
