@@ -415,6 +415,91 @@ __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------
+// Few-token batched GEMV (gemv_multi role for T <= TT on aligned fp32 rows):
+// Y[t*N+n] = W[n,:].X[t,:] + bias?[n].  The decode GEMV's team scheme with TT input vectors:
+// a team of LPR lanes owns one row at a time, each lane holds S fixed 16-byte segments of
+// every token's X row in registers for the whole persistent row loop, streams its segments of
+// the row once (issued one row ahead of use) and accumulates all TT tokens from them; the
+// team then reduces the TT sums (DPP within a wave, wave sums through LDS for 256-lane
+// teams, fixed order).  Preconditions (launcher): blockDim 256, K % 4 == 0, W and X 16-byte
+// aligned, K/4 <= S*LPR, 1 <= T <= TT.
+template <int LPR, int S, int TT>
+__device__ __forceinline__ void gemv_multi_xreg(const float* __restrict__ W, const float* __restrict__ X,
+                                                const float* __restrict__ bias, float* __restrict__ Y, int K, int N,
+                                                int T) {
+    static_assert(LPR == 64 || LPR == 256, "team of one wave or of the block");
+    constexpr int TEAMS = 256 / LPR, WPT = LPR / 64;
+    __shared__ float red[TT][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int team = tid / LPR, sub = tid % LPR;
+    const int nseg = K / 4;
+    bool has[S];
+#pragma unroll
+    for (int j = 0; j < S; j++) has[j] = sub + LPR * j < nseg;
+    sgpu_f32x4 w[S];
+    auto fetch = [&](int n) __attribute__((always_inline)) {
+        const sgpu_f32x4* rv = reinterpret_cast<const sgpu_f32x4*>(W + (size_t)n * K) + sub;
+#pragma unroll
+        for (int j = 0; j < S; j++)
+            if (has[j]) w[j] = sgpu_ldnt(rv + LPR * j);
+    };
+    int n = blockIdx.x * TEAMS + team;
+    if (n < N) fetch(n);
+    float xr[TT][S][4];
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            const sgpu_f32x4 a = (t < T && has[j])
+                ? *reinterpret_cast<const sgpu_f32x4*>(X + (size_t)t * K + 4 * (sub + LPR * j))
+                : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) xr[t][j][e] = a[e];
+        }
+    const int stride = gridDim.x * TEAMS;
+    for (int nb = blockIdx.x * TEAMS; nb < N; nb += stride) {   // block-uniform loop
+        const bool cur = n < N;
+        const int cur_n = n;
+        float acc[TT];
+#pragma unroll
+        for (int t = 0; t < TT; t++) acc[t] = 0.0f;
+        if (cur) {
+#pragma unroll
+            for (int j = 0; j < S; j++)
+                if (has[j])
+#pragma unroll
+                    for (int t = 0; t < TT; t++) acc[t] = WF32::dot(w[j], xr[t][j], acc[t]);
+        }
+        n += stride;
+        if (n < N) fetch(n);
+        if constexpr (LPR == 64) {
+#pragma unroll
+            for (int t = 0; t < TT; t++) acc[t] = sgpu_group_sum<64>(acc[t]);
+            if (lane == 63 && cur) {
+                const float bv = bias ? bias[cur_n] : 0.0f;
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+                    if (t < T) Y[(size_t)t * N + cur_n] = acc[t] + bv;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                acc[t] = sgpu_group_sum<64>(acc[t]);
+                if (lane == 63) red[t][wave] = acc[t];
+            }
+            __syncthreads();
+            if (tid < TT && tid < T && cur) {
+                float v = red[tid][0];
+#pragma unroll
+                for (int i = 1; i < WPT; i++) v += red[tid][i];
+                Y[(size_t)tid * N + cur_n] = v + (bias ? bias[cur_n] : 0.0f);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // Batched GEMV on the fp32 matrix cores (gemv_multi role when K % 4 == 0 and the rows are
 // 16-byte aligned): Y[t*N+n] = sum_k W[n*K+k] * X[t*K+k] + bias?[n], with
 // v_mfma_f32_32x32x2_f32 (fp32 inputs, fp32 accumulate).

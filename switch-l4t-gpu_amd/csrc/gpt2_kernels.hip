@@ -71,6 +71,22 @@ __global__ void __launch_bounds__(256) gemv_multi_splitk(const float* __restrict
     sgpu::gemm_nt_mfma<1, sgpu::WF32, true>(W, X, bias, Y, K, N, T, S, ws, cnt);
 }
 
+// gemv_multi for 1..8 tokens on aligned rows: the register-resident team GEMV with eight
+// input vectors, a wave per row for K <= 1024 and a block per row for K <= 4096 (launcher's
+// choice; any grid of 256-thread blocks).
+__global__ void __launch_bounds__(256) gemv_multi_x8_l64(const float* __restrict__ W, const float* __restrict__ X,
+                                                         const float* __restrict__ bias, float* __restrict__ Y,
+                                                         int K, int N, int T) {
+    if (blockDim.x != 256) return;
+    sgpu::gemv_multi_xreg<64, 4, 8>(W, X, bias, Y, K, N, T);
+}
+__global__ void __launch_bounds__(256) gemv_multi_x8_l256(const float* __restrict__ W, const float* __restrict__ X,
+                                                          const float* __restrict__ bias, float* __restrict__ Y,
+                                                          int K, int N, int T) {
+    if (blockDim.x != 256) return;
+    sgpu::gemv_multi_xreg<256, 4, 8>(W, X, bias, Y, K, N, T);
+}
+
 // y = (x - mean) / sqrt(var + eps) * w + b per row (grid = rows), with the two-pass
 // mean/variance of the CPU golden (gpt2_engine.c:331-339).
 __global__ void __launch_bounds__(1024) layernorm(const float* __restrict__ x, const float* __restrict__ w,

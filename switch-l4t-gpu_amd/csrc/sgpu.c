@@ -45,7 +45,8 @@ static const struct {
 /* Every kernel the launchers use: (module, symbol). */
 enum {
     K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_NAIVE, K_MEMBW,
-    K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK,
+    K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK, K_GEMV_MULTI_X8_64,
+    K_GEMV_MULTI_X8_256,
     K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
     K_EMBED_H,
     K_LAYERNORM, K_GELU, K_ADD_BIAS, K_G2_SCORES, K_G2_SOFTMAX, K_G2_MIX,
@@ -60,6 +61,7 @@ static const struct {
     {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
+    {MOD_GPT2, "gemv_multi_x8_l64"}, {MOD_GPT2, "gemv_multi_x8_l256"},
     {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
     {MOD_QWEN, "attn_scores_gqa"}, {MOD_QWEN, "attn_softmax"}, {MOD_QWEN, "attn_mix_gqa"},
     {MOD_QWEN, "add2"},
@@ -701,9 +703,20 @@ int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, 
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    const int aligned = K > 0 && K % 4 == 0 && !(((uintptr_t)W | (uintptr_t)X) & 15);
+    /* Up to 8 tokens on aligned rows of at most 4096: the register-resident team GEMV with
+     * eight input vectors (a wave per row up to K = 1024, a block per row beyond; one block
+     * per 4 or 1 rows, capped at the 2 or 3 blocks per CU their registers allow). */
+    if (aligned && T <= 8 && K <= 4096) {
+        const int wide = K > 1024;
+        const unsigned teams = wide ? 1u : 4u, cap = (unsigned)d->cus * (wide ? 3u : 2u);
+        unsigned g[3] = {umin(cdiv(N, (int)teams), cap), 1, 1}, b[3] = {256, 1, 1};
+        void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T};
+        return launch(d->fn[wide ? K_GEMV_MULTI_X8_256 : K_GEMV_MULTI_X8_64], g, b, stream, args);
+    }
     /* Too few 32x32 tiles to fill the CUs: split each tile's K over blocks (matrix-core path
      * conditions: whole aligned quads and at least 4 tokens). */
-    const int mfma_ok = K > 0 && K % 4 == 0 && !(((uintptr_t)W | (uintptr_t)X) & 15) && T >= 4;
+    const int mfma_ok = aligned && T >= 4;
     const int S = (mfma_ok && ws && cnt) ? nt_splits(T, N, K, d->cus) : 1;
     if (S > 1) {
         const long long tiles = (long long)cdiv(T, 32) * cdiv(N, 32);

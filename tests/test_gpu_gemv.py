@@ -162,12 +162,15 @@ def test_gemv_multi(gpu, og, T, with_bias):
 
 
 # (K, N, T): matrix-core path (32-token x 32-row tiles) with ragged token/row tiles, K tails
-# inside a 32-deep chunk, K shorter than the four-wave split, the GPT-2 shapes, the vector
-# path (T < 4, unaligned rows), and shapes with fewer tiles than CUs, whose tiles' K is split
-# across blocks (the launcher's rule: up to 16 splits of at least four 32-deep chunks).
+# inside a 32-deep chunk, K shorter than the four-wave split, the GPT-2 shapes, shapes with
+# fewer tiles than CUs, whose tiles' K is split across blocks (the launcher's rule: up to 16
+# splits of at least four 32-deep chunks), and up to 8 tokens on aligned rows, which take the
+# register team GEMV (a wave per row to K = 1024, a block per row to K = 4096; beyond, the
+# split matrix-core path).
 MULTI_SHAPES = [(768, 2304, 128), (772, 100, 33), (64, 65, 1), (3072, 768, 64), (40, 1000, 300),
                 (768, 2048, 512), (36, 37, 31), (768, 50257, 3), (4, 7, 5), (3072, 3072, 257),
-                (64, 100, 3), (64, 100, 4), (1028, 40, 8), (1028, 40, 9), (1024, 40, 8)]
+                (64, 100, 3), (64, 100, 4), (1028, 40, 8), (1028, 40, 9), (1024, 40, 8),
+                (4096, 96, 8), (4100, 96, 8), (3072, 768, 2)]
 
 
 @pytest.mark.parametrize("K,N,T", MULTI_SHAPES)
