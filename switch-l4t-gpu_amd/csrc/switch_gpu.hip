@@ -17,9 +17,10 @@
 // fp32 accumulate; no reduced-precision xf32).  A block of 64*WGM*WGN threads owns a BMxBN
 // tile of C; each wave owns a (BM/WGM)x(BN/WGN) sub-tile held as 32x32 MFMA blocks.
 // A and B k-slices of depth BK are staged through LDS, double-buffered (one barrier per
-// slice; in the large members it sits before the slice's last MFMA group, so the next
-// slice's first operand reads overlap that group): A either k-major with a 2-float row pad
-// or m-major with a 4-float pad, B row-major with a pad.  Tiles are walked with a grid-stride
+// slice, before the slice's last MFMA group on whole tiles, so the next slice's first
+// operand reads overlap that group): A m-major with a 4-float row pad, B row-major with an
+// 8-float pad.  The 64x64 members keep two slices' global loads in flight (their slices are
+// short next to the load latency).  Tiles are walked with a grid-stride
 // loop over a linear tile index, so any grid of 64*WGM*WGN-thread blocks is correct (surplus
 // blocks exit); with one block per tile the index is remapped so each XCD (blocks are dealt
 // round-robin to the 8 XCDs) works on a compact group of tiles that shares A and B panels in
@@ -41,14 +42,11 @@ struct MfmaTile {
     static constexpr int NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN;   // wave tile
     static constexpr int FM = WTM / 32, FN = WTN / 32;      // 32x32 MFMA blocks per wave
-    static constexpr int LDA = BM + 2;                      // As[BK][LDA], k-major
-    static constexpr int LDB = BN;                          // Bs[BK][LDB]
     static constexpr int KQ = BK / 4, NQ = BN / 4;          // float4 per A row / per B row
     static constexpr int A_PER_T = (BM * KQ) / NT;          // float4 loads per thread
     static constexpr int B_PER_T = (BK * NQ) / NT;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     static_assert(BK % 4 == 0 && (BM * KQ) % NT == 0 && (BK * NQ) % NT == 0, "load split");
-    static_assert(BM % 8 == 0, "LDA pad trick needs BM % 8 == 0");
 };
 
 // Map a linear tile id to (tile_m, tile_n).  With exactly one block per tile and a tile
@@ -65,13 +63,6 @@ __device__ __forceinline__ void sgemm_tile_coords(int t, int ntm, int ntn, bool 
     tn = r / gsz;
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN>
-struct SgemmLds {
-    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    float As[2][BK][T::LDA];
-    float Bs[2][BK][T::LDB];
-};
-
 // Per-thread constants of one tile's staging and operand reads.
 template <int BM, int BN, int BK, int WGM, int WGN>
 struct SgemmThread {
@@ -86,26 +77,6 @@ struct SgemmThread {
         khalf = lane >> 5;
     }
 };
-
-// Registers -> LDS buffer s (A transposed to k-major).
-template <int BM, int BN, int BK, int WGM, int WGN>
-__device__ __forceinline__ void sgemm_store_slice(SgemmLds<BM, BN, BK, WGM, WGN>& L, int s, int tid,
-                                                  const sgpu_f32x4* ra, const sgpu_f32x4* rb) {
-    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-#pragma unroll
-    for (int r = 0; r < T::A_PER_T; r++) {
-        const int idx = tid + r * T::NT, row = idx / T::KQ, kq = idx % T::KQ;
-        L.As[s][4 * kq + 0][row] = ra[r].x;
-        L.As[s][4 * kq + 1][row] = ra[r].y;
-        L.As[s][4 * kq + 2][row] = ra[r].z;
-        L.As[s][4 * kq + 3][row] = ra[r].w;
-    }
-#pragma unroll
-    for (int r = 0; r < T::B_PER_T; r++) {
-        const int idx = tid + r * T::NT, kr = idx / T::NQ, nq = idx % T::NQ;
-        *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][kr][4 * nq]) = rb[r];
-    }
-}
 
 // D layout of a 32x32 block: lane l, acc r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
 template <int BM, int BN, int BK, int WGM, int WGN>
@@ -126,78 +97,7 @@ __device__ __forceinline__ void sgemm_store_c(float* __restrict__ C, int M, int 
         }
 }
 
-// One interior tile with K a multiple of BK (at least two slices) and 16-byte aligned rows:
-// software-pipelined.  Slice kt+1's global loads are issued before slice kt's MFMAs; each
-// k-step's LDS operands are read one step ahead into a second register set, so their
-// latency runs under the previous step's MFMAs; slice kt+1 is written to the idle LDS buffer
-// after MFMA step STORE_AT of slice kt, once its loads have had that long to land.  One
-// barrier per slice.  (Edge tiles of the same member run the m-major masked pipeline, whose
-// k order inside each 8-deep group differs, so their sums round independently of these.)
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT>
-__device__ __forceinline__ void sgemm_tile_fast(const float* __restrict__ A, const float* __restrict__ B,
-                                                int N, int K, int lda, int m0, int n0,
-                                                SgemmLds<BM, BN, BK, WGM, WGN>& L,
-                                                const SgemmThread<BM, BN, BK, WGM, WGN>& th,
-                                                sgpu_f32x16 (&acc)[BM / WGM / 32][BN / WGN / 32]) {
-    using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    constexpr int NS = BK / 2;                    // MFMA k-steps per slice
-    static_assert(STORE_AT >= 0 && STORE_AT < NS, "store point inside the slice");
-    const int tid = th.tid, nk = K / BK;
-    static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
-    // Load round r of a thread reads A row (tid/KQ + r*NT/KQ) and B row (tid/NQ + r*NT/NQ):
-    // one base pointer each plus wave-uniform strides.
-    const float* pa = A + (size_t)(m0 + tid / T::KQ) * lda + 4 * (tid % T::KQ);
-    const float* pb = B + (size_t)(tid / T::NQ) * N + n0 + 4 * (tid % T::NQ);
-    const size_t astep = (size_t)(T::NT / T::KQ) * lda, bstep_r = (size_t)(T::NT / T::NQ) * N;
-    const size_t bstep = (size_t)BK * N;
-    sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
-    auto load_slice = [&](int kt) __attribute__((always_inline)) {
-#pragma unroll
-        for (int r = 0; r < T::A_PER_T; r++)
-            ra[r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
-#pragma unroll
-        for (int r = 0; r < T::B_PER_T; r++)
-            rb[r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
-    };
-    auto read_ops = [&](int s, int ks, float* a, float* b) __attribute__((always_inline)) {
-        const int kk = 2 * ks + th.khalf;
-#pragma unroll
-        for (int i = 0; i < T::FM; i++) a[i] = L.As[s][kk][th.wm * T::WTM + i * 32 + th.l32];
-#pragma unroll
-        for (int j = 0; j < T::FN; j++) b[j] = L.Bs[s][kk][th.wn * T::WTN + j * 32 + th.l32];
-    };
-    auto slice = [&](int s, bool more) __attribute__((always_inline)) {
-        float a[2][T::FM], b[2][T::FN];
-        read_ops(s, 0, a[0], b[0]);
-#pragma unroll
-        for (int ks = 0; ks < NS; ks++) {
-            const int c = ks & 1;
-            if (ks + 1 < NS) read_ops(s, ks + 1, a[c ^ 1], b[c ^ 1]);
-            __builtin_amdgcn_sched_barrier(0);    // keep the next step's reads ahead of these MFMAs
-#pragma unroll
-            for (int i = 0; i < T::FM; i++)
-#pragma unroll
-                for (int j = 0; j < T::FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
-            if (more && ks == STORE_AT) sgemm_store_slice(L, s ^ 1, tid, ra, rb);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    load_slice(0);
-    sgemm_store_slice(L, 0, tid, ra, rb);
-    __syncthreads();
-    for (int kt = 0; kt + 1 < nk; kt++) {
-        load_slice(kt + 1);
-        __builtin_amdgcn_sched_barrier(0);        // issue the loads before the first MFMA
-        slice(kt & 1, true);
-        __syncthreads();
-    }
-    slice((nk - 1) & 1, false);
-    __syncthreads();                              // the next tile overwrites both buffers
-}
-
-// Second LDS layout for the pipelined path: A m-major (row pitch BK+4 floats), B k-major
+// LDS layout of the pipeline: A m-major (row pitch BK+4 floats), B k-major
 // (row pitch BN+8).  Both are written straight from the dwordx4 global loads.  Inside a
 // slice the MFMA k-steps run in groups of four with the k order permuted per lane half:
 // at step t of group g, lane half h supplies k = 8g + 4h + t, so a lane's four A operands of
@@ -220,7 +120,7 @@ struct SgemmLdsM {
 //   is applied to data.  Floats are written to LDS one each.
 //   MODE 2 (larger operands): dwordx4-shaped map, each float loaded from a clamped
 //   (in-bounds) 64-bit address and zeroed outside A or B when the slice is written to LDS.
-template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, bool SPREAD = false, int MODE = 0, bool EARLY = false>
+template <int BM, int BN, int BK, int WGM, int WGN, int STORE_G, int MODE = 0, bool EARLY = false, int PF = 1>
 __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, const float* __restrict__ B,
                                                   int M, int N, int K, int lda, int m0, int n0,
                                                   SgemmLdsM<BM, BN, BK, WGM, WGN>& L,
@@ -232,6 +132,7 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     static_assert(BK % 8 == 0, "k slice of whole 8-deep groups");
     static_assert(STORE_G >= 0 && STORE_G < NG, "store point inside the slice");
     static_assert(!EARLY || (STORE_G < NG - 1 && NG % 2 == 0), "early barrier: store before the last group");
+    static_assert(PF == 1 || (PF == 2 && MODE == 0), "two slices in flight on the dwordx4 path only");
     static_assert(T::NT % T::KQ == 0 && T::NT % T::NQ == 0, "whole rows per load round");
     static_assert(MODE != 1 || (T::NT % BK == 0 && T::NT % BN == 0), "lane map: whole rows per round");
     constexpr int AE = 4 * T::A_PER_T, BE = 4 * T::B_PER_T;   // staged floats per thread
@@ -252,16 +153,21 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
     // MODE 2 map
     const int ar0 = m0 + tid / T::KQ, ak0 = 4 * (tid % T::KQ);
     const int bk0 = tid / T::NQ, bn0 = n0 + 4 * (tid % T::NQ);
-    sgpu_f32x4 ra[T::A_PER_T], rb[T::B_PER_T];
+    // Staging registers: PF sets (PF = 2: slice kt+1 waits in one set while slice kt+2 loads
+    // into the other).  Set indices are compile-time (set_c) everywhere.
+    sgpu_f32x4 ras[PF][T::A_PER_T], rbs[PF][T::B_PER_T];
+    sgpu_f32x4 (&ra)[T::A_PER_T] = ras[0];
+    sgpu_f32x4 (&rb)[T::B_PER_T] = rbs[0];
     float sa[AE], sb[BE];
-    auto load_slice = [&](int kt) __attribute__((always_inline)) {
+    auto load_slice = [&](int kt, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
         if constexpr (MODE == 0) {
 #pragma unroll
             for (int r = 0; r < T::A_PER_T; r++)
-                ra[r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
+                ras[SET][r] = *reinterpret_cast<const sgpu_f32x4*>(pa + r * astep + (size_t)kt * BK);
 #pragma unroll
             for (int r = 0; r < T::B_PER_T; r++)
-                rb[r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
+                rbs[SET][r] = *reinterpret_cast<const sgpu_f32x4*>(pb + r * bstep_r + (size_t)kt * bstep);
         } else if constexpr (MODE == 1) {
             const unsigned ao = kt * BK + ak < K ? a_off0 + (unsigned)(kt * BK) * 4u : kOut;
 #pragma unroll
@@ -307,17 +213,18 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
             }
         }
     };
-    auto store_slice = [&](int s) __attribute__((always_inline)) {
+    auto store_slice = [&](int s, auto set_c) __attribute__((always_inline)) {
+        constexpr int SET = decltype(set_c)::value;
         if constexpr (MODE != 1) {
 #pragma unroll
             for (int r = 0; r < T::A_PER_T; r++) {
                 const int idx = tid + r * T::NT;
-                *reinterpret_cast<sgpu_f32x4*>(&L.As[s][idx / T::KQ][4 * (idx % T::KQ)]) = ra[r];
+                *reinterpret_cast<sgpu_f32x4*>(&L.As[s][idx / T::KQ][4 * (idx % T::KQ)]) = ras[SET][r];
             }
 #pragma unroll
             for (int r = 0; r < T::B_PER_T; r++) {
                 const int idx = tid + r * T::NT;
-                *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][idx / T::NQ][4 * (idx % T::NQ)]) = rb[r];
+                *reinterpret_cast<sgpu_f32x4*>(&L.Bs[s][idx / T::NQ][4 * (idx % T::NQ)]) = rbs[SET][r];
             }
         } else {
 #pragma unroll
@@ -336,28 +243,27 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
 #pragma unroll
             for (int j = 0; j < T::FN; j++) b[j][t] = L.Bs[s][kc + t][th.wn * T::WTN + j * 32 + th.l32];
     };
-    // SPREAD: the slice's memory instructions (next slice's global loads in group 0, next
-    // group's LDS reads, the slice store in group STORE_G) are dealt out one per MFMA instead
-    // of issued in bursts, so the MFMA stream never waits behind a full memory queue.
+    // The slice's memory instructions (next slice's global loads in group 0, next group's LDS
+    // reads, the slice store in group STORE_G) are dealt out one per MFMA instead of issued in
+    // bursts, so the MFMA stream never waits behind a full memory queue.
     // EARLY: the slice's barrier sits before its last group instead of after it, and that
     // group's MFMAs run under the LDS reads of the next slice's first group (the next slice
     // was stored at group STORE_G < NG-1; every read of this slice's buffer except the last
     // group's was issued, and waited for, before the barrier), so no LDS latency is exposed
     // between slices.
+    // A slice with `more` loads slice kt_ld into staging set LS (in group 0) and writes set SS,
+    // holding slice kt_st, to the idle buffer s^1 (at group STORE_G).
     sgpu_f32x4 a[2][T::FM], b[2][T::FN];
-    auto slice = [&](int s, int kt_next, auto more_c) __attribute__((always_inline)) {
+    using Z = std::integral_constant<int, 0>;
+    auto slice = [&](int s, int kt_ld, int kt_st, auto more_c, auto ls_c, auto ss_c) __attribute__((always_inline)) {
         constexpr bool more = decltype(more_c)::value;
         constexpr int NMF = 4 * T::FM * T::FN;
         constexpr int NLD = (MASKED ? 4 : 1) * (T::A_PER_T + T::B_PER_T);   // global loads
         constexpr int LPM = (NLD + NMF - 1) / NMF;                            // ... per MFMA slot
         constexpr int NST = (MODE == 1 ? 4 : 1) * (T::A_PER_T + T::B_PER_T);  // LDS writes
         constexpr int WPM = (NST + NMF / 2 - 1) / (NMF / 2);                  // ... per slot (half group)
-        if constexpr (!SPREAD) {
-            if (more) load_slice(kt_next);
-            __builtin_amdgcn_sched_barrier(0);
-        }
         if constexpr (!EARLY) read_group(s, 0, a[0], b[0]);
-        if constexpr (SPREAD) __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
             const int c = g & 1;
@@ -366,12 +272,9 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
                 __syncthreads();
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (SPREAD) {
-                if (more && g == 0) load_slice(kt_next);
-            }
+            if (more && g == 0) load_slice(kt_ld, ls_c);
             if (g + 1 < NG) read_group(s, g + 1, a[c ^ 1], b[c ^ 1]);
             else if (rd_next) read_group(s ^ 1, 0, a[c ^ 1], b[c ^ 1]);
-            if constexpr (!SPREAD) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -380,63 +283,72 @@ __device__ __forceinline__ void sgemm_tile_fast_m(const float* __restrict__ A, c
                     for (int j = 0; j < T::FN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[c][i][t], b[c][j][t], acc[i][j], 0, 0, 0);
             if (more && g == STORE_G) {
-                if constexpr (MASKED) mask_slice(kt_next);
-                store_slice(s ^ 1);
+                if constexpr (MASKED) mask_slice(kt_st);
+                store_slice(s ^ 1, ss_c);
             }
-            if constexpr (SPREAD) {
 #pragma unroll
-                for (int q = 0; q < NMF; q++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // 1 MFMA
-                    if (more && g == 0 && q * LPM < NLD)
-                        __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);            // global loads
-                    if ((g + 1 < NG || rd_next) && q < T::FM + 4 * T::FN)
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);              // 1 LDS read
-                    if (more && g == STORE_G && q >= NMF / 2 && (q - NMF / 2) * WPM < NST)
-                        __builtin_amdgcn_sched_group_barrier(0x200, WPM, 0);            // LDS writes
-                }
+            for (int q = 0; q < NMF; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // 1 MFMA
+                if (more && g == 0 && q * LPM < NLD)
+                    __builtin_amdgcn_sched_group_barrier(0x020, LPM, 0);                // global loads
+                if ((g + 1 < NG || rd_next) && q < T::FM + 4 * T::FN)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                  // 1 LDS read
+                if (more && g == STORE_G && q >= NMF / 2 && (q - NMF / 2) * WPM < NST)
+                    __builtin_amdgcn_sched_group_barrier(0x200, WPM, 0);                // LDS writes
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    load_slice(0);
+    load_slice(0, Z{});
     if constexpr (MASKED) mask_slice(0);
-    store_slice(0);
-    __syncthreads();
-    if constexpr (EARLY) read_group(0, 0, a[0], b[0]);
-    for (int kt = 0; kt + 1 < nk; kt++) {
-        slice(kt & 1, kt + 1, std::true_type{});
-        if constexpr (!EARLY) __syncthreads();
+    store_slice(0, Z{});
+    if constexpr (PF == 2) {
+        // Slice 1 into set 1 before the loop; slice kt (buffer kt & 1) loads slice kt+2 into
+        // set kt & 1 and writes slice kt+1 from the other set, so each slice's loads have a
+        // whole slice to land.  Loads past the last slice re-read slice nk-1 (never stored).
+        using O = std::integral_constant<int, 1>;
+        load_slice(min(1, nk - 1), O{});
+        __syncthreads();
+        if constexpr (EARLY) read_group(0, 0, a[0], b[0]);
+        for (int kt = 0;; kt += 2) {
+            if (kt + 1 >= nk) {
+                slice(0, 0, 0, std::false_type{}, Z{}, Z{});
+                break;
+            }
+            slice(0, min(kt + 2, nk - 1), kt + 1, std::true_type{}, Z{}, O{});
+            if constexpr (!EARLY) __syncthreads();
+            if (kt + 2 >= nk) {
+                slice(1, 0, 0, std::false_type{}, O{}, O{});
+                break;
+            }
+            slice(1, min(kt + 3, nk - 1), kt + 2, std::true_type{}, O{}, Z{});
+            if constexpr (!EARLY) __syncthreads();
+        }
+    } else {
+        __syncthreads();
+        if constexpr (EARLY) read_group(0, 0, a[0], b[0]);
+        for (int kt = 0; kt + 1 < nk; kt++) {
+            slice(kt & 1, kt + 1, kt + 1, std::true_type{}, Z{}, Z{});
+            if constexpr (!EARLY) __syncthreads();
+        }
+        slice((nk - 1) & 1, 0, 0, std::false_type{}, Z{}, Z{});
     }
-    slice((nk - 1) & 1, 0, std::false_type{});
     __syncthreads();
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN>
-union SgemmLdsU {
-    SgemmLds<BM, BN, BK, WGM, WGN> k;
-    SgemmLdsM<BM, BN, BK, WGM, WGN> m;
-};
-
-template <int BM, int BN, int BK, int WGM, int WGN>
-__device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLds<BM, BN, BK, WGM, WGN>& l) { return l; }
-template <int BM, int BN, int BK, int WGM, int WGN>
-__device__ __forceinline__ SgemmLds<BM, BN, BK, WGM, WGN>& sgemm_lds_k(SgemmLdsU<BM, BN, BK, WGM, WGN>& u) { return u.k; }
-
 // Whole tiles of a problem with 16-byte rows and K whole slices run the dwordx4 pipeline
-// with the slice store after k-step (LAYOUT 0) or 4-step group (LAYOUT 1-3) STORE_AT;
-// LAYOUT 0: k-major A staging; 1: m-major A staging; 2: m-major with memory instructions
-// spread one per MFMA; 3: as 2, with each slice's barrier moved before its last group.
-// All other tiles run the masked m-major pipeline (spread for LAYOUT 2 and 3, barrier at
+// with the slice store after 4-step group STORE_AT; LAYOUT 2: memory instructions spread one
+// per MFMA; 3: as 2, with each slice's barrier moved before its last group; 4: as 3, with
+// two slices' loads in flight.  All other tiles run the masked pipeline (spread, barrier at
 // the end of the slice).
 template <int BM, int BN, int BK, int WGM, int WGN, int STORE_AT, int LAYOUT, bool SPLIT = false>
 __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const float* __restrict__ B,
                                            float* __restrict__ C, int M, int N, int K, int S = 1,
                                            float* __restrict__ ws = nullptr, unsigned* __restrict__ cnt = nullptr) {
     using T = MfmaTile<BM, BN, BK, WGM, WGN>;
-    static_assert(STORE_AT >= 0, "store point");
-    __shared__ __attribute__((aligned(16))) SgemmLdsU<BM, BN, BK, WGM, WGN> LU;
-    SgemmLds<BM, BN, BK, WGM, WGN>& L = sgemm_lds_k(LU);
+    static_assert(STORE_AT >= 0 && LAYOUT >= 2 && LAYOUT <= 4, "store point and layout");
+    __shared__ __attribute__((aligned(16))) SgemmLdsM<BM, BN, BK, WGM, WGN> LM;
 
     // The tile split assumes exactly NT threads per block; any other block size is rejected
     // by every thread alike (no barrier is reached, C is left untouched).
@@ -539,8 +451,8 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
                 if (kext > 0)
-                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, SG, LAYOUT >= 2, MODE, false>(
-                        A + k0, B + (size_t)k0 * N, M, N, kext, K, m0, n0, LU.m, th, acc);
+                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, SG, MODE, false>(
+                        A + k0, B + (size_t)k0 * N, M, N, kext, K, m0, n0, LM, th, acc);
                 finish(u, m0, n0, interior, acc);
             }
         };
@@ -562,12 +474,8 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                     for (int j = 0; j < T::FN; j++)
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-                if constexpr (LAYOUT >= 1)
-                    sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, LAYOUT >= 2, 0, LAYOUT == 3>(
-                        A + k0, B + (size_t)k0 * N, M, N, kext, K, m0, n0, LU.m, th, acc);
-                else
-                    sgemm_tile_fast<BM, BN, BK, WGM, WGN, STORE_AT>(A + k0, B + (size_t)k0 * N, N, kext, K, m0, n0, L,
-                                                                    th, acc);
+                sgemm_tile_fast_m<BM, BN, BK, WGM, WGN, STORE_AT, 0, LAYOUT >= 3, LAYOUT == 4 ? 2 : 1>(
+                    A + k0, B + (size_t)k0 * N, M, N, kext, K, m0, n0, LM, th, acc);
                 finish(u, m0, n0, true, acc);
             }
         }
@@ -581,19 +489,19 @@ extern "C" {
 // The tiled members differ only in tile shape and staging; each runs interior tiles of
 // 16-byte-row problems with K a multiple of BK on the dwordx4 pipeline and every other tile
 // on the masked pipeline (edges, K tails, unaligned rows).
-//   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), k-major A
-//                  staging -- small shapes
-//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks), m-major A staging,
-//                  memory instructions spread over the MFMA stream, early slice barrier
-//   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks), m-major A staging,
-//                  spread, early slice barrier -- large shapes
+// All of them stage A m-major, deal their memory instructions out over the MFMA stream and
+// put the slice barrier before the last MFMA group.
+//   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), two slices'
+//                  loads in flight -- small shapes
+//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks)
+//   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks) -- large shapes
 //   sgemm_opt256 : 256x256 tile, BK 32, 4 waves of 128x128 (4x4 blocks), one wave per SIMD
 //                  (138 KB of LDS, 256 accumulator registers): half the LDS operand traffic
 //                  per flop of the 64x128 wave tile and 16384 MFMA cycles between barriers --
 //                  shapes whose 256x256 tiles fill the CUs in whole rounds
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<64, 64, 32, 2, 2, 8, 0>(A, B, C, M, N, K);
+    sgemm_mfma<64, 64, 32, 2, 2, 1, 4>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -617,7 +525,7 @@ sgemm_opt256(const float* __restrict__ A, const float* __restrict__ B, float* __
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 sgemm_splitk(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
              int S, float* __restrict__ ws, unsigned* __restrict__ cnt) {
-    sgemm_mfma<64, 64, 32, 2, 2, 1, 3, true>(A, B, C, M, N, K, S, ws, cnt);
+    sgemm_mfma<64, 64, 32, 2, 2, 1, 4, true>(A, B, C, M, N, K, S, ws, cnt);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:
