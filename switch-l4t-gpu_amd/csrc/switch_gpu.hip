@@ -19,8 +19,8 @@
 // A and B k-slices of depth BK are staged through LDS, double-buffered (one barrier per
 // slice, before the slice's last MFMA group on whole tiles, so the next slice's first
 // operand reads overlap that group): A m-major with a 4-float row pad, B row-major with an
-// 8-float pad.  The 64x64 members keep two slices' global loads in flight (their slices are
-// short next to the load latency).  Tiles are walked with a grid-stride
+// 8-float pad.  The 64x64 and 128x128 members keep two slices' global loads in flight (their
+// slices are short next to the load latency).  Tiles are walked with a grid-stride
 // loop over a linear tile index, so any grid of 64*WGM*WGN-thread blocks is correct (surplus
 // blocks exit); with one block per tile the index is remapped so each XCD (blocks are dealt
 // round-robin to the 8 XCDs) works on a compact group of tiles that shares A and B panels in
@@ -493,7 +493,8 @@ extern "C" {
 // put the slice barrier before the last MFMA group.
 //   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), two slices'
 //                  loads in flight -- small shapes
-//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks)
+//   sgemm_tiled4 : 128x128 tile, BK 16, 4 waves of 64x64 (2x2 blocks), two slices' loads
+//                  in flight
 //   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks) -- large shapes
 //   sgemm_opt256 : 256x256 tile, BK 32, 4 waves of 128x128 (4x4 blocks), one wave per SIMD
 //                  (138 KB of LDS, 256 accumulator registers): half the LDS operand traffic
@@ -506,7 +507,7 @@ sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __r
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 128, 32, 2, 2, 1, 3>(A, B, C, M, N, K);
+    sgemm_mfma<128, 128, 16, 2, 2, 0, 4>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
