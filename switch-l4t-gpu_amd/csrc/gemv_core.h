@@ -648,18 +648,33 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
                          (unsigned)(nsplit - 1);
             __syncthreads();
             if (!last_s) continue;                  // block-uniform; staging is free again
+            // Partials come back U splits at a time, every load of a round issued before the
+            // first add (one round trip per round instead of one per split), summed in split order.
+            constexpr int U = 16;
             float sum[FN][RPW];
-            for (int s2 = 0; s2 < nsplit; s2++) {
-                const float* src = ws + (size_t)(s2 * ntiles + tile) * REC + tid;
+            for (int s0 = 0; s0 < nsplit; s0 += U) {
+                float o[U][FN][RPW];
 #pragma unroll
-                for (int f = 0; f < FN; f++)
+                for (int u = 0; u < U; u++) {
+                    const int s2 = s0 + u;
+                    const float* src = ws + (size_t)(s2 * ntiles + tile) * REC + tid;
 #pragma unroll
-                    for (int rr = 0; rr < RPW; rr++) {
-                        const float o = s2 == sp ? v[f][rr]
-                                                 : __hip_atomic_load(src + (f * RPW + rr) * 256, __ATOMIC_RELAXED,
-                                                                     __HIP_MEMORY_SCOPE_AGENT);
-                        sum[f][rr] = s2 == 0 ? o : sum[f][rr] + o;
-                    }
+                    for (int f = 0; f < FN; f++)
+#pragma unroll
+                        for (int rr = 0; rr < RPW; rr++)
+                            o[u][f][rr] = s2 >= nsplit || s2 == sp
+                                              ? v[f][rr]
+                                              : __hip_atomic_load(src + (f * RPW + rr) * 256, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int u = 0; u < U; u++)
+                    if (s0 + u < nsplit)
+#pragma unroll
+                        for (int f = 0; f < FN; f++)
+#pragma unroll
+                            for (int rr = 0; rr < RPW; rr++)
+                                sum[f][rr] = s0 + u == 0 ? o[u][f][rr] : sum[f][rr] + o[u][f][rr];
             }
 #pragma unroll
             for (int f = 0; f < FN; f++)

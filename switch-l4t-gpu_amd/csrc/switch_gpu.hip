@@ -400,20 +400,37 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                              (unsigned)(nsplit - 1);
                 __syncthreads();
                 if (!last_s) return;
+                // U splits per round, every load of a round issued before the first add (one
+                // round trip per round, not per split); sums in split order.
+                constexpr int U = 4;
                 sgpu_f32x16 sum[T::FM][T::FN];
-                for (int s2 = 0; s2 < nsplit; s2++) {
-                    const float* src = ws + (size_t)(s2 * ntiles + t) * TILE + th.tid;
+                for (int s0 = 0; s0 < nsplit; s0 += U) {
+                    sgpu_f32x16 o[U][T::FM][T::FN];
 #pragma unroll
-                    for (int i = 0; i < T::FM; i++)
+                    for (int u = 0; u < U; u++) {
+                        const int s2 = s0 + u;
+                        const float* src = ws + (size_t)(s2 * ntiles + t) * TILE + th.tid;
 #pragma unroll
-                        for (int j = 0; j < T::FN; j++)
+                        for (int i = 0; i < T::FM; i++)
 #pragma unroll
-                            for (int r = 0; r < 16; r++) {
-                                const float v = s2 == sp ? acc[i][j][r]
-                                                         : __hip_atomic_load(src + ((i * T::FN + j) * 16 + r) * T::NT,
-                                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                                sum[i][j][r] = s2 == 0 ? v : sum[i][j][r] + v;
-                            }
+                            for (int j = 0; j < T::FN; j++)
+#pragma unroll
+                                for (int r = 0; r < 16; r++)
+                                    o[u][i][j][r] = s2 >= nsplit || s2 == sp
+                                                        ? acc[i][j][r]
+                                                        : __hip_atomic_load(src + ((i * T::FN + j) * 16 + r) * T::NT,
+                                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+#pragma unroll
+                    for (int u = 0; u < U; u++)
+                        if (s0 + u < nsplit)
+#pragma unroll
+                            for (int i = 0; i < T::FM; i++)
+#pragma unroll
+                                for (int j = 0; j < T::FN; j++)
+#pragma unroll
+                                    for (int r = 0; r < 16; r++)
+                                        sum[i][j][r] = s0 + u == 0 ? o[u][i][j][r] : sum[i][j][r] + o[u][i][j][r];
                 }
                 sgemm_store_c(C, M, N, m0, n0, interior, th, sum);
                 if (th.tid == 0) __hip_atomic_store(cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
