@@ -570,7 +570,14 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
         for (int f = 0; f < FN; f++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[f][r] = 0.0f;
-        sgpu_f32x4 g[NI];
+        // Staged chunk in registers: fp32 rows as loaded; fp16 rows as their raw codes, decoded
+        // only when written to LDS, so the loads stay in flight under the previous chunk's MFMAs.
+        // Staged chunk in registers: fp32 rows as loaded; fp16 rows as their raw codes, decoded
+        // only when written to LDS, so the loads stay in flight under the previous chunk's MFMAs.
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        constexpr bool H = sizeof(typename WT::elem) == 2;
+        sgpu_f32x4 g[H ? 4 : NI];
+        u32x2 gh[H ? NI - 4 : 1];
         auto load = [&](int c) __attribute__((always_inline)) {
             const int k0 = 32 * c;
             const bool ok = k0 + 4 * lq < K;                // K % 4 == 0: whole quads
@@ -579,18 +586,26 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
             for (int q = 0; q < 4; q++) g[q] = ok ? *reinterpret_cast<const sgpu_f32x4*>(xsrc[q] + k0) : z;
 #pragma unroll
             for (int q = 4; q < NI; q++) {
-                if constexpr (sizeof(typename WT::elem) == 4) {
+                if constexpr (!H)
                     g[q] = ok ? *reinterpret_cast<const sgpu_f32x4*>(wsrc[q - 4] + k0) : z;
-                } else {
-                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                    const u32x2 h = ok ? *reinterpret_cast<const u32x2*>(wsrc[q - 4] + k0) : u32x2{0u, 0u};
-                    g[q] = sgpu_f32x4{sgpu_h2f_lo(h[0]), sgpu_h2f_hi(h[0]), sgpu_h2f_lo(h[1]), sgpu_h2f_hi(h[1])};
-                }
+                else
+                    gh[q - 4] = ok ? *reinterpret_cast<const u32x2*>(wsrc[q - 4] + k0) : u32x2{0u, 0u};
             }
         };
         auto chunk = [&](bool more, int cn) __attribute__((always_inline)) {
 #pragma unroll
-            for (int q = 0; q < NI; q++) *reinterpret_cast<sgpu_f32x4*>(&st[8 * q + lr][4 * lq]) = g[q];
+            for (int q = 0; q < NI; q++) {
+                sgpu_f32x4 v;
+                if constexpr (!H) {
+                    v = g[q];
+                } else if (q < 4) {
+                    v = g[q];
+                } else {
+                    const u32x2 h = gh[q - 4];
+                    v = sgpu_f32x4{sgpu_h2f_lo(h[0]), sgpu_h2f_hi(h[0]), sgpu_h2f_lo(h[1]), sgpu_h2f_hi(h[1])};
+                }
+                *reinterpret_cast<sgpu_f32x4*>(&st[8 * q + lr][4 * lq]) = v;
+            }
             if (more) load(cn);                             // next chunk in flight during the MFMAs
             sgpu_f32x4 xa[4], wa[FN][4];
 #pragma unroll
