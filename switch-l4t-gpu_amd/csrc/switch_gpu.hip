@@ -568,17 +568,30 @@ __global__ void __launch_bounds__(256) membw_read4(const float4* __restrict__ bu
     const int i0 = threadIdx.x + blockIdx.x * blockDim.x;
     const int stride = gridDim.x * blockDim.x;
     float acc = 0.0f;
+    auto sum4 = [](const sgpu_f32x4& v) { return ((v.x + v.y) + v.z) + v.w; };
+    constexpr int G = 8;                          // loads per lane per group
     for (int it = 0; it < iters; ++it) {
         int i = i0;
-        for (; i + 3 * stride < n4; i += 4 * stride) {
-            const sgpu_f32x4 v0 = sgpu_ldnt(buf + i);
-            const sgpu_f32x4 v1 = sgpu_ldnt(buf + i + stride);
-            const sgpu_f32x4 v2 = sgpu_ldnt(buf + i + 2 * stride);
-            const sgpu_f32x4 v3 = sgpu_ldnt(buf + i + 3 * stride);
-            acc += ((v0.x + v0.y) + v0.z) + v0.w;
-            acc += ((v1.x + v1.y) + v1.z) + v1.w;
-            acc += ((v2.x + v2.y) + v2.z) + v2.w;
-            acc += ((v3.x + v3.y) + v3.z) + v3.w;
+        // Groups of G loads, software-pipelined: the next group is issued before the current
+        // one is added, so every lane keeps G loads in flight across the loop edge (the sums
+        // keep the element order of the plain loop).
+        if (i + (G - 1) * stride < n4) {
+            sgpu_f32x4 v[G];
+#pragma unroll
+            for (int u = 0; u < G; u++) v[u] = sgpu_ldnt(buf + i + u * stride);
+            for (; i + (2 * G - 1) * stride < n4; i += G * stride) {
+                sgpu_f32x4 w[G];
+#pragma unroll
+                for (int u = 0; u < G; u++) w[u] = sgpu_ldnt(buf + i + (G + u) * stride);
+#pragma unroll
+                for (int u = 0; u < G; u++) {
+                    acc += sum4(v[u]);
+                    v[u] = w[u];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < G; u++) acc += sum4(v[u]);
+            i += G * stride;
         }
         for (; i < n4; i += stride) {
             const sgpu_f32x4 v = sgpu_ldnt(buf + i);

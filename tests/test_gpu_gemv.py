@@ -218,15 +218,17 @@ def test_gemv_multi_integer_ragged(gpu):
     assert np.array_equal(dY.to_host(), (X @ W.T).astype(np.float32))
 
 
-def test_membw_read4_sums(gpu):
+@pytest.mark.parametrize("groups,extra", [(3, 17), (19, 5), (16, 0)])
+def test_membw_read4_sums(gpu, groups, extra):
     """Every thread's grid-stride sum, repeated `iters` times, lands in out[first index]
-    (switch_gpu.cu:41-54); integer-valued data makes the sums exact."""
+    (switch_gpu.cu:41-54); integer-valued data makes the sums exact.  Buffer sizes cover
+    the tail loop only, the pipelined groups of eight plus a tail, and whole groups."""
     import ctypes as ct
 
     threads = ct.c_int()
     gpu.call("sgpu_membw_read4", None, None, 0, 1, ct.byref(threads), None)
     nthr = threads.value
-    n4 = 3 * nthr + 17
+    n4 = groups * nthr + extra
     rng = np.random.default_rng(8)
     buf = rng.integers(-8, 9, (n4, 4)).astype(np.float32)
     dbuf = gpu.DeviceArray.from_host(buf)
