@@ -526,12 +526,14 @@ __device__ __forceinline__ void gemv_multi_xreg(const float* __restrict__ W, con
 // tile goes to ws with device-coherent stores (written through to memory, waited for) before
 // the unit counts in on cnt[tile]; the last split of a tile sums the S partials in split
 // order (deterministic), adds the bias, writes Y and resets the counter.  ws holds
-// S * ntiles * 1024 * FN floats, cnt one zeroed counter per tile.
+// S * ntiles * 1024 * FN floats, cnt one zeroed counter per tile.  accum != 0 adds the
+// result to Y instead of overwriting it (Y[t][n] = Y[t][n] + (sum + bias), the residual
+// add of the decoders, in the order the separate add kernel computes it).
 template <int FN, class WT = WF32, bool SPLIT = false>
 __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict__ W, const float* __restrict__ X,
                                              const float* __restrict__ bias, float* __restrict__ Y,
                                              int K, int N, int T, int S = 1, float* __restrict__ ws = nullptr,
-                                             unsigned* __restrict__ cnt = nullptr) {
+                                             unsigned* __restrict__ cnt = nullptr, int accum = 0) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     constexpr int NW = 4;                                   // waves per block (K split)
     constexpr int R = 32 * (1 + FN);                        // staged rows per wave: tokens, then W
@@ -705,7 +707,10 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
             for (int rr = 0; rr < RPW; rr++) {
                 const int r = RPW * wave + rr;
                 const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (t < T && n < N) Y[(size_t)t * N + n] = v[f][rr] + bv;
+                if (t < T && n < N) {
+                    float* y = Y + (size_t)t * N + n;
+                    *y = accum ? *y + (v[f][rr] + bv) : v[f][rr] + bv;
+                }
             }
         }
         __syncthreads();                          // staging is reused by the next tile

@@ -429,20 +429,19 @@ static int prefill_rows(sgpu_qwen *e, const int *ids, int T) {
         for (int l = 0; l < c->NL; l++) {
             TRY(sgpu_rmsnorm(e->d_pf_x, e->d_ln1w[l], e->d_pf_xn, C, eps, Tc, s));
             TRY(sgpu_internal_pf_gemm(e->d_qkvw[l], e->d_pf_xn, e->d_qkvb[l], e->d_pf_qkv, C, QKVD, Tc,
-                e->d_split_ws, e->d_split_cnt, s));
+                e->d_split_ws, e->d_split_cnt, 0, s));
             TRY(sgpu_internal_pf_qkv_post(e->d_pf_qkv, Tc, c0, e->d_cos, e->d_sin, e->d_kc[l], e->d_vc[l], NH, NKV,
                                           HD, s));
             TRY(sgpu_internal_pf_attn(e->d_pf_qkv, e->d_kc[l], e->d_vc[l], e->d_pf_att, Tc, c0, NH, NKV, HD, scale, s));
-            TRY(sgpu_internal_pf_gemm(e->d_ow[l], e->d_pf_att, NULL, e->d_pf_y, C, C, Tc,
-                e->d_split_ws, e->d_split_cnt, s));
-            TRY(sgpu_add2(e->d_pf_x, e->d_pf_y, e->d_pf_x, Tc * C, s));
+            /* x += o(att): the residual add in the GEMM's store (x + y, as add2 computes it) */
+            TRY(sgpu_internal_pf_gemm(e->d_ow[l], e->d_pf_att, NULL, e->d_pf_x, C, C, Tc,
+                e->d_split_ws, e->d_split_cnt, 1, s));
             TRY(sgpu_rmsnorm(e->d_pf_x, e->d_ln2w[l], e->d_pf_xn, C, eps, Tc, s));
             TRY(sgpu_internal_pf_gemm(e->d_gateupw[l], e->d_pf_xn, NULL, e->d_pf_y, C, 2 * FC, Tc,
-                e->d_split_ws, e->d_split_cnt, s));
+                e->d_split_ws, e->d_split_cnt, 0, s));
             TRY(sgpu_internal_pf_swiglu(e->d_pf_y, e->d_pf_g, FC, Tc, s));
-            TRY(sgpu_internal_pf_gemm(e->d_downw[l], e->d_pf_g, NULL, e->d_pf_y, FC, C, Tc,
-                e->d_split_ws, e->d_split_cnt, s));
-            TRY(sgpu_add2(e->d_pf_x, e->d_pf_y, e->d_pf_x, Tc * C, s));
+            TRY(sgpu_internal_pf_gemm(e->d_downw[l], e->d_pf_g, NULL, e->d_pf_x, FC, C, Tc,
+                e->d_split_ws, e->d_split_cnt, 1, s));
         }
     }
     TRY(sgpu_internal_dec_lmhead(e->d_emb, C, c->V, e->d_pf_x + (size_t)(Tc - 1) * C, e->d_lnfw, eps, e->d_logits, s));

@@ -1150,7 +1150,7 @@ int sgpu_internal_pf_embed(const uint16_t *emb, const int *ids, int T, float *x,
 }
 
 int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, float *Y, int K, int N, int T,
-                          float *ws, unsigned *cnt, void *stream) {
+                          float *ws, unsigned *cnt, int accum, void *stream) {
     if (!W || !X || !Y || K <= 0 || N <= 0 || T <= 0 || K % 4 || ((uintptr_t)W & 7) || ((uintptr_t)X & 15))
         return SGPU_ERR_INVALID_ARG;
     int rc;
@@ -1159,7 +1159,7 @@ int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, 
     const int S = (ws && cnt) ? nt_splits(T, N, K, d->cus) : 1;
     const long long units = (long long)cdiv(T, 32) * cdiv(N, 32) * S;
     unsigned g[3] = {(unsigned)(units < 0x7fffffffLL ? units : 0x7fffffffLL), 1, 1}, b[3] = {256, 1, 1};
-    void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T, (void *)&S, &ws, &cnt};
+    void *args[] = {(void *)&W, (void *)&X, (void *)&bias, (void *)&Y, &K, &N, &T, (void *)&S, &ws, &cnt, &accum};
     return launch(d->pf_gemm, g, b, stream, args);
 }
 

@@ -448,13 +448,13 @@ __global__ void sgpu_pf_embed(const uint16_t* __restrict__ emb, const int* __res
 // Y[t][n] = sum_k X[t][k] * h2f(W[n][k]) + bias?[n] on the fp32 matrix cores (one block per
 // 32-token x 32-row tile and k-split, grid-stride over units; blockDim 256, K % 4 == 0,
 // 16-byte X rows).  S > 1 splits each tile's K over S blocks (ws: S * tiles * 1024 floats,
-// cnt: one zeroed counter per tile, left at zero).
+// cnt: one zeroed counter per tile, left at zero).  accum != 0: Y += result (the residual).
 __global__ void __launch_bounds__(256) sgpu_pf_gemm(const uint16_t* __restrict__ W, const float* __restrict__ X,
                                                     const float* __restrict__ bias, float* __restrict__ Y, int K,
                                                     int N, int T, int S, float* __restrict__ ws,
-                                                    unsigned* __restrict__ cnt) {
+                                                    unsigned* __restrict__ cnt, int accum) {
     if (blockDim.x != 256) return;
-    sgpu::gemm_nt_mfma<1, WF16, true>(W, X, bias, Y, K, N, T, S, ws, cnt);
+    sgpu::gemm_nt_mfma<1, WF16, true>(W, X, bias, Y, K, N, T, S, ws, cnt, accum);
 }
 
 // Per prompt row t (position pos0 + t) of the qkv matrix (rows of QKVD = (NH + 2*NKV)*HD):

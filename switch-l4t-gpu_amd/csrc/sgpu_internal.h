@@ -38,8 +38,9 @@ SGPU_HIDDEN int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, i
  * of k into the key cache with v into the value cache, causal attention of T prompt rows
  * (positions pos0..pos0+T-1, pos0 + T <= 8192), and row SwiGLU over gate|up rows of 2*FC. */
 SGPU_HIDDEN int sgpu_internal_pf_embed(const uint16_t *emb, const int *ids, int T, float *x, int C, void *stream);
+/* accum != 0: Y += X W^T (+ bias), the residual add fused into the GEMM. */
 SGPU_HIDDEN int sgpu_internal_pf_gemm(const uint16_t *W, const float *X, const float *bias, float *Y, int K, int N,
-                                      int T, float *ws, unsigned *cnt, void *stream);
+                                      int T, float *ws, unsigned *cnt, int accum, void *stream);
 /* gemv_multi with an explicit split-K workspace (NULL: never split). */
 SGPU_HIDDEN int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N,
                                          int T, float *ws, unsigned *cnt, void *stream);
