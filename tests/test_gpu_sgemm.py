@@ -102,7 +102,10 @@ def test_integer_exact(gpu, fn, M, N, K):
 # (M, N whole tiles, K whole slices, at least two slices) and its bounds-checked path.
 DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 4096, 16),
                    (2048, 4096, 64), (2048, 4096, 96), (256, 256, 64), (192, 320, 40),
-                   (4096, 4096, 96), (4096, 4352, 64), (4352, 4096, 160)]
+                   (4096, 4096, 96), (4096, 4352, 64), (4352, 4096, 160),
+                   # sgpu_sgemm_opt's split-K regimes: one row or column of tiles, and the
+                   # largest K-tailed problem the 4-way split takes (484 tiles, 31 MB of partials)
+                   (1, 4096, 4096), (4096, 1, 2048), (1408, 1408, 997)]
 
 
 @pytest.mark.parametrize("M,N,K", DISPATCH_SHAPES)
