@@ -163,8 +163,11 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 // One query head over cached positions p0..p1-1 (p1 - p0 <= the length of sc): scores in
 // sc, block max m and sum of exp(s - m) returned in every thread, and the exp-weighted sum of
 // V returned in the lanes tid < HD (dim tid).  Scores: LPT lanes per position (DPL dims each),
-// 256/LPT positions per pass; mix: 256/HD t-slices of HD lanes, eight independent loads in
-// flight per lane.
+// 256/LPT positions per pass, KU passes' K loads issued before any of their dot products.
+// Mix: HD/4 lanes per cached row (a float4 of V each), 1024/HD rows per pass, VU passes' V
+// loads issued before any of their FMAs; each lane sums its rows in position order, then the
+// 1024/HD row slices are summed in slice order through part (1024 floats).  The round trips
+// to the cache are per round of KU or VU passes, not per position.
 template <int HD>
 __device__ __forceinline__ float attn_chunk(const float* __restrict__ qh, const float* __restrict__ kg,
                                             const float* __restrict__ vg, int KVD, int p0, int p1, float scale,
@@ -172,7 +175,9 @@ __device__ __forceinline__ float attn_chunk(const float* __restrict__ qh, const 
     constexpr int LPT = HD >= 64 ? HD / 16 : 4;   // lanes per position
     constexpr int DPL = HD / LPT;                  // dims per lane (16 or 8)
     constexpr int PPP = 256 / LPT;                 // positions per pass
-    constexpr int SLICES = 256 / HD;
+    constexpr int KU = 4;                          // score passes per round
+    constexpr int VL = HD / 4, VR = 256 / VL;      // mix: lanes per row, rows per pass
+    constexpr int VU = HD >= 128 ? 8 : 16;         // mix passes per round
     const int tid = threadIdx.x;
     const int d0 = (tid % LPT) * DPL;
     float qv[DPL];
@@ -182,20 +187,27 @@ __device__ __forceinline__ float attn_chunk(const float* __restrict__ qh, const 
 #pragma unroll
         for (int i = 0; i < 4; i++) qv[e + i] = a[i];
     }
-    for (int tb = p0; tb < p1; tb += PPP) {
-        const int t = tb + tid / LPT;
-        float s = 0.0f;
-        if (t < p1) {
+    const sgpu_f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tb = p0; tb < p1; tb += PPP * KU) {
+        sgpu_f32x4 kv[KU][DPL / 4];
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = tb + u * PPP + tid / LPT;
             const float* kr = kg + (size_t)t * KVD + d0;
 #pragma unroll
-            for (int e = 0; e < DPL; e += 4) {
-                const sgpu_f32x4 k4 = *reinterpret_cast<const sgpu_f32x4*>(kr + e);
-#pragma unroll
-                for (int i = 0; i < 4; i++) s = __builtin_fmaf(qv[e + i], k4[i], s);
-            }
+            for (int e = 0; e < DPL / 4; e++) kv[u][e] = t < p1 ? *reinterpret_cast<const sgpu_f32x4*>(kr + 4 * e) : z4;
         }
-        s = sgpu_group_sum<LPT>(s);
-        if (tid % LPT == LPT - 1 && t < p1) sc[t - p0] = s * scale;
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int t = tb + u * PPP + tid / LPT;
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < DPL / 4; e++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) s = __builtin_fmaf(qv[4 * e + i], kv[u][e][i], s);
+            s = sgpu_group_sum<LPT>(s);
+            if (tid % LPT == LPT - 1 && t < p1) sc[t - p0] = s * scale;
+        }
     }
     __syncthreads();
     const int n = p1 - p0;
@@ -209,16 +221,28 @@ __device__ __forceinline__ float attn_chunk(const float* __restrict__ qh, const 
         sum += e;
     }
     sum = block_sum256(sum, red);          // its barriers also publish sc[]
-    const int slice = tid / HD, d = tid % HD;
-    float acc = 0.0f;
-#pragma unroll 8
-    for (int t = slice; t < n; t += SLICES) acc = __builtin_fmaf(sc[t], vg[(size_t)(p0 + t) * KVD + d], acc);
-    part[tid] = acc;
+    const int vs = tid / VL, vq = tid % VL;
+    sgpu_f32x4 acc = z4;
+    for (int t0 = 0; t0 < n; t0 += VR * VU) {
+        sgpu_f32x4 vv[VU];
+        float w[VU];
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int t = t0 + u * VR + vs;
+            vv[u] = t < n ? *reinterpret_cast<const sgpu_f32x4*>(vg + (size_t)(p0 + t) * KVD + 4 * vq) : z4;
+            w[u] = t < n ? sc[t] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < VU; u++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = __builtin_fmaf(w[u], vv[u][e], acc[e]);
+    }
+    *reinterpret_cast<sgpu_f32x4*>(&part[vs * HD + 4 * vq]) = acc;
     __syncthreads();
     float tot = 0.0f;
-    if (slice == 0) {
+    if (tid < HD) {
 #pragma unroll
-        for (int s2 = 0; s2 < SLICES; s2++) tot += part[s2 * HD + d];
+        for (int s2 = 0; s2 < VR; s2++) tot += part[s2 * HD + tid];
     }
     m_out = m;
     sum_out = sum;
@@ -241,7 +265,7 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
     constexpr int WSTRIDE = HD + 2;                // ws record: o[HD], m, l
     __shared__ float sc[kAttnMaxLen];
     __shared__ float red[4];
-    __shared__ float part[256];
+    __shared__ __attribute__((aligned(16))) float part[1024];
     __shared__ int last_s;
     // Block b -> XCD b % 8 (blocks are dealt round-robin to the 8 XCDs).  The G query heads
     // that share KV group g and chunk c get the same b % 8, so the chunk's K and V come from
@@ -333,7 +357,7 @@ __device__ __forceinline__ void pf_attn(const float* __restrict__ qkv, const flo
                                         int NKV, float scale, int QKVD) {
     __shared__ float sc[kMaxCtx];
     __shared__ float red[4];
-    __shared__ float part[256];
+    __shared__ __attribute__((aligned(16))) float part[1024];
     const int h = blockIdx.x, t = blockIdx.y, KVD = NKV * HD, g = h / (NH / NKV);
     const int n = min(pos0 + t + 1, kMaxCtx);
     float m, sum;
