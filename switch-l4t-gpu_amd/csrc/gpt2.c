@@ -218,15 +218,19 @@ static int fused_lm_head(sgpu_gpt2 *e) {
                                    e->logits, (void *)e->stream);
 }
 
-/* One greedy step on the device: token from step[0], pos = step[1] + 1. */
-static int device_step(sgpu_gpt2 *e) {
+/* Greedy argmax of the logits into step[0] and the token list, then the next position's
+ * input: x = wte[token] + wpe[step[1] + 1], step[1] + 1. */
+static int argmax_next(sgpu_gpt2 *e) {
     const float *W = e->w;
-    int rc = sgpu_internal_g2_embed_next(W + e->L.wte, W + e->L.wpe, e->x, e->cfg.C, e->d_step, (void *)e->stream);
-    if (!rc) rc = fused_layers(e);
+    return sgpu_internal_dec_argmax_next(e->logits, e->cfg.V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens, NULL,
+                                         W + e->L.wte, W + e->L.wpe, e->x, e->cfg.C, e->cfg.CTX, (void *)e->stream);
+}
+
+/* One greedy step on the device, x and step already set for its position. */
+static int device_step(sgpu_gpt2 *e) {
+    int rc = fused_layers(e);
     if (!rc) rc = fused_lm_head(e);
-    if (!rc)
-        rc = sgpu_internal_dec_argmax(e->logits, e->cfg.V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
-                                      (void *)e->stream);
+    if (!rc) rc = argmax_next(e);
     return rc;
 }
 
@@ -412,9 +416,7 @@ int sgpu_gpt2_generate(sgpu_gpt2 *e, const int *prompt, int T, int n_gen, int *o
     const int st[2] = {prompt[T - 1], T - 1};
     hipError_t hs = hipMemcpyAsync(e->d_step, st, sizeof st, hipMemcpyHostToDevice, e->stream);
     if (hs != hipSuccess) return (int)hs;
-    if ((rc = sgpu_internal_dec_argmax(e->logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
-                                       (void *)e->stream)))
-        return rc;
+    if ((rc = argmax_next(e))) return rc;
     for (int g = 0; g < n_gen; g++) {
         if (e->path == SGPU_GPT2_PATH_GRAPH) {
             if (!e->ge_step && (rc = capture(e, device_step, &e->g_step, &e->ge_step))) return rc;

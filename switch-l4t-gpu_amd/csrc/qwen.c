@@ -317,14 +317,18 @@ static int lm_head(sgpu_qwen *e) {
                                     (void *)e->stream);
 }
 
-/* One greedy step entirely on the device: next token from step[0], pos = step[1] + 1. */
+/* Greedy argmax of the logits into step[0] and the token list, then the next position's
+ * input: x = embedding of that token, step[1] + 1. */
+static int argmax_next(sgpu_qwen *e) {
+    return sgpu_internal_dec_argmax_next(e->d_logits, e->cfg.V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
+                                         e->d_emb, NULL, NULL, e->d_x, e->cfg.C, e->cfg.CTX, (void *)e->stream);
+}
+
+/* One greedy step entirely on the device, x and step already set for its position. */
 static int device_step(sgpu_qwen *e) {
-    int rc = sgpu_internal_dec_embed_next(e->d_emb, e->d_x, e->cfg.C, e->d_step, (void *)e->stream);
-    if (!rc) rc = fused_layers(e);
+    int rc = fused_layers(e);
     if (!rc) rc = lm_head(e);
-    if (!rc)
-        rc = sgpu_internal_dec_argmax(e->d_logits, e->cfg.V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
-                                      (void *)e->stream);
+    if (!rc) rc = argmax_next(e);
     return rc;
 }
 
@@ -484,9 +488,7 @@ int sgpu_qwen_generate(sgpu_qwen *e, const int *prompt, int T, int n_gen, int *o
         return rc;
     }
     if ((rc = prefill_rows(e, prompt, T))) return rc;
-    if ((rc = sgpu_internal_dec_argmax(e->d_logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, e->d_tokens,
-                                       (void *)e->stream)))
-        return rc;
+    if ((rc = argmax_next(e))) return rc;
     for (int g = 0; g < n_gen; g++) {
         if (e->path == SGPU_QWEN_PATH_GRAPH) {
             if (!e->ge_step && (rc = capture(e, device_step, &e->g_step, &e->ge_step))) return rc;

@@ -95,8 +95,8 @@ typedef struct {
     hipFunction_t fn[NKERN];
     hipFunction_t gemv_f32[NLPR][NSEG], gemv_h[NLPR][NSEG];
     hipFunction_t dec[NDECFAM][NDEC_ALL];
-    hipFunction_t dec_attn[3], dec_embed, dec_embed_next, dec_argmax_part, dec_argmax_final;
-    hipFunction_t dec_g2embed, dec_g2embed_next;
+    hipFunction_t dec_attn[3], dec_embed, dec_argmax_part, dec_argmax_embed;
+    hipFunction_t dec_g2embed, dec_argmax_g2embed;
     hipFunction_t pf_embed, pf_gemm, pf_qkv_post, pf_attn[3], pf_swiglu;
     float *sk_ws;          /* split-K partial tiles, SK_WS_FLOATS */
     unsigned *sk_cnt;      /* split-K arrival counters, SK_MAX_TILES, zero between launches */
@@ -178,11 +178,10 @@ static int load_device(int dev) {
                 goto out;
             }
         if (hipModuleGetFunction(&d->dec_embed, d->mod[MOD_DECODE], "sgpu_dec_embed") != hipSuccess ||
-            hipModuleGetFunction(&d->dec_embed_next, d->mod[MOD_DECODE], "sgpu_dec_embed_next") != hipSuccess ||
             hipModuleGetFunction(&d->dec_argmax_part, d->mod[MOD_DECODE], "sgpu_dec_argmax_part") != hipSuccess ||
-            hipModuleGetFunction(&d->dec_argmax_final, d->mod[MOD_DECODE], "sgpu_dec_argmax_final") != hipSuccess ||
-            hipModuleGetFunction(&d->dec_g2embed, d->mod[MOD_DECODE], "sgpu_dec_g2embed") != hipSuccess ||
-            hipModuleGetFunction(&d->dec_g2embed_next, d->mod[MOD_DECODE], "sgpu_dec_g2embed_next") != hipSuccess) {
+            hipModuleGetFunction(&d->dec_argmax_embed, d->mod[MOD_DECODE], "sgpu_dec_argmax_embed") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_argmax_g2embed, d->mod[MOD_DECODE], "sgpu_dec_argmax_g2embed") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_g2embed, d->mod[MOD_DECODE], "sgpu_dec_g2embed") != hipSuccess) {
             rc = SGPU_ERR_NO_KERNEL;
             goto out;
         }
@@ -1114,28 +1113,25 @@ int sgpu_internal_dec_embed(const uint16_t *emb, int token, int pos, float *x, i
     return launch(d->dec_embed, g, b, stream, args);
 }
 
-int sgpu_internal_dec_embed_next(const uint16_t *emb, float *x, int C, int *step, void *stream) {
+int sgpu_internal_dec_argmax_next(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
+                                  const uint16_t *emb, const float *wte, const float *wpe, float *x, int C, int ctx,
+                                  void *stream) {
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
-    unsigned g[3] = {1, 1, 1}, b[3] = {256, 1, 1};
-    void *args[] = {(void *)&emb, (void *)&x, &C, (void *)&step};
-    return launch(d->dec_embed_next, g, b, stream, args);
-}
-
-int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
-                             void *stream) {
-    int rc;
-    devstate *d = cur(&rc);
-    if (!d) return rc;
-    if (n <= 0) return SGPU_ERR_INVALID_ARG;
+    if (n <= 0 || C <= 0 || !x || (!emb && (!wte || !wpe))) return SGPU_ERR_INVALID_ARG;
     int np = SGPU_ARGMAX_PARTS;
     unsigned g[3] = {(unsigned)np, 1, 1}, b[3] = {256, 1, 1};
     void *a1[] = {(void *)&v, &n, (void *)&part_v, (void *)&part_i};
     if ((rc = launch(d->dec_argmax_part, g, b, stream, a1))) return rc;
     unsigned g2[3] = {1, 1, 1};
-    void *a2[] = {(void *)&part_v, (void *)&part_i, &np, (void *)&step, (void *)&out};
-    return launch(d->dec_argmax_final, g2, b, stream, a2);
+    if (emb) {
+        void *a2[] = {(void *)&part_v, (void *)&part_i, &np, (void *)&step, (void *)&out, (void *)&emb, (void *)&x, &C};
+        return launch(d->dec_argmax_embed, g2, b, stream, a2);
+    }
+    void *a2[] = {(void *)&part_v, (void *)&part_i, &np,          (void *)&step, (void *)&out,
+                  (void *)&wte,    (void *)&wpe,    (void *)&x, &C, &ctx};
+    return launch(d->dec_argmax_g2embed, g2, b, stream, a2);
 }
 
 /* ---- batched prompt prefill (sgpu_decode.hip sgpu_pf_*) ---- */
@@ -1252,11 +1248,3 @@ int sgpu_internal_g2_embed(const float *wte, const float *wpe, int token, int po
     return launch(d->dec_g2embed, g, b, stream, args);
 }
 
-int sgpu_internal_g2_embed_next(const float *wte, const float *wpe, float *x, int C, int *step, void *stream) {
-    int rc;
-    devstate *d = cur(&rc);
-    if (!d) return rc;
-    unsigned g[3] = {1, 1, 1}, b[3] = {256, 1, 1};
-    void *args[] = {(void *)&wte, (void *)&wpe, (void *)&x, &C, (void *)&step};
-    return launch(d->dec_g2embed_next, g, b, stream, args);
-}

@@ -11,7 +11,8 @@
 //   sgpu_dec_gateup_* RMSNorm(x) -> gate and up rows of the same output -> SwiGLU
 //   sgpu_dec_lmhead_* final RMSNorm -> tied lm_head GEMV
 //   sgpu_dec_embed    token embedding (h2f) and the step record {token, pos} for the layers
-//   sgpu_dec_argmax_* first-max argmax of the logits into the step record (greedy decode)
+//   sgpu_dec_argmax_* first-max argmax of the logits into the step record (greedy decode),
+//                     the second stage also writing the next token's embedding
 //   sgpu_dec_g2*      the GPT-2 (fp32) counterparts: LayerNorm+qkv+bias+KV write, GEMV+bias+
 //                     residual, LayerNorm+fc+bias+GELU, LayerNorm+lm_head, wte+wpe embedding
 // The position lives in device memory (`step`), so a whole position can be captured once as
@@ -384,18 +385,6 @@ __global__ void sgpu_dec_embed(const uint16_t* __restrict__ emb, int token, int 
         x[i] = sgpu_h2f(emb[(size_t)token * C + i]);
 }
 
-// Same, with the token taken from step[0] (written by sgpu_dec_argmax) and pos = step[1] + 1.
-// One block: the step record is read before the barrier and rewritten after it.
-__global__ void __launch_bounds__(256) sgpu_dec_embed_next(const uint16_t* __restrict__ emb, float* __restrict__ x,
-                                                           int C, int* __restrict__ step) {
-    __shared__ int tok;
-    if (threadIdx.x == 0) tok = step[0];
-    __syncthreads();
-    for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = sgpu_h2f(emb[(size_t)tok * C + i]);
-    __syncthreads();
-    if (threadIdx.x == 0) step[1] = step[1] + 1;
-}
-
 // GPT-2: x = wte[token] + wpe[pos] (fp32; the reference adds on the host,
 // gpt2_engine.c:176-179); step = {token, pos}.
 __global__ void sgpu_dec_g2embed(const float* __restrict__ wte, const float* __restrict__ wpe, int token, int pos,
@@ -407,21 +396,6 @@ __global__ void sgpu_dec_g2embed(const float* __restrict__ wte, const float* __r
     }
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < C; i += gridDim.x * blockDim.x)
         x[i] = wte[(size_t)token * C + i] + wpe[(size_t)pos * C + i];
-}
-
-// Same, with the token from step[0] and pos = step[1] + 1 (one block).
-__global__ void __launch_bounds__(256) sgpu_dec_g2embed_next(const float* __restrict__ wte, const float* __restrict__ wpe,
-                                                             float* __restrict__ x, int C, int* __restrict__ step) {
-#pragma clang fp contract(off)
-    __shared__ int tok, pos;
-    if (threadIdx.x == 0) {
-        tok = step[0];
-        pos = step[1] + 1;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = wte[(size_t)tok * C + i] + wpe[(size_t)pos * C + i];
-    __syncthreads();
-    if (threadIdx.x == 0) step[1] = pos;
 }
 
 // First-max argmax over n logits (qwen_engine.c:360-364 tie rule), stage 1: each of the
@@ -440,21 +414,50 @@ __global__ void __launch_bounds__(256) sgpu_dec_argmax_part(const float* __restr
     if (threadIdx.x == 0) { pv[blockIdx.x] = best; pi[blockIdx.x] = idx; }
 }
 
-// Stage 2 (one block of 256 threads over np <= 256 partials): the index goes to step[0] and,
-// if out != NULL, to out[step[1] + 1].
-__global__ void __launch_bounds__(256) sgpu_dec_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi,
-                                                             int np, int* __restrict__ step, int* __restrict__ out) {
+// Stage 2, one block of 256 threads over np <= 256 partials, fused with the next step's
+// embedding: the index goes to step[0] and, if out != NULL, to out[step[1] + 1]; then the
+// position advances (step[1] + 1) and x becomes the new token's embedding -- h2f(emb[token])
+// (Qwen) or wte[token] + wpe[position] (GPT-2, skipped once the position reaches ctx).
+__device__ __forceinline__ int amax_final(const float* __restrict__ pv, const int* __restrict__ pi, int np) {
     __shared__ float sv[4];
     __shared__ int si[4];
     float best = -INFINITY;
     int idx = 0x7fffffff;
     if ((int)threadIdx.x < np) { best = pv[threadIdx.x]; idx = pi[threadIdx.x]; }
     amax_block256(best, idx, sv, si);
+    return idx == 0x7fffffff ? 0 : idx;
+}
+__global__ void __launch_bounds__(256) sgpu_dec_argmax_embed(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                             int np, int* __restrict__ step, int* __restrict__ out,
+                                                             const uint16_t* __restrict__ emb, float* __restrict__ x,
+                                                             int C) {
+    __shared__ int pos;
+    const int idx = amax_final(pv, pi, np);
     if (threadIdx.x == 0) {
-        if (idx == 0x7fffffff) idx = 0;
+        pos = step[1];
         step[0] = idx;
-        if (out) out[step[1] + 1] = idx;
+        if (out) out[pos + 1] = idx;
+        step[1] = pos + 1;
     }
+    for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = sgpu_h2f(emb[(size_t)idx * C + i]);
+}
+__global__ void __launch_bounds__(256) sgpu_dec_argmax_g2embed(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                               int np, int* __restrict__ step, int* __restrict__ out,
+                                                               const float* __restrict__ wte,
+                                                               const float* __restrict__ wpe, float* __restrict__ x,
+                                                               int C, int ctx) {
+#pragma clang fp contract(off)
+    __shared__ int pos;
+    const int idx = amax_final(pv, pi, np);
+    if (threadIdx.x == 0) {
+        pos = step[1] + 1;
+        step[0] = idx;
+        if (out) out[pos] = idx;
+        step[1] = pos;
+    }
+    __syncthreads();
+    if (pos < ctx)
+        for (int i = threadIdx.x; i < C; i += blockDim.x) x[i] = wte[(size_t)idx * C + i] + wpe[(size_t)pos * C + i];
 }
 
 // ---- batched prompt prefill (T rows at positions pos0..pos0+T-1) ----

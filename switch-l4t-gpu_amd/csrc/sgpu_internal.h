@@ -28,11 +28,14 @@ SGPU_HIDDEN int sgpu_internal_dec_attn(const float *q, const float *kc, const fl
                                        unsigned *cnt, void *stream);
 SGPU_HIDDEN int sgpu_internal_dec_embed(const uint16_t *emb, int token, int pos, float *x, int C, int *step,
                                         void *stream);
-SGPU_HIDDEN int sgpu_internal_dec_embed_next(const uint16_t *emb, float *x, int C, int *step, void *stream);
-/* Two-stage argmax: SGPU_ARGMAX_PARTS partial (value, index) pairs in part_v / part_i. */
+/* Greedy step tail: two-stage argmax of v (SGPU_ARGMAX_PARTS partial (value, index) pairs in
+ * part_v / part_i); the second stage writes the token to step[0] (and out[step[1] + 1] if out
+ * != NULL), advances step[1] and writes the next position's input x: h2f(emb[token]) when emb
+ * != NULL, else wte[token] + wpe[step[1]] while step[1] < ctx. */
 #define SGPU_ARGMAX_PARTS 256
-SGPU_HIDDEN int sgpu_internal_dec_argmax(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
-                                         void *stream);
+SGPU_HIDDEN int sgpu_internal_dec_argmax_next(const float *v, int n, float *part_v, int *part_i, int *step, int *out,
+                                              const uint16_t *emb, const float *wte, const float *wpe, float *x,
+                                              int C, int ctx, void *stream);
 /* Batched prompt prefill of the Qwen engine (qwen.c sgpu_qwen_prefill): row embedding, the
  * fp16-weight matrix-core GEMM Y[T][N] = X[T][K] W[N][K]^T + bias, RoPE of q in place and
  * of k into the key cache with v into the value cache, causal attention of T prompt rows
@@ -66,6 +69,4 @@ SGPU_HIDDEN int sgpu_internal_g2_lmhead(const float *W, int K, int N, const floa
                                         const float *lnb, float eps, float *y, void *stream);
 SGPU_HIDDEN int sgpu_internal_g2_embed(const float *wte, const float *wpe, int token, int pos, float *x, int C,
                                        int *step, void *stream);
-SGPU_HIDDEN int sgpu_internal_g2_embed_next(const float *wte, const float *wpe, float *x, int C, int *step,
-                                            void *stream);
 #endif
