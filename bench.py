@@ -364,9 +364,15 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true", help="one launch per measured kernel, for rocprofv3 --pmc")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (for profiling it)")
     ap.add_argument("--decode-path", choices=["reference", "fused", "graph"], default="graph")
+    ap.add_argument("--decode-model", choices=["qwen", "gpt2"], default="qwen",
+                    help="model of the --decode-only leg (gpt2: the graph path)")
     args = ap.parse_args()
     if args.decode_only:
         sgpu.init(0)
+        if args.decode_model == "gpt2":
+            dec = bench_gpt2_decode()
+            print(json.dumps({"gpt2_decode_tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4)}))
+            return
         path = {"reference": 0, "fused": 1, "graph": 2}[args.decode_path]
         dec = bench_decode(path=path, compare=False)
         print(json.dumps({"decode_tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4)}))
