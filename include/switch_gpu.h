@@ -119,8 +119,10 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * 128x128; one output per thread).  sgpu_sgemm_opt is the tuned entry: it launches the
  * member (sgemm_opt256 256x256, sgemm_opt 128x256, sgemm_tiled4 128x128 or sgemm_tiled
  * 64x64 tiles) whose busiest CU has the least work: ceil(tiles / CUs) tiles times the
- * tile's area over the member's sustained rate; problems with fewer 64x64 tiles than half
- * the CUs, and small ones whose K is not a multiple of 32, go to sgemm_splitk instead. */
+ * tile's area over the member's sustained rate.  Problems whose 16x16 tiles fit the CUs in
+ * one round (K <= 4096) go to sgemm_small16, else those whose 32x32 tiles do (K <= 1024) to
+ * sgemm_small32; of the rest, problems with fewer 64x64 tiles than half the CUs, and small
+ * ones whose K is not a multiple of 32, go to sgemm_splitk. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
@@ -136,6 +138,11 @@ int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, in
  * of workspace (SGPU_ERR_INVALID_ARG).  Launches on one device that overlap in time share
  * the workspace and must not run concurrently.  No counterpart in the reference. */
 int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream);
+/* The small-problem members sgemm_small16 / sgemm_small32 (tile = 16 or 32): one tile x tile
+ * block of C per workgroup, A and B read straight into the matrix cores (no LDS staging), the
+ * workgroup's four waves splitting K and summing their partials in a fixed order.  Any shape
+ * with A and B under 2 GB (SGPU_ERR_INVALID_ARG otherwise).  No counterpart in the reference. */
+int sgpu_sgemm_small(const float *A, const float *B, float *C, int M, int N, int K, int tile, void *stream);
 int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 
 /* Read-bandwidth probe, membw_read4 (switch_gpu.cu:41-54; launched gpu_workload.c:210-213):

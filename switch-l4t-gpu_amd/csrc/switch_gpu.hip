@@ -499,6 +499,115 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
     }
 }
 
+// Small problems: one TSxTS tile of C per block of 256 threads (grid-stride over tiles), the
+// operands read straight from global memory into MFMA registers (at these sizes A and B stay
+// in L2, and there is no slice pipeline to fill), no LDS staging.  The four waves take
+// interleaved k-groups (group g to wave g % 4) and sum their partial tiles through LDS in
+// wave order.  Any M, N >= 1, K >= 0 with A and B under 2^31 bytes each; VEC (K % 4 == 0,
+// A 16-byte aligned) reads A with 16-byte loads.
+//   TS 32: v_mfma_f32_32x32x2f32, k-groups 8 deep: in group kb, lane half h = lane / 32
+//          holds A[m][kb + 4h + t] and B[kb + 4h + t][n] for MFMA step t = 0..3.
+//   TS 16: v_mfma_f32_16x16x4f32, k-groups 16 deep: lane quarter q = lane / 16 holds
+//          A[m][kb + 4q + t] and B[kb + 4q + t][n] for step t.
+// Reads go through buffer resources sized to A and B: B past row K-1 and A past row M-1
+// read as zero; A elements past K (the next row's) are zeroed explicitly; columns past N read
+// the next row's elements and are not stored, nor are rows past M.
+template <int TS, int U, bool VEC>
+__device__ __forceinline__ void sgemm_small_tiles(const float* __restrict__ A, const float* __restrict__ B,
+                                                  float* __restrict__ C, int M, int N, int K,
+                                                  float (&red)[4][TS * TS / 64][64]) {
+    static_assert(TS == 16 || TS == 32, "tile size");
+    constexpr int R = TS * TS / 64;               // accumulator registers per lane
+    constexpr int KG = 4 * (64 / TS);             // k per group
+    typedef float accv __attribute__((ext_vector_type(R)));
+    const int tid = sgpu_tid(), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane % TS, hq = lane / TS;
+    const int ntn = (N + TS - 1) / TS, ntiles = ((M + TS - 1) / TS) * ntn;
+    const int ng = (K + KG - 1) / KG;                        // k-groups
+    const int nper = ng > wave ? (ng - wave + 3) / 4 : 0;    // this wave's groups
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * K * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, K * N * 4, 0x00020000);
+    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {   // block-uniform loop
+        const int m0 = (tile / ntn) * TS, n0 = (tile % ntn) * TS;
+        // byte offsets of this lane's k = 4*hq in its A row and its B column
+        const int aoff = ((m0 + li) * K + 4 * hq) * 4, boff = (4 * hq * N + n0 + li) * 4;
+        sgpu_f32x4 a[2][U], b[2][U];
+        // per-lane byte offsets (voffset) fixed for the tile; the k-group part is wave-uniform
+        // and goes in the scalar offset, so no per-group address registers stay live
+        auto load = [&](int i0, auto set_c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int kb = (wave + 4 * (i0 + u)) * KG;          // wave-uniform
+                if constexpr (VEC) {
+                    a[SET][u] = __builtin_bit_cast(sgpu_f32x4,
+                                                   __builtin_amdgcn_raw_buffer_load_b128(rsa, aoff, kb * 4, 0));
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        a[SET][u][t] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rsa, aoff, (kb + t) * 4, 0));
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    if (kb + 4 * hq + t >= K) a[SET][u][t] = 0.0f;
+                    b[SET][u][t] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rsb, boff, (kb + t) * N * 4, 0));
+                }
+            }
+        };
+        accv acc0 = {}, acc1 = {};                 // two chains: even and odd steps
+        auto mfma = [&](auto set_c) __attribute__((always_inline)) {
+            constexpr int SET = decltype(set_c)::value;
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int t = 0; t < 4; t += 2) {
+                    if constexpr (TS == 32) {
+                        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[SET][u][t], b[SET][u][t], acc0, 0, 0, 0);
+                        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[SET][u][t + 1], b[SET][u][t + 1], acc1, 0, 0, 0);
+                    } else {
+                        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[SET][u][t], b[SET][u][t], acc0, 0, 0, 0);
+                        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[SET][u][t + 1], b[SET][u][t + 1], acc1, 0, 0, 0);
+                    }
+                }
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        // batches of U groups, the next batch's loads issued before this batch's MFMAs
+        if (nper > 0) load(0, S0{});
+        for (int i = 0; i < nper; i += 2 * U) {
+            if (i + U < nper) load(i + U, S1{});
+            mfma(S0{});
+            if (i + U >= nper) break;
+            if (i + 2 * U < nper) load(i + 2 * U, S0{});
+            mfma(S1{});
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) red[wave][r][lane] = acc0[r] + acc1[r];
+        __syncthreads();
+        // D layout: TS 32, lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32;
+        // TS 16 -> row 4*(l/16) + r, column l%16
+#pragma unroll
+        for (int e = tid; e < R * 64; e += 256) {
+            const int r = e / 64, l = e % 64;
+            const int row = TS == 32 ? 8 * (r / 4) + 4 * (l / 32) + r % 4 : 4 * (l / 16) + r;
+            const int gm = m0 + row, gn = n0 + l % TS;
+            const float v = ((red[0][r][l] + red[1][r][l]) + red[2][r][l]) + red[3][r][l];
+            if (gm < M && gn < N) C[(size_t)gm * N + gn] = v;
+        }
+        __syncthreads();
+    }
+}
+template <int TS, int U>
+__device__ __forceinline__ void sgemm_small(const float* __restrict__ A, const float* __restrict__ B,
+                                            float* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) float red[4][TS * TS / 64][64];
+    if (sgpu_nthreads() != 256) return;
+    if (K % 4 == 0 && ((uintptr_t)A & 15) == 0) sgemm_small_tiles<TS, U, true>(A, B, C, M, N, K, red);
+    else sgemm_small_tiles<TS, U, false>(A, B, C, M, N, K, red);
+}
+
 }  // namespace
 
 extern "C" {
@@ -544,6 +653,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 sgemm_splitk(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
              int S, float* __restrict__ ws, unsigned* __restrict__ cnt) {
     sgemm_mfma<64, 64, 32, 2, 2, 1, 4, true>(A, B, C, M, N, K, S, ws, cnt);
+}
+
+// sgemm_small16 / sgemm_small32: problems too small to fill the chip with 64x64 tiles (one
+// 16x16 or 32x32 tile of C per block, operands straight from memory into the matrix cores,
+// the block's four waves splitting K).
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+sgemm_small16(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    sgemm_small<16, 4>(A, B, C, M, N, K);
+}
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+sgemm_small32(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    sgemm_small<32, 4>(A, B, C, M, N, K);
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:

@@ -73,6 +73,7 @@ _SIGS = {
     "sgpu_sgemm_opt": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_opt256": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_splitk": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "sgpu_sgemm_small": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_sgemm_naive": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_membw_read4": (_I, [_P, _P, _I, _I, ct.POINTER(_I), _P]),
     "sgpu_stream_create": (_I, [_P]),

@@ -12,7 +12,8 @@ import pytest
 # gpt2_engine.c:119-128, qwen_engine.c:148-155); a missing one is fatal to those hosts.
 REFERENCE_KERNELS = {
     "switch_gpu": {"sgemm_tiled", "sgemm_tiled4", "sgemm_opt", "sgemm_naive", "membw_read4",
-                   "sgemm_opt256", "sgemm_splitk"},   # the last two are added members (no reference counterpart)
+                   "sgemm_opt256", "sgemm_splitk", "sgemm_small16",
+                   "sgemm_small32"},   # the last four are added members (no reference counterpart)
     "gemv": {"gemv", "gemv4", "gemv_warp"},
     "gpt2_kernels": {"gemv_warp", "gemv_warp_b", "gemv_multi", "layernorm", "gelu", "add_bias", "add2",
                      "attn_scores", "attn_softmax", "attn_mix"},
@@ -114,6 +115,10 @@ def test_argument_errors_before_device(sg):
     assert L.sgpu_sgemm_splitk(None, None, None, 64, 64, 64, 0, None) == sg.SGPU_ERR_INVALID_ARG
     assert L.sgpu_sgemm_splitk(None, None, None, 4096, 4096, 4096, 2, None) == sg.SGPU_ERR_INVALID_ARG
     assert L.sgpu_sgemm_splitk(None, None, None, 0, 64, 64, 2, None) == 0
+    assert L.sgpu_sgemm_small(None, None, None, 64, 64, 64, 8, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_small(None, None, None, 64, 64, 64, 16, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_small(None, None, None, 1 << 16, 64, 1 << 14, 32, None) == sg.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_small(None, None, None, 64, 0, 64, 32, None) == 0
     # streams and recorded launch sequences: NULL handles
     assert L.sgpu_stream_create(None) == sg.SGPU_ERR_INVALID_ARG
     assert L.sgpu_stream_destroy(None) == 0

@@ -103,9 +103,10 @@ def test_integer_exact(gpu, fn, M, N, K):
 DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 4096, 16),
                    (2048, 4096, 64), (2048, 4096, 96), (256, 256, 64), (192, 320, 40),
                    (4096, 4096, 96), (4096, 4352, 64), (4352, 4096, 160),
-                   # sgpu_sgemm_opt's split-K regimes: one row or column of tiles, and the
-                   # largest K-tailed problem the 4-way split takes (484 tiles, 31 MB of partials)
-                   (1, 4096, 4096), (4096, 1, 2048), (1408, 1408, 997)]
+                   # sgpu_sgemm_opt's small-member and split-K regimes: one row or column of
+                   # tiles (the 16x16 member at 4096 wide, split-K at 8192), and the largest
+                   # K-tailed problem the 4-way split takes (484 tiles, 31 MB of partials)
+                   (1, 4096, 4096), (4096, 1, 2048), (1, 8192, 4096), (8192, 1, 2048), (1408, 1408, 997)]
 
 
 @pytest.mark.parametrize("M,N,K", DISPATCH_SHAPES)
@@ -156,6 +157,50 @@ def test_splitk_integer_exact(gpu, M, N, K, S):
         gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, S, None)
         gpu.synchronize()
         assert np.array_equal(dC.to_host(), want)
+
+
+SMALL_CASES = [(1, 1, 1), (16, 16, 16), (33, 17, 96), (7, 300, 13), (256, 256, 256), (512, 512, 512),
+               (100, 70, 3000), (130, 260, 40), (257, 511, 1030), (1023, 1025, 997), (64, 48, 2)]
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+@pytest.mark.parametrize("M,N,K", SMALL_CASES)
+def test_small_integer_exact(gpu, M, N, K, tile):
+    """The small-problem members give the exact product on integer inputs (K tails, partial
+    tiles, K % 4 != 0 on the scalar A path), twice in a row."""
+    say(f"sgemm small{tile} integer {M}x{N}x{K}")
+    rng = np.random.default_rng(M * 3 + N * 5 + K + tile)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    for _ in range(2):
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_small", dA.ptr, dB.ptr, dC.ptr, M, N, K, tile, None)
+        gpu.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+
+
+@pytest.mark.parametrize("tile", [16, 32])
+def test_small_reference_generator_unaligned_and_k_zero(gpu, og, tile):
+    """Reference-generator inputs within the normwise bar of the oracle with A one float past
+    a 16-byte boundary (scalar A path), and K = 0 writing zeros."""
+    M, N, K = 200, 300, 512
+    say(f"sgemm small{tile} srand unaligned {M}x{N}x{K}")
+    A, B = gpu.gen_sgemm_inputs(max(M * K, K * N), 42)
+    A, B = A[:M * K], B[:K * N]
+    dA = gpu.DeviceArray(M * K + 1)
+    gpu.call("sgpu_memcpy_htod", dA.offset(1), A.ctypes.data, M * K * 4)
+    dB, dC = gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    gpu.call("sgpu_sgemm_small", dA.offset(1), dB.ptr, dC.ptr, M, N, K, tile, None)
+    gpu.synchronize()
+    C = dC.to_host().reshape(M, N)
+    ref = og.sgemm(A, B, M, N, K).astype(np.float64)
+    assert np.abs(C - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    dC.fill_bytes(0xFF)
+    gpu.call("sgpu_sgemm_small", dA.ptr, dB.ptr, dC.ptr, 5, 7, 0, tile, None)
+    gpu.synchronize()
+    assert np.array_equal(dC.to_host().reshape(-1)[:35], np.zeros(35, np.float32))
 
 
 def test_splitk_reference_generator_and_unaligned(gpu, og):
