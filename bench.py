@@ -112,10 +112,11 @@ GEMV_SHAPES = [("fp32", "gpt2 qkv", 2304, 768), ("fp32", "gpt2 attn-out", 768, 7
 ROTATE_BYTES = 600e6     # weight copies rotated per shape, up to 64: past the 256 MB MALL where that fits
 
 
-def bench_sgemm_sweep(reps=100, warm=50):
+def bench_sgemm_sweep(reps=100, warm=50, graphs=True):
     """sgpu_sgemm_opt over the SGEMM size sweep (square 256..4096 and the ragged 1023x1025x997),
     reference-generator inputs; HIP-event time per launch after warm-up, normwise error of
-    sampled rows against a float64 product."""
+    sampled rows against a float64 product.  graphs=False skips the recorded-graph timing
+    (a kernel trace of graph replay is not taken by the profiler)."""
     out = []
     for M, N, K in SWEEP_SHAPES:
         A, B = sgpu.gen_sgemm_inputs(max(M * K, K * N), 42)
@@ -136,6 +137,11 @@ def bench_sgemm_sweep(reps=100, warm=50):
             run()
         ev.record_stop(None)
         us = ev.elapsed_ms() * 1e3 / reps
+        if not graphs:
+            out.append({"M": M, "N": N, "K": K, "us_host_loop": round(us, 2), "normwise_err": err})
+            for d in (dA, dB, dC):
+                d.close()
+            continue
         # the same launches recorded once and replayed: no host submission cost per launch
         st = sgpu.Stream()
         per_graph = 10
@@ -363,6 +369,8 @@ def main():
                     help="skip the SGEMM size sweep and GEMV shape legs (they replay recorded graphs)")
     ap.add_argument("--pmc-probe", action="store_true", help="one launch per measured kernel, for rocprofv3 --pmc")
     ap.add_argument("--decode-only", action="store_true", help="run only the decode leg (for profiling it)")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="run only the SGEMM size sweep, host-loop launches (for profiling it)")
     ap.add_argument("--decode-path", choices=["reference", "fused", "graph"], default="graph")
     ap.add_argument("--decode-model", choices=["qwen", "gpt2"], default="qwen",
                     help="model of the --decode-only leg (gpt2: the graph path)")
@@ -376,6 +384,10 @@ def main():
         path = {"reference": 0, "fused": 1, "graph": 2}[args.decode_path]
         dec = bench_decode(path=path, compare=False)
         print(json.dumps({"decode_tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4)}))
+        return
+    if args.sweep_only:
+        sgpu.init(0)
+        print(json.dumps({"sgemm_sweep": bench_sgemm_sweep(graphs=False)}))
         return
     if args.pmc_probe:
         sgpu.init(0)
