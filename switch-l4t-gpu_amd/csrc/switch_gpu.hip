@@ -5,8 +5,10 @@
 //   sgemm_tiled, sgemm_tiled4, sgemm_opt : (const float*A, const float*B, float*C, int M, int N, int K)
 //   sgemm_naive                          : same arguments, one output per thread
 //   membw_read4                          : (const float4*buf, float*out, int n4, int iters)
-// plus sgemm_opt256, a larger-tile member with the same arguments, and sgemm_splitk
-//   (A, B, C, M, N, K, int S, float* ws, unsigned* cnt), the 64x64 tile with K split S ways.
+// plus sgemm_opt256, a larger-tile member with the same arguments, sgemm_splitk
+//   (A, B, C, M, N, K, int S, float* ws, unsigned* cnt), the 64x64 tile with K split S ways,
+// and sgemm_small16 / sgemm_small32 (same arguments as the reference members), one 16x16 /
+// 32x32 tile per block with the operands read straight into MFMA registers, no LDS staging.
 //
 // C = A*B, fp32, row-major (A: MxK stride K, B: KxN stride N, C: MxN stride N), overwrite
 // (alpha 1, beta 0).  Unlike the reference kernels, every shape is accepted: interior tiles
@@ -25,7 +27,8 @@
 // blocks exit); with one block per tile the index is remapped so each XCD (blocks are dealt
 // round-robin to the 8 XCDs) works on a compact group of tiles that shares A and B panels in
 // its own L2.  sgemm_splitk walks (tile, k-split) units the same way and sums a tile's splits
-// in the last split to finish.
+// in the last split to finish.  The small members (for problems whose few tiles cannot keep
+// a slice pipeline busy) are described where they are defined.
 #include <type_traits>
 
 #include "sgpu_device.h"
