@@ -622,8 +622,8 @@ extern "C" {
 // put the slice barrier before the last MFMA group.
 //   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), two slices'
 //                  loads in flight -- small shapes
-//   sgemm_tiled4 : 128x128 tile, BK 16, 4 waves of 64x64 (2x2 blocks), two slices' loads
-//                  in flight
+//   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks), two slices' loads
+//                  in flight, one wave per SIMD (288 registers, 70 KB of LDS)
 //   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks) -- large shapes
 //   sgemm_opt256 : 256x256 tile, BK 32, 4 waves of 128x128 (4x4 blocks), one wave per SIMD
 //                  (138 KB of LDS, 256 accumulator registers): half the LDS operand traffic
@@ -634,9 +634,9 @@ sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __r
     sgemm_mfma<64, 64, 32, 2, 2, 1, 4>(A, B, C, M, N, K);
 }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sgemm_tiled4(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
-    sgemm_mfma<128, 128, 16, 2, 2, 0, 4>(A, B, C, M, N, K);
+    sgemm_mfma<128, 128, 32, 2, 2, 1, 4>(A, B, C, M, N, K);
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
