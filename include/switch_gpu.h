@@ -120,7 +120,8 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * member (sgemm_opt256 256x256, sgemm_opt 128x256, sgemm_tiled4 128x128 or sgemm_tiled
  * 64x64 tiles) whose busiest CU has the least work: ceil(tiles / CUs) tiles times the
  * tile's area over the member's sustained rate.  Problems whose 16x16 tiles fit the CUs in
- * one round (K <= 4096) go to sgemm_small16, else those whose 32x32 tiles do (K <= 1024) to
+ * one round go to sgemm_small16 (K <= 2048, or K <= 4096 with a quarter of the CUs' tiles
+ * or one row or column of tiles), else those whose 32x32 tiles do (K <= 1024) to
  * sgemm_small32; of the rest, problems with fewer 64x64 tiles than half the CUs, and small
  * ones whose K is not a multiple of 32, go to sgemm_splitk. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);

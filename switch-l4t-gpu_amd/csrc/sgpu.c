@@ -570,8 +570,11 @@ static int splitk_pick(int M, int N, int K, int cus) {
     const int nk = cdiv(K, SK_BK);
     int S = 1;
     if (tiles * 2 <= cus) {
+        /* up to 8 splits, 16 when each split still holds 512 of K (one or two tiles of a
+         * tall-K problem: 64x64x8192 20.0 vs 25.3 us at 8, 32x32x16384 33.3 vs 52.1) */
         const long long r = cus / tiles;
-        while (S < 8 && S * 2 <= r) S *= 2;
+        const int cap = K / 16 >= 512 ? 16 : 8;
+        while (S < cap && S * 2 <= r) S *= 2;
     } else if (K % SK_BK && tiles <= 2LL * cus) {
         S = 4;
     }
@@ -614,11 +617,14 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     if (!d) return rc;
     /* Problems whose 16x16 (32x32) tiles fit the CUs in one round go to the small members
      * (measured in recorded graphs, srand inputs: 256^3 4.0 vs 7.7 us, 512^3 7.6 vs 9.7,
-     * 256x256x2048 9.4 vs 13.7, 100x70x3000 11.3 vs 16.0); past K 4096 (1024) a block's
-     * serial k-chain outlasts the split-K member. */
+     * 256x256x2048 9.4 vs 13.7, 100x70x3000 11.3 vs 16.0, 1x4096x4096 23.6 vs 27.8); past
+     * K 2048 a full round of 16x16 blocks' serial k-chains outlasts the split-K member
+     * (256x256x4096 22.0 vs 18.2) unless the tiles are few or the problem is one row or
+     * column of tiles, and past K 4096 (1024 for 32x32) it always does. */
     if (small_fits(M, N, K)) {
         const long long t16 = (long long)cdiv(M, 16) * cdiv(N, 16), t32 = (long long)cdiv(M, 32) * cdiv(N, 32);
-        if (t16 <= d->cus && K <= 4096) return small_launch(d, 16, A, B, C, M, N, K, stream);
+        if (t16 <= d->cus && K <= 4096 && (K <= 2048 || t16 * 4 <= d->cus || M <= 16 || N <= 16))
+            return small_launch(d, 16, A, B, C, M, N, K, stream);
         if (t32 <= d->cus && K <= 1024) return small_launch(d, 32, A, B, C, M, N, K, stream);
     }
     const int S = K > 0 ? splitk_pick(M, N, K, d->cus) : 1;

@@ -106,7 +106,9 @@ DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 
                    # sgpu_sgemm_opt's small-member and split-K regimes: one row or column of
                    # tiles (the 16x16 member at 4096 wide, split-K at 8192), and the largest
                    # K-tailed problem the 4-way split takes (484 tiles, 31 MB of partials)
-                   (1, 4096, 4096), (4096, 1, 2048), (1, 8192, 4096), (8192, 1, 2048), (1408, 1408, 997)]
+                   (1, 4096, 4096), (4096, 1, 2048), (1, 8192, 4096), (8192, 1, 2048), (1408, 1408, 997),
+                   # the small members' K bounds and the 16-way split of one tall-K tile
+                   (256, 256, 4096), (100, 70, 3000), (16, 4096, 4096), (64, 64, 8192)]
 
 
 @pytest.mark.parametrize("M,N,K", DISPATCH_SHAPES)
