@@ -142,7 +142,8 @@ int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, in
 /* The small-problem members sgemm_small16 / sgemm_small32 (tile = 16 or 32): one tile x tile
  * block of C per workgroup, A and B read straight into the matrix cores (no LDS staging), the
  * workgroup's four waves splitting K and summing their partials in a fixed order.  Any shape
- * with A and B under 2 GB (SGPU_ERR_INVALID_ARG otherwise).  No counterpart in the reference. */
+ * whose A (plus 32 rows) and B (plus 256 rows) stay under 2 GB (SGPU_ERR_INVALID_ARG
+ * otherwise).  No counterpart in the reference. */
 int sgpu_sgemm_small(const float *A, const float *B, float *C, int M, int N, int K, int tile, void *stream);
 int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 

@@ -585,10 +585,13 @@ static int splitk_pick(int M, int N, int K, int cus) {
 }
 
 /* sgemm_small16 / sgemm_small32: one 16x16 / 32x32 tile of C per block, operands read through
- * buffer resources with 32-bit offsets: A and B must stay under 2 GB including the k-group
- * overrun past K (at most 64 rows of B) and the row overrun past M (32 rows of A). */
+ * buffer resources with 32-bit offsets, which must not wrap: a wave's last batch of k-groups
+ * reads up to 4 * 4 groups (4 * 4 * 16 = 256 rows of B, 256 floats of an A row) past K, and
+ * rows past M up to the tile edge (32 rows of A); those reads land past the buffers' ends
+ * and return zero only while every offset stays below 2^31. */
 static int small_fits(int M, int N, int K) {
-    return (long long)(M + 32) * K * 4 + 256 < (1LL << 31) && (long long)(K + 64) * N * 4 < (1LL << 31);
+    return (long long)(M + 32) * K * 4 + (K + 256) * 4LL < (1LL << 31) &&
+           (long long)(K + 256) * N * 4 + 256 < (1LL << 31);
 }
 static int small_launch(devstate *d, int ts, const float *A, const float *B, float *C, int M, int N, int K,
                         void *stream) {
