@@ -590,7 +590,7 @@ static int splitk_pick(int M, int N, int K, int cus) {
  * rows past M up to the tile edge (32 rows of A); those reads land past the buffers' ends
  * and return zero only while every offset stays below 2^31. */
 static int small_fits(int M, int N, int K) {
-    return (long long)(M + 32) * K * 4 + (K + 256) * 4LL < (1LL << 31) &&
+    return (long long)(M + 32) * K * 4 + (K + 272) * 4LL < (1LL << 31) &&
            (long long)(K + 256) * N * 4 + 256 < (1LL << 31);
 }
 static int small_launch(devstate *d, int ts, const float *A, const float *B, float *C, int M, int N, int K,
