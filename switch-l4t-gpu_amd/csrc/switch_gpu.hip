@@ -621,7 +621,7 @@ extern "C" {
 // All of them stage A m-major, deal their memory instructions out over the MFMA stream and
 // put the slice barrier before the last MFMA group.
 //   sgemm_tiled  : 64x64 tile, BK 32, 4 waves of 32x32 (1 MFMA block each), two slices'
-//                  loads in flight -- small shapes
+//                  loads in flight, unconstrained register budget (172) -- small shapes
 //   sgemm_tiled4 : 128x128 tile, BK 32, 4 waves of 64x64 (2x2 blocks), two slices' loads
 //                  in flight, one wave per SIMD (288 registers, 70 KB of LDS)
 //   sgemm_opt    : 128x256 tile, BK 16, 4 waves of 64x128 (2x4 blocks) -- large shapes
@@ -629,7 +629,7 @@ extern "C" {
 //                  (138 KB of LDS, 256 accumulator registers): half the LDS operand traffic
 //                  per flop of the 64x128 wave tile and 16384 MFMA cycles between barriers --
 //                  shapes whose 256x256 tiles fill the CUs in whole rounds
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sgemm_tiled(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_mfma<64, 64, 32, 2, 2, 1, 4>(A, B, C, M, N, K);
 }
