@@ -652,7 +652,7 @@ sgemm_opt256(const float* __restrict__ A, const float* __restrict__ B, float* __
 // sgemm_splitk: the 64x64 tile with K split S ways: blocks are (tile, split) units, so a
 // problem with fewer tiles than CUs still spreads over the chip.  ws holds S*ntiles*4096
 // floats of partial tiles, cnt one zero-initialised counter per tile (left at zero again).
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_splitk(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K,
              int S, float* __restrict__ ws, unsigned* __restrict__ cnt) {
     sgemm_mfma<64, 64, 32, 2, 2, 1, 4, true>(A, B, C, M, N, K, S, ws, cnt);
