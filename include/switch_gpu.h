@@ -122,8 +122,9 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * tile's area over the member's sustained rate.  Problems whose 16x16 tiles fit the CUs in
  * one round go to sgemm_small16 (K <= 2048, or K <= 4096 with a quarter of the CUs' tiles
  * or one row or column of tiles), else those whose 32x32 tiles do (K <= 1024) to
- * sgemm_small32; of the rest, problems with fewer 64x64 tiles than half the CUs, and small
- * ones whose K is not a multiple of 32, go to sgemm_splitk. */
+ * sgemm_small32; of the rest, problems with fewer 64x64 tiles than half the CUs, small ones
+ * whose K is not a multiple of 32, and one-round ones where a 2-4 way split shortens the
+ * busiest CU's run of k-slices, go to sgemm_splitk. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);

@@ -108,7 +108,9 @@ DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 
                    # K-tailed problem the 4-way split takes (484 tiles, 31 MB of partials)
                    (1, 4096, 4096), (4096, 1, 2048), (1, 8192, 4096), (8192, 1, 2048), (1408, 1408, 997),
                    # the small members' K bounds and the 16-way split of one tall-K tile
-                   (256, 256, 4096), (100, 70, 3000), (16, 4096, 4096), (64, 64, 8192)]
+                   (256, 256, 4096), (100, 70, 3000), (16, 4096, 4096), (64, 64, 8192),
+                   # one round of 64x64 tiles split 3 and 4 ways
+                   (768, 768, 2048), (1024, 768, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", DISPATCH_SHAPES)
