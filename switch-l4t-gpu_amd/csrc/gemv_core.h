@@ -65,21 +65,48 @@ struct WF16 {
     __device__ static __forceinline__ float one(elem w) { return sgpu_h2f(w); }
 };
 
+// x element k as fp32: fp32 x as is, fp16-bit x (the fp16-x GEMV) with the exact reference
+// h2f decode -- the same operand values gemv_h sees for x = h2f(x16).
+__device__ __forceinline__ float x_at(const float* x, int k) { return x[k]; }
+__device__ __forceinline__ float x_at(const uint16_t* x, int k) { return sgpu_h2f(x[k]); }
+// The VEC values of x behind weight segment s (16 bytes of weights): fp32 x is read as
+// VEC/4 float4; fp16 x (VEC = 8 fp16 weights per segment) as one 16-byte load of 8 codes.
+template <int VEC>
+__device__ __forceinline__ void x_seg(const float* x, int s, float (&xa)[VEC]) {
+    const sgpu_f32x4* xv4 = reinterpret_cast<const sgpu_f32x4*>(x);
+#pragma unroll
+    for (int q = 0; q < VEC / 4; q++) {
+        const sgpu_f32x4 a = xv4[s * (VEC / 4) + q];
+#pragma unroll
+        for (int e = 0; e < 4; e++) xa[4 * q + e] = a[e];
+    }
+}
+template <int VEC>
+__device__ __forceinline__ void x_seg(const uint16_t* x, int s, float (&xa)[VEC]) {
+    static_assert(VEC == 8, "fp16 x pairs with fp16 weights: 8 codes per 16-byte segment");
+    const sgpu_u32x4 h = reinterpret_cast<const sgpu_u32x4*>(x)[s];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        xa[2 * i] = sgpu_h2f_lo(h[i]);
+        xa[2 * i + 1] = sgpu_h2f_hi(h[i]);
+    }
+}
+
 // Serial k-ascending dot product of one row with the exact reference decode; used for the
 // rare rows whose fast sum is not finite.
-template <class WT>
-__device__ __noinline__ float recompute_row(const typename WT::elem* __restrict__ row, const float* __restrict__ x,
+template <class WT, class XT>
+__device__ __noinline__ float recompute_row(const typename WT::elem* __restrict__ row, const XT* __restrict__ x,
                                             int K) {
     float acc = 0.0f;
-    for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
+    for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), x_at(x, k), acc);
     return acc;
 }
 
 // ---------------------------------------------------------------------------------------
-// Generic: wave per row.
-template <class WT>
+// Generic: wave per row.  XT = float, or uint16_t for fp16-bit x (fp16 weights only).
+template <class WT, class XT = float>
 __device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict__ W,
-                                             const float* __restrict__ x,
+                                             const XT* __restrict__ x,
                                              const float* __restrict__ bias,
                                              float* __restrict__ y, int K, int N) {
     typedef typename WT::vec vec;
@@ -94,7 +121,7 @@ __device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict
         for (int n = t; n < N; n += nt) {
             const typename WT::elem* row = W + (size_t)n * K;
             float acc = 0.0f;
-            for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
+            for (int k = 0; k < K; k++) acc = __builtin_fmaf(WT::one(row[k]), x_at(x, k), acc);
             y[n] = acc + (bias ? bias[n] : 0.0f);
         }
         return;
@@ -106,33 +133,23 @@ __device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict
         float acc = 0.0f;
         if (vec_ok) {
             const vec* rv = reinterpret_cast<const vec*>(row);
-            const sgpu_f32x4* xv4 = reinterpret_cast<const sgpu_f32x4*>(x);
             int s = lane;
             for (; s + 64 < nseg; s += 128) {         // two segments in flight per lane
                 const vec w0 = sgpu_ldnt(rv + s), w1 = sgpu_ldnt(rv + s + 64);
                 float xa[VEC], xb[VEC];
-#pragma unroll
-                for (int q = 0; q < VEC / 4; q++) {
-                    const sgpu_f32x4 a = xv4[s * (VEC / 4) + q], b = xv4[(s + 64) * (VEC / 4) + q];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) { xa[4 * q + e] = a[e]; xb[4 * q + e] = b[e]; }
-                }
+                x_seg<VEC>(x, s, xa);
+                x_seg<VEC>(x, s + 64, xb);
                 acc = WT::dot(w0, xa, acc);
                 acc = WT::dot(w1, xb, acc);
             }
             for (; s < nseg; s += 64) {
                 const vec w0 = sgpu_ldnt(rv + s);
                 float xa[VEC];
-#pragma unroll
-                for (int q = 0; q < VEC / 4; q++) {
-                    const sgpu_f32x4 a = xv4[s * (VEC / 4) + q];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) xa[4 * q + e] = a[e];
-                }
+                x_seg<VEC>(x, s, xa);
                 acc = WT::dot(w0, xa, acc);
             }
         } else {
-            for (int k = lane; k < K; k += 64) acc = __builtin_fmaf(WT::one(row[k]), x[k], acc);
+            for (int k = lane; k < K; k += 64) acc = __builtin_fmaf(WT::one(row[k]), x_at(x, k), acc);
         }
         acc = sgpu_group_sum<64>(acc);
         if (lane == 63) {
@@ -180,6 +197,22 @@ struct XPlain {
     const float* x;
     __device__ __forceinline__ sgpu_f32x4 load4(int k) const { return *reinterpret_cast<const sgpu_f32x4*>(x + k); }
     __device__ __forceinline__ float at(int k) const { return x[k]; }
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&)[S][VEC], const bool (&)[S], int, int, float*) {}
+};
+
+// x given as fp16 bit patterns (the fp16-x GEMV): each lane decodes its slice once into its
+// registers with the exact reference h2f (integer decode: subnormal codes +0, exponent-31
+// codes finite), so every dot product sees the operands gemv_h sees for x = h2f(x16).
+// load4(k) needs k % 4 == 0 and x 8-byte aligned.
+struct XHalf {
+    const uint16_t* x;
+    __device__ __forceinline__ sgpu_f32x4 load4(int k) const {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 h = *reinterpret_cast<const u32x2*>(x + k);
+        return sgpu_f32x4{sgpu_h2f_lo(h[0]), sgpu_h2f_hi(h[0]), sgpu_h2f_lo(h[1]), sgpu_h2f_hi(h[1])};
+    }
+    __device__ __forceinline__ float at(int k) const { return sgpu_h2f(x[k]); }
     template <int LPR, int S, int VEC>
     __device__ __forceinline__ void prepare(float (&)[S][VEC], const bool (&)[S], int, int, float*) {}
 };
@@ -412,6 +445,12 @@ template <class WT, int LPR, int S>
 __device__ __forceinline__ void gemv_xreg(const typename WT::elem* __restrict__ W, const float* __restrict__ x,
                                           const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
     gemv_team<WT, LPR, S, 1>(W, K, N, XPlain{x}, MapRows{}, EpiStore{bias, y});
+}
+// The tuned fp16-x GEMV: fp16 weights and fp16 x, fp32 accumulate, fp32 bias.
+template <int LPR, int S>
+__device__ __forceinline__ void gemv_xreg_hh(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+                                             const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
+    gemv_team<WF16, LPR, S, 1>(W, K, N, XHalf{x}, MapRows{}, EpiStore{bias, y});
 }
 
 // ---------------------------------------------------------------------------------------

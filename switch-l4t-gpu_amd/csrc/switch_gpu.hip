@@ -512,9 +512,10 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
 //          holds A[m][kb + 4h + t] and B[kb + 4h + t][n] for MFMA step t = 0..3.
 //   TS 16: v_mfma_f32_16x16x4f32, k-groups 16 deep: lane quarter q = lane / 16 holds
 //          A[m][kb + 4q + t] and B[kb + 4q + t][n] for step t.
-// Reads go through buffer resources sized to A and B: B past row K-1 and A past row M-1
-// read as zero; A elements past K (the next row's) are zeroed explicitly; columns past N read
-// the next row's elements and are not stored, nor are rows past M.
+// Reads go through buffer resources sized to A and B, the whole offset in the range-checked
+// vector offset: B past row K-1 and A past its last element read as zero (no memory past
+// either is touched); A elements past K (the next row's) are zeroed explicitly; columns past N
+// read the next row's elements and are not stored, nor are rows past M.
 template <int TS, int U, bool VEC>
 __device__ __forceinline__ void sgemm_small_tiles(const float* __restrict__ A, const float* __restrict__ B,
                                                   float* __restrict__ C, int M, int N, int K,
@@ -535,28 +536,35 @@ __device__ __forceinline__ void sgemm_small_tiles(const float* __restrict__ A, c
         // byte offsets of this lane's k = 4*hq in its A row and its B column
         const int aoff = ((m0 + li) * K + 4 * hq) * 4, boff = (4 * hq * N + n0 + li) * 4;
         sgpu_f32x4 a[2][U], b[2][U];
-        // per-lane byte offsets (voffset) fixed for the tile; the k-group part is wave-uniform
-        // and goes in the scalar offset, so no per-group address registers stay live
+        // The whole byte offset of every load, k part included, is its vector offset: the
+        // hardware range check covers the vector offset but not the scalar offset field, so
+        // only this way do B rows past K-1 and A elements past A's end read as zero without
+        // touching memory past either operand.  Batches load k-groups strictly in order, so
+        // the offsets are five running registers advanced in place by one group stride.
+        unsigned va = (unsigned)(aoff + wave * KG * 4), vb[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) vb[t] = (unsigned)(boff + (wave * KG + t) * N * 4);
+        const unsigned astride = 4u * KG * 4u, bstride = 4u * KG * (unsigned)N * 4u;   // 4 waves' groups
         auto load = [&](int i0, auto set_c) __attribute__((always_inline)) {
             constexpr int SET = decltype(set_c)::value;
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int kb = (wave + 4 * (i0 + u)) * KG;          // wave-uniform
                 if constexpr (VEC) {
-                    a[SET][u] = __builtin_bit_cast(sgpu_f32x4,
-                                                   __builtin_amdgcn_raw_buffer_load_b128(rsa, aoff, kb * 4, 0));
+                    a[SET][u] = __builtin_bit_cast(sgpu_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsa, (int)va, 0, 0));
                 } else {
 #pragma unroll
                     for (int t = 0; t < 4; t++)
                         a[SET][u][t] = __builtin_bit_cast(
-                            float, __builtin_amdgcn_raw_buffer_load_b32(rsa, aoff, (kb + t) * 4, 0));
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rsa, (int)(va + t * 4u), 0, 0));
                 }
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     if (kb + 4 * hq + t >= K) a[SET][u][t] = 0.0f;
-                    b[SET][u][t] = __builtin_bit_cast(
-                        float, __builtin_amdgcn_raw_buffer_load_b32(rsb, boff, (kb + t) * N * 4, 0));
+                    b[SET][u][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsb, (int)vb[t], 0, 0));
+                    vb[t] += bstride;
                 }
+                va += astride;
             }
         };
         accv acc0 = {}, acc1 = {};                 // two chains: even and odd steps
@@ -661,7 +669,7 @@ sgemm_splitk(const float* __restrict__ A, const float* __restrict__ B, float* __
 // sgemm_small16 / sgemm_small32: problems too small to fill the chip with 64x64 tiles (one
 // 16x16 or 32x32 tile of C per block, operands straight from memory into the matrix cores,
 // the block's four waves splitting K).
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 sgemm_small16(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_small<16, 4>(A, B, C, M, N, K);
 }

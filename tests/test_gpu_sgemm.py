@@ -185,6 +185,41 @@ def test_small_integer_exact(gpu, M, N, K, tile):
         assert np.array_equal(dC.to_host(), want)
 
 
+NAN_PAD_CASES = [(7, 300, 13), (100, 70, 3000), (33, 17, 96), (64, 48, 2), (257, 511, 1030)]
+
+
+@pytest.mark.parametrize("a_off", [0, 1])
+@pytest.mark.parametrize("launcher", ["small16", "small32", "splitk4", "sgpu_sgemm_opt", "sgpu_sgemm_tiled",
+                                      "sgpu_sgemm_opt256"])
+@pytest.mark.parametrize("M,N,K", NAN_PAD_CASES)
+def test_operands_followed_by_nan_integer_exact(gpu, M, N, K, launcher, a_off):
+    """A and B sit at the start of larger allocations whose remaining floats are NaN: 512 rows
+    of B past row K-1 and K + 512 floats past A's last element (more than any load of a K tail
+    or k-group batch reaches).  A kernel that read past either operand would put NaN into C
+    (0 * NaN); every read stays inside the allocations, so the run is in bounds either way.
+    a_off = 1 starts A one float past a 16-byte boundary (scalar A loads)."""
+    say(f"sgemm {launcher} nan-padded {M}x{N}x{K} a_off={a_off}")
+    rng = np.random.default_rng(M * 5 + N * 3 + K)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    ha = np.full(a_off + M * K + K + 512, np.nan, np.float32)
+    ha[a_off:a_off + M * K] = A.reshape(-1)
+    hb = np.full((K + 512) * N, np.nan, np.float32)
+    hb[:K * N] = B.reshape(-1)
+    dA, dB, dC = gpu.DeviceArray.from_host(ha), gpu.DeviceArray.from_host(hb), gpu.DeviceArray((M, N))
+    for _ in range(2):
+        dC.fill_bytes(0xFF)
+        if launcher.startswith("small"):
+            gpu.call("sgpu_sgemm_small", dA.offset(a_off), dB.ptr, dC.ptr, M, N, K, int(launcher[5:]), None)
+        elif launcher == "splitk4":
+            gpu.call("sgpu_sgemm_splitk", dA.offset(a_off), dB.ptr, dC.ptr, M, N, K, 4, None)
+        else:
+            gpu.call(launcher, dA.offset(a_off), dB.ptr, dC.ptr, M, N, K, None)
+        gpu.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+
+
 @pytest.mark.parametrize("tile", [16, 32])
 def test_small_reference_generator_unaligned_and_k_zero(gpu, og, tile):
     """Reference-generator inputs within the normwise bar of the oracle with A one float past
