@@ -175,6 +175,15 @@ int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y,
  * bias are fp32, bias nullable.  Any K (the reference needs K % 4 == 0). */
 int sgpu_gemv_h(const uint16_t *W, const float *x, const float *bias, float *y, int K, int N,
                 void *stream);
+/* fp16-x GEMV, gemv_hh: gemv_h (qwen_kernels.cu:34-70) with x stored as fp16 bit patterns
+ * as well, decoded with the same h2f contract as W (qwen_kernels.cu:6-14), fp32 accumulate,
+ * fp32 bias (nullable): y[n] = sum_k h2f(W[n*K+k]) * h2f(x[k]) + bias?[n] -- bit for bit
+ * what sgpu_gemv_h gives for x = h2f(x16).  Any K; the tuned path needs W and x 16-byte
+ * aligned (K % 8 == 0), other calls take the by-name gemv_hh symbol.  No counterpart in the
+ * reference, whose gemv_h reads fp32 x only: the fp16-activation variant of the Qwen GEMV
+ * shapes (qwen_engine.c:219,242,249,256,265). */
+int sgpu_gemv_hh(const uint16_t *W, const uint16_t *x, const float *bias, float *y, int K, int N,
+                 void *stream);
 
 /* ---- Qwen2.5 decode support kernels (qwen_kernels.cu:72-189), launched per layer by
  * gpu_forward (qwen_engine.c:216-264). ---- */

@@ -101,6 +101,18 @@ void og_gemv_h_fbias(const uint16_t *W, const float *x, const float *bias, float
     }
 }
 
+/* gemv_h's dot product (qwen_kernels.cu:34-70; serial golden qwen_engine.c:276-284) with x
+ * given as fp16 bits: every x code decoded once with the reference h2f (qwen_engine.c:90-98),
+ * then the same k-ascending sum as og_gemv_h_fbias. */
+void og_gemv_hh(const uint16_t *W, const uint16_t *x, const float *bias, float *y,
+                int K, int N, int nthreads) {
+    float *xf = (float *)malloc((K > 0 ? (size_t)K : 1) * sizeof(float));
+    if (!xf) return;
+    for (int k = 0; k < K; k++) xf[k] = og_h2f(x[k]);
+    og_gemv_h_fbias(W, xf, bias, y, K, N, nthreads);
+    free(xf);
+}
+
 /* gpt2_kernels.cu:110-155 computes Y[t*N+n] = W[n,:].X[t,:] + bias?[n]; the golden is the
  * serial dot product per (t, n), as cpu_gemv (gpt2_engine.c:342-349) applied row by row. */
 void og_gemv_multi(const float *W, const float *X, const float *bias, float *Y,

@@ -14,6 +14,8 @@
  *   og_sgemm*         small-integer inputs (exact in fp32) vs int64 matmul; identity;
  *                     fp64 brute force within the fp32 rounding bound
  *   og_gemv*          same integer trick, bias/NULL-bias, N != K argument order
+ *   og_gemv_hh        integer fp16 W and x vs int64; equals og_gemv_h_fbias on numpy's IEEE
+ *                     decode of normal x codes; x subnormals read +0, exponent-31 x finite
  *   og_gemv_multi     reduces to og_gemv row by row (T = 1 and T > 1)
  *   og_rms            torch.nn.functional.rms_norm
  *   og_rope_tables    closed form cos/sin(pos * theta^(-2d/HD)) in float64
@@ -57,6 +59,12 @@ void og_gemv_h(const uint16_t *W, const float *x, const uint16_t *bias, float *y
  * decode of qwen_engine.c:170-175): bias is fp32 (already h2f-decoded), nullable. */
 void og_gemv_h_fbias(const uint16_t *W, const float *x, const float *bias, float *y,
                      int K, int N, int nthreads);
+
+/* The fp16-x form of gemv_h: x as fp16 bits too, decoded with og_h2f like W (the same
+ * contract, qwen_kernels.cu:6-14), then og_gemv_h_fbias's serial dot product; bias fp32,
+ * nullable.  No reference counterpart (the reference gemv_h reads fp32 x only). */
+void og_gemv_hh(const uint16_t *W, const uint16_t *x, const float *bias, float *y,
+                int K, int N, int nthreads);
 
 /* Batched GEMV, Y[t*N+n] = sum_k W[n*K+k]*X[t*K+k] + (bias ? bias[n] : 0)
  * (gpt2_kernels.cu:110-155 semantics; serial k order per output). */

@@ -35,6 +35,7 @@ _SIGS = {
     "og_gemv": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "og_gemv_h": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "og_gemv_h_fbias": (None, [_P, _P, _P, _P, _I, _I, _I]),
+    "og_gemv_hh": (None, [_P, _P, _P, _P, _I, _I, _I]),
     "og_gemv_multi": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "og_rms": (None, [_P, _P, _P, _I, _F]),
     "og_qwen_file_bytes": (_S, [ct.POINTER(QwenCfg)]),
@@ -122,6 +123,16 @@ def gemv_h_fbias(W16, x, bias, K, N, nthreads=1):
     y = np.empty(N, np.float32)
     lib().og_gemv_h_fbias(W16.ctypes.data, x.ctypes.data, b.ctypes.data if b is not None else None, y.ctypes.data,
                           K, N, nthreads)
+    return y
+
+
+def gemv_hh(W16, x16, bias, K, N, nthreads=1):
+    W16 = np.ascontiguousarray(W16, np.uint16)
+    x16 = np.ascontiguousarray(x16, np.uint16)
+    b = _f32(bias) if bias is not None else None
+    y = np.empty(N, np.float32)
+    lib().og_gemv_hh(W16.ctypes.data, x16.ctypes.data, b.ctypes.data if b is not None else None, y.ctypes.data,
+                     K, N, nthreads)
     return y
 
 

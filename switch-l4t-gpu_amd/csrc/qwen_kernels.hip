@@ -4,6 +4,9 @@
 // Symbols and arguments as the reference; activations fp32, weights fp16 bits decoded with
 // the reference's h2f contract (subnormals -> +0, exponent 31 finite):
 //   gemv_h          (const u16*W, const float*x, const float*bias, float*y, int K, int N)
+//   gemv_hh         (const u16*W, const u16*x, const float*bias, float*y, int K, int N)
+//                   the fp16-x form of gemv_h (no reference counterpart): x holds fp16 bit
+//                   patterns decoded with the same h2f contract as W, fp32 accumulate
 //   rmsnorm         (const float*x, const u16*w, float*y, int n, float eps)   grid = rows
 //   rope            (float*x, const float*cosT, const float*sinT, int T, int H, int HD, int pos0)
 //   swiglu          (const float*g, const float*u, float*y, int n)
@@ -23,6 +26,13 @@ extern "C" {
 __global__ void gemv_h(const uint16_t* __restrict__ W, const float* __restrict__ x,
                        const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
     sgpu::gemv_generic<sgpu::WF16>(W, x, bias, y, K, N);
+}
+
+// y[n] = sum_k h2f(W[n*K+k]) * h2f(x[k]) + (bias ? bias[n] : 0): gemv_h's contract with x
+// stored as fp16 bits (half the x bytes; activations kept in fp16).  Any grid.
+__global__ void gemv_hh(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+                        const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
+    sgpu::gemv_generic<sgpu::WF16, uint16_t>(W, x, bias, y, K, N);
 }
 
 // One block per row (grid = rows), blockDim a multiple of 64 (256 from the launcher).

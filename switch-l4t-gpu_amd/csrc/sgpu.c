@@ -48,7 +48,7 @@ enum {
     K_SGEMM_NAIVE, K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK, K_GEMV_MULTI_X8_64,
     K_GEMV_MULTI_X8_256,
-    K_GEMV_H, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
+    K_GEMV_H, K_GEMV_HH, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
     K_EMBED_H,
     K_LAYERNORM, K_GELU, K_ADD_BIAS, K_G2_SCORES, K_G2_SOFTMAX, K_G2_MIX,
     NKERN
@@ -64,7 +64,7 @@ static const struct {
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
     {MOD_GPT2, "gemv_multi_x8_l64"}, {MOD_GPT2, "gemv_multi_x8_l256"},
-    {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
+    {MOD_QWEN, "gemv_h"}, {MOD_QWEN, "gemv_hh"}, {MOD_QWEN, "rmsnorm"}, {MOD_QWEN, "rope"}, {MOD_QWEN, "swiglu"},
     {MOD_QWEN, "attn_scores_gqa"}, {MOD_QWEN, "attn_softmax"}, {MOD_QWEN, "attn_mix_gqa"},
     {MOD_QWEN, "add2"},
     {MOD_TUNED, "sgpu_embed_h"},
@@ -95,7 +95,7 @@ typedef struct {
     int cus;
     hipModule_t mod[NMOD];
     hipFunction_t fn[NKERN];
-    hipFunction_t gemv_f32[NLPR][NSEG], gemv_h[NLPR][NSEG];
+    hipFunction_t gemv_f32[NLPR][NSEG], gemv_h[NLPR][NSEG], gemv_hh[NLPR][NSEG];
     hipFunction_t dec[NDECFAM][NDEC_ALL];
     hipFunction_t dec_attn[3], dec_embed, dec_argmax_part, dec_argmax_embed;
     hipFunction_t dec_g2embed, dec_argmax_g2embed;
@@ -161,6 +161,9 @@ static int load_device(int dev) {
             if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
             snprintf(name, sizeof name, "sgpu_gemv_h_l%d_s%d", g_lpr[i], g_segs[j]);
             e = hipModuleGetFunction(&d->gemv_h[i][j], d->mod[MOD_TUNED], name);
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+            snprintf(name, sizeof name, "sgpu_gemv_hh_l%d_s%d", g_lpr[i], g_segs[j]);
+            e = hipModuleGetFunction(&d->gemv_hh[i][j], d->mod[MOD_TUNED], name);
             if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
         }
     for (int f = 0; f < NDECFAM; f++) {
@@ -437,7 +440,7 @@ static int geometry(const devstate *d, const char *kernel, int M, int N, int K, 
         return SGPU_OK;
     }
     if (!strcmp(kernel, "gemv") || !strcmp(kernel, "gemv4") || !strcmp(kernel, "gemv_warp") ||
-        !strcmp(kernel, "gemv_warp_b") || !strcmp(kernel, "gemv_h")) {
+        !strcmp(kernel, "gemv_warp_b") || !strcmp(kernel, "gemv_h") || !strcmp(kernel, "gemv_hh")) {
         g[0] = umin(cdiv(N > 0 ? N : 1, 4), cus * 16);   /* a wave per row, 4 waves per block */
         b[0] = 256;
         return SGPU_OK;
@@ -689,13 +692,17 @@ static void pick_tuned(const devstate *d, int K, int N, int vec, int *li, int *s
         if (g_segs[j] >= s) { *li = best_l; *si = j; return; }
 }
 
+/* Weight / x storage of a GEMV launch: fp32 W and x, fp16 W with fp32 x (gemv_h), or fp16 W
+ * with fp16 x (gemv_hh). */
+enum { GV_F32, GV_H, GV_HH };
+
 /* Grid cap of the persistent tuned GEMVs (blocks per CU), reached only by lm_head-sized row
  * counts.  Measured on the lm_head shapes with rotating weight copies: fp16 [151936 x 896]
  * peaks at 18 blocks per CU (86.2% of HBM; 84.0% at 8), fp32 [50257 x 768] at 4 (81.5%;
  * 80.3% at 8) -- its lanes keep 1.7x more bytes in flight. */
-static unsigned gemv_blocks_per_cu(int is_h) { return is_h ? 18u : 4u; }
+static unsigned gemv_blocks_per_cu(int kind) { return kind != GV_F32 ? 18u : 4u; }
 
-static int gemv_launch(int generic_kid, int is_h, const void *W, const float *x, const float *bias, float *y,
+static int gemv_launch(int generic_kid, int kind, const void *W, const void *x, const float *bias, float *y,
                        int K, int N, void *stream) {
     if (K < 0 || N < 0) return SGPU_ERR_INVALID_ARG;
     if (N == 0) return SGPU_OK;
@@ -704,14 +711,15 @@ static int gemv_launch(int generic_kid, int is_h, const void *W, const float *x,
     devstate *d = cur(&rc);
     if (!d) return rc;
     void *args[] = {(void *)&W, (void *)&x, (void *)&bias, (void *)&y, &K, &N};
-    const int vec = is_h ? 8 : 4;
+    const int vec = kind == GV_F32 ? 4 : 8;
     int li, si;
     pick_tuned(d, K, N, vec, &li, &si);
     const int aligned = ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0;
     if (li >= 0 && aligned) {
         const int teams = 256 / g_lpr[li];
-        unsigned g[3] = {umin(cdiv(N, teams), (unsigned)d->cus * gemv_blocks_per_cu(is_h)), 1, 1}, b[3] = {256, 1, 1};
-        return launch(is_h ? d->gemv_h[li][si] : d->gemv_f32[li][si], g, b, stream, args);
+        unsigned g[3] = {umin(cdiv(N, teams), (unsigned)d->cus * gemv_blocks_per_cu(kind)), 1, 1}, b[3] = {256, 1, 1};
+        hipFunction_t f = kind == GV_F32 ? d->gemv_f32[li][si] : kind == GV_H ? d->gemv_h[li][si] : d->gemv_hh[li][si];
+        return launch(f, g, b, stream, args);
     }
     unsigned g[3], b[3];
     geometry(d, "gemv_h", 0, N, K, g, b);
@@ -723,19 +731,22 @@ static int gemv_launch(int generic_kid, int is_h, const void *W, const float *x,
 }
 
 int sgpu_gemv(const float *W, const float *x, float *y, int K, int N, void *stream) {
-    return gemv_launch(K_GEMV, 0, W, x, NULL, y, K, N, stream);
+    return gemv_launch(K_GEMV, GV_F32, W, x, NULL, y, K, N, stream);
 }
 int sgpu_gemv4(const float *W, const float *x, float *y, int K, int N, void *stream) {
-    return gemv_launch(K_GEMV4, 0, W, x, NULL, y, K, N, stream);
+    return gemv_launch(K_GEMV4, GV_F32, W, x, NULL, y, K, N, stream);
 }
 int sgpu_gemv_warp(const float *W, const float *x, float *y, int K, int N, void *stream) {
-    return gemv_launch(K_GEMV_WARP, 0, W, x, NULL, y, K, N, stream);
+    return gemv_launch(K_GEMV_WARP, GV_F32, W, x, NULL, y, K, N, stream);
 }
 int sgpu_gemv_warp_b(const float *W, const float *x, const float *bias, float *y, int K, int N, void *stream) {
-    return gemv_launch(K_GEMV_WARP_B, 0, W, x, bias, y, K, N, stream);
+    return gemv_launch(K_GEMV_WARP_B, GV_F32, W, x, bias, y, K, N, stream);
 }
 int sgpu_gemv_h(const uint16_t *W, const float *x, const float *bias, float *y, int K, int N, void *stream) {
-    return gemv_launch(K_GEMV_H, 1, W, x, bias, y, K, N, stream);
+    return gemv_launch(K_GEMV_H, GV_H, W, x, bias, y, K, N, stream);
+}
+int sgpu_gemv_hh(const uint16_t *W, const uint16_t *x, const float *bias, float *y, int K, int N, void *stream) {
+    return gemv_launch(K_GEMV_HH, GV_HH, W, x, bias, y, K, N, stream);
 }
 
 /* K splits for the batched matrix-core GEMM (32-token x 32-row tiles): with fewer tiles than

@@ -2,6 +2,8 @@
 //
 //   sgpu_gemv_f32_l<LPR>_s<S>(const float*W,  const float*x, const float*bias, float*y, int K, int N)
 //   sgpu_gemv_h_l<LPR>_s<S>  (const u16*W,    const float*x, const float*bias, float*y, int K, int N)
+//   sgpu_gemv_hh_l<LPR>_s<S> (const u16*W,    const u16*x,   const float*bias, float*y, int K, int N)
+//     (fp16 x, decoded with the reference h2f; fp32 accumulate)
 //
 // LPR = lanes per row (16, 64, or 256 = four waves split-K), S = 16-byte segments per lane.
 // Launch: blocks of 256 threads; preconditions in gemv_core.h (gemv_xreg).
@@ -17,6 +19,11 @@
         const uint16_t* __restrict__ W, const float* __restrict__ x, const float* __restrict__ bias, \
         float* __restrict__ y, int K, int N) {                                                     \
         sgpu::gemv_xreg<sgpu::WF16, LPR, S>(W, x, bias, y, K, N);                                  \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) sgpu_gemv_hh_l##LPR##_s##S(                  \
+        const uint16_t* __restrict__ W, const uint16_t* __restrict__ x, const float* __restrict__ bias, \
+        float* __restrict__ y, int K, int N) {                                                     \
+        sgpu::gemv_xreg_hh<LPR, S>(W, x, bias, y, K, N);                                           \
     }
 
 #define SGPU_GEMV_INST_S(LPR) \

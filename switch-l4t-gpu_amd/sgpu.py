@@ -88,6 +88,7 @@ _SIGS = {
     "sgpu_gemv_warp_b": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "sgpu_gemv_multi": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "sgpu_gemv_h": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "sgpu_gemv_hh": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "sgpu_rmsnorm": (_I, [_P, _P, _P, _I, _F, _I, _P]),
     "sgpu_rope": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_swiglu": (_I, [_P, _P, _P, _I, _P]),

@@ -1,6 +1,7 @@
 """Batch-1 GEMV family and the read-bandwidth probe on the GPU through the C ABI, against
 the oracle (og_gemv: gemv_test.c:85-90 / gpt2_engine.c:342-349; og_gemv_h: qwen_engine.c:276-284;
-og_gemv_multi: gpt2_kernels.cu:110-155 semantics) and exact integer arithmetic.
+og_gemv_multi: gpt2_kernels.cu:110-155 semantics; og_gemv_hh: the fp16-x form of gemv_h) and
+exact integer arithmetic.
 
 Bars: fp32 weights, per element |y - y_ref| <= 1e-4 |y_ref| + 1e-4 (gemv_test.c:119);
 fp16 weights (fp32 accumulate) max|y - y_ref| / max|y_ref| <= 1e-3 and per element
@@ -63,6 +64,77 @@ def test_qwen_shapes_fp16(gpu, og, N, K):
     m = np.abs(ref).max()
     assert np.abs(y - ref).max() / m <= 1e-3
     assert np.all(np.abs(y - ref) <= 1e-3 * np.abs(ref) + 1e-3 * m)
+
+
+def gemv_hh_dev(gpu, W, x16, bias, K, N, x_off=0):
+    """sgpu_gemv_hh with x (fp16 codes) placed x_off codes into its allocation."""
+    dW = gpu.DeviceArray.from_host(W)
+    dx = gpu.DeviceArray(K + x_off + 8, np.uint16)
+    gpu.call("sgpu_memcpy_htod", dx.offset(x_off), np.ascontiguousarray(x16, np.uint16).ctypes.data, K * 2)
+    dy = gpu.DeviceArray(N)
+    dy.fill_bytes(0xFF)
+    db = gpu.DeviceArray.from_host(np.asarray(bias, np.float32)) if bias is not None else None
+    gpu.call("sgpu_gemv_hh", dW.ptr, dx.offset(x_off), db.ptr if db is not None else None, dy.ptr, K, N, None)
+    gpu.synchronize()
+    return dy.to_host()
+
+
+@pytest.mark.parametrize("N,K", QWEN_SHAPES)
+def test_qwen_shapes_fp16_x(gpu, og, N, K):
+    """The fp16-x GEMV at every Qwen shape (fused qkv with its bias, gate|up, the lm_head):
+    within the fp16 bars of the oracle, and bit for bit sgpu_gemv_h on the h2f-decoded x."""
+    say(f"gemv_hh {N}x{K}")
+    Wf, s = gpu.gen_normal(N * K, 11 + N, 0.0, 0.02)
+    W = gpu.f32_to_f16(Wf)
+    xf, s = gpu.gen_normal(K, s, 0.0, 1.0)
+    x16 = gpu.f32_to_f16(xf)
+    bias = gpu.gen_normal(N, s, 0.0, 0.02)[0] if N == 1152 else None
+    y = gemv_hh_dev(gpu, W, x16, bias, K, N)
+    ref = og.gemv_hh(W, x16, bias, K, N, NT)
+    m = np.abs(ref).max()
+    assert np.abs(y - ref).max() / m <= 1e-3
+    assert np.all(np.abs(y - ref) <= 1e-3 * np.abs(ref) + 1e-3 * m)
+    yh = gemv_dev(gpu, "sgpu_gemv_h", W, og.h2f_array(x16), bias, K, N)
+    assert np.array_equal(y.view(np.uint32), yh.view(np.uint32))
+
+
+EDGE_HH = [(1, 1), (5, 3), (64, 8), (63, 16), (1000, 63), (7, 896), (300, 4864), (33, 5000), (2, 40000)]
+
+
+@pytest.mark.parametrize("N,K", EDGE_HH)
+def test_gemv_hh_integer_exact_edges(gpu, N, K):
+    """Integer-valued fp16 W, x and bias: exact at ragged K, with x aligned (tuned kernels)
+    and one code off 16 bytes (the by-name gemv_hh symbol)."""
+    say(f"gemv_hh integer {N}x{K}")
+    rng = np.random.default_rng(N * 17 + K)
+    Wi, xi, bi = rng.integers(-3, 4, (N, K)), rng.integers(-3, 4, K), rng.integers(-5, 6, N)
+    W, x16 = Wi.astype(np.float16).view(np.uint16), xi.astype(np.float16).view(np.uint16)
+    want = (Wi @ xi + bi).astype(np.float32)
+    for x_off in (0, 1):
+        assert np.array_equal(gemv_hh_dev(gpu, W, x16, bi, K, N, x_off=x_off), want)
+
+
+def test_gemv_hh_special_x_codes(gpu, og):
+    """x codes decoded with the reference h2f on the device: subnormals and -0 read +0,
+    exponent-31 codes the finite 2^16 (1 + m/1024).  Integer W codes and at most 48
+    exponent-31 x codes per row keep every fp32 partial sum exact (multiples of 64 below
+    2^24 plus small integers), so the result is order-free and compared bit for bit."""
+    rng = np.random.default_rng(23)
+    N, K = 64, 896
+    big = np.concatenate([np.arange(0x7c00, 0x8000), np.arange(0xfc00, 0x10000)]).astype(np.uint16)
+    small = np.concatenate([np.arange(0, 1024), np.arange(0x8000, 0x8400),               # subnormals, -0
+                            np.array([0x3c00, 0x4000, 0x4200, 0xbc00, 0xc000, 0xc200] * 50)]).astype(np.uint16)
+    x16 = rng.choice(small, K).astype(np.uint16)
+    x16[rng.choice(K, 48, replace=False)] = rng.choice(big, 48)
+    W = rng.integers(-2, 3, (N, K)).astype(np.float16).view(np.uint16)
+    ref = og.gemv_hh(W, x16, None, K, N)
+    # independent of the oracle: the closed-form decode of x in float64
+    e, m = (x16 >> 10) & 31, (x16 & 1023).astype(np.float64)
+    sgn = np.where(x16 >> 15, -1.0, 1.0)
+    xd = np.where(e == 0, 0.0, np.where(e == 31, sgn * 65536.0 * (1 + m / 1024), x16.view(np.float16).astype(np.float64)))
+    assert np.array_equal(ref, (W.view(np.float16).astype(np.float64) @ xd).astype(np.float32))
+    for x_off in (0, 1):
+        assert np.array_equal(gemv_hh_dev(gpu, W, x16, None, K, N, x_off=x_off), ref)
 
 
 def test_recorded_launches_replay(gpu, og):

@@ -223,6 +223,47 @@ def test_gemv_h_special_codes(og):
     assert og.gemv_h(W, x, None, K, 1)[0] == np.float32(want)
 
 
+# ------------------------------------- GEMV fp16 weights and fp16 x (the fp16-x variant)
+def test_gemv_hh_integers_exact(og):
+    """Integer fp16 W and x (exact in fp16 and in every fp32 partial sum) against int64,
+    with and without bias, N != K (a transposed operand or a dropped bias fails)."""
+    rng = np.random.default_rng(19)
+    N, K = 37, 200
+    Wi = rng.integers(-16, 17, (N, K))
+    xi = rng.integers(-16, 17, K)
+    bi = rng.integers(-50, 51, N)
+    Wh = Wi.astype(np.float16).view(np.uint16)
+    xh = xi.astype(np.float16).view(np.uint16)
+    assert np.array_equal(og.gemv_hh(Wh, xh, None, K, N).astype(np.int64), Wi @ xi)
+    assert np.array_equal(og.gemv_hh(Wh, xh, bi.astype(np.float32), K, N).astype(np.int64), Wi @ xi + bi)
+
+
+def test_gemv_hh_is_gemv_h_on_ieee_decoded_x(og):
+    """On normal x codes (exponent 1..30) the fp16-x GEMV is gemv_h over numpy's IEEE half
+    decode of x, bit for bit, at a Qwen shape with the fused-qkv bias."""
+    rng = np.random.default_rng(20)
+    N, K = 1152, 896
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float16).view(np.uint16)
+    x16 = rng.standard_normal(K).astype(np.float16)
+    x16[np.abs(x16) < np.float16(2.0 ** -14)] = np.float16(0.5)         # keep every code normal
+    bias = (rng.standard_normal(N) * 0.02).astype(np.float32)
+    got = og.gemv_hh(W, x16.view(np.uint16), bias, K, N, nthreads=4)
+    want = og.gemv_h_fbias(W, x16.astype(np.float32), bias, K, N, nthreads=4)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_gemv_hh_special_x_codes(og):
+    """x codes follow the reference h2f: subnormals and -0 read +0 (IEEE would give nonzero
+    subnormals), exponent 31 reads the finite 2^16 (1 + m/1024) (IEEE: inf/NaN)."""
+    K = 6
+    x = np.array([0x0001, 0x83ff, 0x7c00, 0xfc01, 0x7fff, 0x3c00], np.uint16)
+    W = np.eye(K, dtype=np.float16).view(np.uint16)                     # y[n] = decoded x[n]
+    y = og.gemv_hh(W, x, None, K, K)
+    want = np.array([0.0, 0.0, 65536.0, -65536.0 * (1 + 1 / 1024), 65536.0 * (1 + 1023 / 1024), 1.0], np.float32)
+    assert np.array_equal(y, want)
+    assert not np.signbit(y[1])
+
+
 # ---------------------------------------------------------- RMSNorm / RoPE tables
 def test_rms_matches_torch(og):
     torch = pytest.importorskip("torch")
