@@ -15,8 +15,16 @@ Secondary figures measured in the same run (same JSON line):
   Both report the time per launch replayed from a recorded graph (rates are computed from it)
   and per launch from a host loop of ctypes calls (which adds the host's submission cost).
   decode -- random-init Qwen2.5-0.5B-architecture decode, 32-token prompt, 128 greedy tokens
-The CPU baseline is the oracle's serial-order SGEMM (row-parallel over the host cores) on a
-bounded sample of rows of the same 4096^3 problem.
+  gemv_hh -- the same lm_head with fp16 x (sgpu_gemv_hh), its own HBM roofline
+Clocks: before the counted warm-up, SGEMM launches run for a stated settling time (the GPU
+clock climbs from idle over tens of milliseconds); the steady-state kernel time of a longer
+event-timed loop after the timed steps is reported beside `value`.
+CPU baselines (the oracle, i.e. the restated reference CPU goldens, on the host's cores --
+the threads used, the CPU model and the visible core count are in each entry): the SGEMM on a
+bounded sample of rows of the same 4096^3 problem (top-level cpu_baseline); og_gemv_h on the
+lm_head shape (gemv.cpu_baseline); og_qwen_forward on the same random-init model for a few
+positions (decode.cpu_baseline); each row-parallel over the threads and, for the GEMV and
+decode, also on one thread in the reference's serial form.
 """
 import argparse
 import ctypes as ct
@@ -42,7 +50,32 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def bench_sgemm(n, steps, warmup):
+def host_info():
+    """CPU model and core counts of the host running the bench."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cpu_count": os.cpu_count(), "cpus_available": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_threads():
+    """Threads for the row-parallel CPU legs: every core this process may use, capped by
+    OMP_NUM_THREADS when it is set (the host's CPU share for one GPU)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def bench_sgemm(n, steps, warmup, settle_s=0.3, steady_launches=200):
     A, B = sgpu.gen_sgemm_inputs(n * n, 42)
     dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((n, n))
     run = lambda: sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, n, n, n, None)
@@ -53,8 +86,16 @@ def bench_sgemm(n, steps, warmup):
     rows = np.linspace(0, n - 1, 8).astype(int)
     ref = A.reshape(n, n)[rows].astype(np.float64) @ B.reshape(n, n).astype(np.float64)
     err = float(np.abs(C[rows] - ref).max() / np.abs(ref).max())
-    # warm-up right before the timed launches: the GPU clock climbs from idle over tens of
-    # milliseconds, and a host-side pause between warm-up and timing would let it fall again
+    # clock settling, then the counted warm-up right before the timed launches: the GPU clock
+    # climbs from idle over tens of milliseconds, and a host-side pause between warm-up and
+    # timing would let it fall again
+    settle = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(20):
+            run()
+        sgpu.synchronize()
+        settle += 20
     ev = sgpu.Events()
     for _ in range(warmup):
         run()
@@ -67,27 +108,45 @@ def bench_sgemm(n, steps, warmup):
     sgpu.synchronize()
     wall = time.perf_counter() - t0
     kernel_ms = ev.elapsed_ms() / steps
+    # steady state beside it: a longer event-timed loop straight after the timed steps
+    ev.record_start(None)
+    for _ in range(steady_launches):
+        run()
+    ev.record_stop(None)
+    sgpu.synchronize()
+    steady_ms = ev.elapsed_ms() / steady_launches
     flops = 2.0 * n * n * n
-    return dict(wall_s=wall, kernel_ms=kernel_ms, flops=flops, err=err)
+    return dict(wall_s=wall, kernel_ms=kernel_ms, flops=flops, err=err, settle_launches=settle, settle_s=settle_s,
+                steady_ms=steady_ms, steady_launches=steady_launches)
 
 
-def bench_gemv_lm_head(reps=100, copies=4, warm=1000):
+def flush_subnormal_f16(codes):
+    """float64 values of fp16 codes with the h2f contract's flush of subnormals to 0."""
+    v = np.asarray(codes, np.uint16).view(np.float16).astype(np.float64)
+    v[np.abs(v) < 2.0 ** -14] = 0.0
+    return v
+
+
+def bench_gemv_lm_head(reps=100, copies=4, warm=1000, x16=False):
+    """The lm_head GEMV [151936 x 896], fp16 weights: sgpu_gemv_h (fp32 x) or, with x16,
+    sgpu_gemv_hh (fp16 x)."""
     N, K = 151936, 896
     Wf, s = sgpu.gen_normal(N * K, 42, 0.0, 0.02)
     W = sgpu.f32_to_f16(Wf)
     del Wf
     x, _ = sgpu.gen_normal(K, s, 0.0, 1.0)
+    xin = sgpu.f32_to_f16(x) if x16 else x
     dWs = [sgpu.DeviceArray.from_host(W) for _ in range(copies)]
-    dx, dy = sgpu.DeviceArray.from_host(x), sgpu.DeviceArray(N)
-    run = lambda i: sgpu.call("sgpu_gemv_h", dWs[i % copies].ptr, dx.ptr, None, dy.ptr, K, N, None)
+    dx, dy = sgpu.DeviceArray.from_host(xin), sgpu.DeviceArray(N)
+    fn = "sgpu_gemv_hh" if x16 else "sgpu_gemv_h"
+    run = lambda i: sgpu.call(fn, dWs[i % copies].ptr, dx.ptr, None, dy.ptr, K, N, None)
     for i in range(copies * 2):
         run(i)
     sgpu.synchronize()
     y = dy.to_host()
     rows = np.arange(0, N, 997)
-    Wd = W.reshape(N, K)[rows].view(np.float16).astype(np.float64)
-    Wd[np.abs(Wd) < 2.0 ** -14] = 0.0          # the h2f contract flushes fp16 subnormals
-    ref = Wd @ x.astype(np.float64)
+    Wd = flush_subnormal_f16(W.reshape(N, K)[rows])        # the h2f contract flushes fp16 subnormals
+    ref = Wd @ (flush_subnormal_f16(xin) if x16 else x.astype(np.float64))
     err = float(np.abs(y[rows] - ref).max() / np.abs(ref).max())
     ev = sgpu.Events()
     for i in range(warm):                      # ~45 ms: clocks to steady state, then timed
@@ -98,8 +157,10 @@ def bench_gemv_lm_head(reps=100, copies=4, warm=1000):
         run(i)
     ev.record_stop(None)
     us = ev.elapsed_ms() * 1e3 / (reps * copies)
-    algo_bytes = 2.0 * N * K + 4.0 * K + 4.0 * N
-    return dict(us=us, bytes=algo_bytes, gbps=algo_bytes / (us * 1e-6) / 1e9, err=err, copies=copies)
+    algo_bytes = 2.0 * N * K + (2.0 if x16 else 4.0) * K + 4.0 * N
+    for d in dWs + [dx, dy]:
+        d.close()
+    return dict(us=us, bytes=algo_bytes, gbps=algo_bytes / (us * 1e-6) / 1e9, err=err, copies=copies, W=W, x=x)
 
 
 SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
@@ -108,7 +169,9 @@ GEMV_SHAPES = [("fp32", "gpt2 qkv", 2304, 768), ("fp32", "gpt2 attn-out", 768, 7
                ("fp32", "gpt2 proj", 768, 3072), ("fp32", "gpt2 lm_head", 50257, 768),
                ("fp16", "qwen q", 896, 896), ("fp16", "qwen k/v", 128, 896), ("fp16", "qwen o", 896, 896),
                ("fp16", "qwen gate/up", 4864, 896), ("fp16", "qwen down", 896, 4864),
-               ("fp16", "qwen lm_head", 151936, 896)]
+               ("fp16", "qwen lm_head", 151936, 896), ("fp16", "qwen qkv fused +bias", 1152, 896),
+               ("fp16", "qwen gate|up fused", 9728, 896)]
+GEMV_SHAPES += [("fp16x", name, N, K) for wt, name, N, K in GEMV_SHAPES if wt == "fp16"]
 ROTATE_BYTES = 600e6     # weight copies rotated per shape, up to 64: past the 256 MB MALL where that fits
 
 
@@ -167,34 +230,41 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True):
 
 def bench_gemv_shapes(reps=50, warm=100):
     """The per-projection GEMV shapes of both decoders: GPT-2 fp32 through sgpu_gemv_warp_b
-    (zero bias, the engine's call), Qwen fp16 through sgpu_gemv_h.  Weights N(0, 0.02), x N(0, 1);
-    copies of W are rotated so consecutive launches read different memory."""
+    (zero bias, the engine's call), Qwen fp16 through sgpu_gemv_h (fp32 x; the fused qkv shape
+    with its bias) and through sgpu_gemv_hh (fp16 x, rows "fp16x").  Weights N(0, 0.02),
+    x N(0, 1); copies of W are rotated so consecutive launches read different memory."""
     out = []
     st = 7
     for wt, name, N, K in GEMV_SHAPES:
         Wf, st = sgpu.gen_normal(N * K, st, 0.0, 0.02)
         x, st = sgpu.gen_normal(K, st, 0.0, 1.0)
-        W = sgpu.f32_to_f16(Wf) if wt == "fp16" else Wf
+        half = wt in ("fp16", "fp16x")
+        W = sgpu.f32_to_f16(Wf) if half else Wf
         del Wf
+        xin = sgpu.f32_to_f16(x) if wt == "fp16x" else x
+        with_bias = "+bias" in name
+        bias = sgpu.gen_normal(N, st, 0.0, 0.02)[0] if with_bias else None
         wbytes = W.nbytes
         copies = int(max(2, min(64, np.ceil(ROTATE_BYTES / wbytes))))
         dWs = [sgpu.DeviceArray.from_host(W) for _ in range(copies)]
-        dx, dy = sgpu.DeviceArray.from_host(x), sgpu.DeviceArray(N)
-        dz = sgpu.DeviceArray.from_host(np.zeros(N, np.float32)) if wt == "fp32" else None
+        dx, dy = sgpu.DeviceArray.from_host(xin), sgpu.DeviceArray(N)
+        dz = sgpu.DeviceArray.from_host(np.zeros(N, np.float32) if bias is None else bias) \
+            if (wt == "fp32" or with_bias) else None
         if wt == "fp32":
             run = lambda i, st=None: sgpu.call("sgpu_gemv_warp_b", dWs[i % copies].ptr, dx.ptr, dz.ptr, dy.ptr,
                                                K, N, st)
         else:
-            run = lambda i, st=None: sgpu.call("sgpu_gemv_h", dWs[i % copies].ptr, dx.ptr, None, dy.ptr, K, N, st)
+            fn = "sgpu_gemv_hh" if wt == "fp16x" else "sgpu_gemv_h"
+            run = lambda i, st=None, fn=fn: sgpu.call(fn, dWs[i % copies].ptr, dx.ptr, dz.ptr if dz else None,
+                                                      dy.ptr, K, N, st)
         run(0)
         sgpu.synchronize()
         y = dy.to_host()
         rows = np.arange(0, N, max(1, N // 64))
-        Wd = (W.reshape(N, K)[rows].view(np.float16).astype(np.float64) if wt == "fp16"
-              else W.reshape(N, K)[rows].astype(np.float64))
-        if wt == "fp16":
-            Wd[np.abs(Wd) < 2.0 ** -14] = 0.0     # the h2f contract flushes fp16 subnormals
-        ref = Wd @ x.astype(np.float64)
+        Wd = flush_subnormal_f16(W.reshape(N, K)[rows]) if half else W.reshape(N, K)[rows].astype(np.float64)
+        ref = Wd @ (flush_subnormal_f16(xin) if wt == "fp16x" else x.astype(np.float64))
+        if bias is not None:
+            ref = ref + bias[rows].astype(np.float64)
         err = float(np.abs(y[rows] - ref).max() / np.abs(ref).max())
         ev = sgpu.Events()
         for i in range(warm):
@@ -218,9 +288,10 @@ def bench_gemv_shapes(reps=50, warm=100):
         us_g = ev.elapsed_ms() * 1e3 / (reps * copies)
         g.close()
         strm.close()
-        algo = wbytes + 4.0 * K + 4.0 * N + (4.0 * N if wt == "fp32" else 0.0)
+        algo = wbytes + (2.0 if wt == "fp16x" else 4.0) * K + 4.0 * N + (4.0 * N if dz is not None else 0.0)
         gbps = algo / (us_g * 1e-6) / 1e9
-        out.append({"shape": [N, K], "name": name, "weights": wt, "us_in_graph": round(us_g, 3),
+        out.append({"shape": [N, K], "name": name, "weights": "fp16" if half else "fp32",
+                    "x": "fp16" if wt == "fp16x" else "fp32", "us_in_graph": round(us_g, 3),
                     "us_host_loop": round(us, 3), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
                     "rotated_mb": round(copies * wbytes / 1e6, 1), "normwise_err": err})
         for d in dWs + [dx, dy] + ([dz] if dz is not None else []):
@@ -241,12 +312,14 @@ def host_loop_tok_s(eng, ids, gen):
     return gen / (time.perf_counter() - t0)
 
 
-def bench_decode(prompt_len=32, gen=128, path=sgpu.QWEN_PATH_GRAPH, compare=True):
+def bench_decode(prompt_len=32, gen=128, path=sgpu.QWEN_PATH_GRAPH, compare=True, keep_blob=False):
     cfg = sgpu.qwen_default_cfg()
     t = time.perf_counter()
     blob = sgpu.qwen_random_blob(cfg, seed=2024, std=0.02)
     eng = sgpu.QwenEngine(cfg, blob, path)
-    del blob
+    if not keep_blob:
+        del blob
+        blob = None
     log(f"decode: weights built and uploaded in {time.perf_counter() - t:.1f} s")
     ids = [int(v) for v in np.random.default_rng(32).integers(0, cfg.V, prompt_len)]
     eng.generate(ids, 4)                      # captures the graphs
@@ -271,7 +344,8 @@ def bench_decode(prompt_len=32, gen=128, path=sgpu.QWEN_PATH_GRAPH, compare=True
     tps = gen / dt
     return dict(tok_s=tps, ms_per_tok=dt / gen * 1e3, bytes_per_token=bytes_tok,
                 hbm_floor_frac=bytes_tok * tps / (PEAK_HBM_GBPS * 1e9), prompt=prompt_len, generated=gen,
-                prefill_ms=t_prefill * 1e3, host_loop_graph=host_graph, host_loop_reference=host_ref)
+                prefill_ms=t_prefill * 1e3, host_loop_graph=host_graph, host_loop_reference=host_ref,
+                cfg=cfg, blob=blob, ids=ids)
 
 
 def bench_gpt2_decode(prompt_len=8, gen=128):
@@ -299,11 +373,64 @@ def bench_gpt2_decode(prompt_len=8, gen=128):
                 prefill_ms=t_prefill * 1e3)
 
 
-def cpu_baseline(n, target_s=1.5):
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    return oracle
+
+
+def cpu_gemv_baseline(W, x, reps=3):
+    """og_gemv_h (cpu_gemv_h, qwen_engine.c:276-284, serial k order per row) on the lm_head
+    [151936 x 896], row-parallel over the host threads (best of `reps`) and on one thread."""
+    oracle = _oracle()
+    N, K = 151936, 896
+    threads = cpu_threads()
+    algo = 2.0 * N * K + 4.0 * K + 4.0 * N
+    best = 1e9
+    for _ in range(reps):
+        t = time.perf_counter()
+        oracle.gemv_h(W, x, None, K, N, threads)
+        best = min(best, time.perf_counter() - t)
+    t = time.perf_counter()
+    oracle.gemv_h(W, x, None, K, N, 1)
+    t1 = time.perf_counter() - t
+    return dict(value=round(algo / best / 1e9, 2), unit="GB/s", cores=threads, kind="port",
+                sample=f"oracle og_gemv_h on the whole lm_head [151936 x 896] fp16 weights (the GPU leg's W and x), "
+                       f"best of {reps} on {threads} threads: {best * 1e3:.1f} ms",
+                single_thread={"value": round(algo / t1 / 1e9, 3), "unit": "GB/s", "ms": round(t1 * 1e3, 1)},
+                **host_info())
+
+
+def cpu_decode_baseline(cfg, blob, ids, tokens=4, single_tokens=2):
+    """og_qwen_forward (cpu_forward, qwen_engine.c:292-358) on the bench's random-init model:
+    positions 0..tokens-1 of the bench prompt, row-parallel GEMVs over the host threads; then
+    positions 0..single_tokens-1 again on one thread.  tok/s over those positions."""
+    oracle = _oracle()
+    ocfg = oracle.qwen_cfg(cfg.V, cfg.C, cfg.NL, cfg.NH, cfg.NKV, cfg.HD, cfg.FC, cfg.CTX, cfg.eps, cfg.theta)
+    threads = cpu_threads()
+    g = oracle.QwenGolden(ocfg, blob, nthreads=threads)
+    t = time.perf_counter()
+    for p in range(tokens):
+        g.forward(ids[p], p, want_logits=True)
+    dt = time.perf_counter() - t
+    g1 = oracle.QwenGolden(ocfg, blob, nthreads=1)
+    t = time.perf_counter()
+    for p in range(single_tokens):
+        g1.forward(ids[p], p, want_logits=True)
+    dt1 = time.perf_counter() - t
+    return dict(value=round(tokens / dt, 3), unit="tok/s", cores=threads, kind="port",
+                sample=f"oracle og_qwen_forward, positions 0..{tokens - 1} of the bench's 32-id prompt on the same "
+                       f"random-init Qwen2.5-0.5B-architecture weights, logits every position, {threads} threads: "
+                       f"{dt:.2f} s",
+                single_thread={"value": round(single_tokens / dt1, 3), "unit": "tok/s", "tokens": single_tokens,
+                               "s": round(dt1, 2)},
+                **host_info())
+
+
+def cpu_baseline(n, target_s=1.5):
+    oracle = _oracle()
+    threads = cpu_threads()
     A, B = sgpu.gen_sgemm_inputs(n * n, 42)
     rows = threads
     t = time.perf_counter()
@@ -318,13 +445,14 @@ def cpu_baseline(n, target_s=1.5):
     tflops = 2.0 * rows * n * n / dt / 1e12
     return dict(value=tflops, unit="TFLOP/s", cores=threads, kind="port",
                 sample=f"oracle og_sgemm_rows (serial k-order fp32, -O2 -ffp-contract=off), rows 0..{rows - 1} "
-                       f"of the {n}^3 SGEMM ({2.0 * rows * n * n / 1e9:.1f} GFLOP), {dt:.2f} s on {threads} threads")
+                       f"of the {n}^3 SGEMM ({2.0 * rows * n * n / 1e9:.1f} GFLOP), {dt:.2f} s on {threads} threads",
+                **host_info())
 
 
 def pmc_probe():
     """One launch each of: add2 over 64 Mi floats (a plain elementwise kernel whose HBM
-    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration) and the lm_head
-    gemv_h, and ten back-to-back launches of sgpu_sgemm_opt 4096^3 (sgemm_opt256; per-dispatch
+    traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), the lm_head
+    gemv_h and gemv_hh, and ten back-to-back launches of sgpu_sgemm_opt 4096^3 (sgemm_opt256; per-dispatch
     counters are averaged).  Run under `rocprofv3 --pmc FETCH_SIZE`, again with WRITE_SIZE,
     and with the MFMA-busy counters; prints the algorithmic bytes of each launch as one JSON
     line."""
@@ -353,9 +481,15 @@ def pmc_probe():
     sgpu.synchronize()
     sgpu.call("sgpu_gemv_h", dW.ptr, dx.ptr, None, dy.ptr, K, N, None)
     sgpu.synchronize()
+    dxh = sgpu.DeviceArray(K, np.uint16)
+    dxh.fill_bytes(0)
+    sgpu.synchronize()
+    sgpu.call("sgpu_gemv_hh", dW.ptr, dxh.ptr, None, dy.ptr, K, N, None)
+    sgpu.synchronize()
     print(json.dumps({"add2_read": 2 * 4 * n, "add2_write": 4 * n,
                       "sgemm_read_min": 2 * 4 * N4 * N4, "sgemm_write": 4 * N4 * N4,
-                      "gemv_h_read": 2 * N * K + 4 * K, "gemv_h_write": 4 * N}), flush=True)
+                      "gemv_h_read": 2 * N * K + 4 * K, "gemv_h_write": 4 * N,
+                      "gemv_hh_read": 2 * N * K + 2 * K, "gemv_hh_write": 4 * N}), flush=True)
 
 
 def main():
@@ -410,20 +544,35 @@ def main():
     achieved = sg["flops"] / (sg["kernel_ms"] * 1e-3) / 1e12
     log(f"sgpu_sgemm_opt {n}^3: {sg['kernel_ms']:.3f} ms/launch, {achieved:.1f} TFLOP/s kernel, "
         f"{tflops:.1f} TFLOP/s wall, normwise err {sg['err']:.2e}")
+    log(f"sgemm steady state: {sg['steady_ms']:.3f} ms/launch over {sg['steady_launches']} launches "
+        f"({sg['flops'] / (sg['steady_ms'] * 1e-3) / 1e12:.1f} TFLOP/s); clock settling {sg['settle_launches']} launches")
     gv = bench_gemv_lm_head()
     log(f"gemv_h lm_head: {gv['us']:.1f} us, {gv['gbps']:.0f} GB/s ({gv['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), "
         f"err {gv['err']:.2e}")
+    gvh = bench_gemv_lm_head(x16=True)
+    log(f"gemv_hh lm_head (fp16 x): {gvh['us']:.1f} us, {gvh['gbps']:.0f} GB/s "
+        f"({gvh['gbps'] / PEAK_HBM_GBPS:.1%} of HBM), err {gvh['err']:.2e}")
+    cpu_gv = None if args.no_cpu else cpu_gemv_baseline(gv["W"], gv["x"])
+    if cpu_gv:
+        log(f"cpu gemv_h lm_head: {cpu_gv['value']} GB/s on {cpu_gv['cores']} threads, "
+            f"{cpu_gv['single_thread']['value']} GB/s on one")
+    del gv["W"], gv["x"], gvh["W"], gvh["x"]
     sweep = gshapes = None
     if not args.no_sweep:
         sweep = bench_sgemm_sweep()
         log("sgemm sweep (in-graph): " + ", ".join(f"{r['M']}x{r['N']}x{r['K']} {r['tflops']:.1f} TF" for r in sweep))
         gshapes = bench_gemv_shapes()
         log("gemv shapes (in-graph): " + ", ".join(f"{r['name']} {r['us_in_graph']:.2f} us" for r in gshapes))
-    dec = g2 = None
+    dec = g2 = cpu_dec = None
     if not args.no_decode:
-        dec = bench_decode()
+        dec = bench_decode(keep_blob=not args.no_cpu)
         log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['ms_per_tok']:.3f} ms/token, "
             f"{dec['hbm_floor_frac']:.1%} of the HBM floor)")
+        if dec["blob"] is not None:
+            cpu_dec = cpu_decode_baseline(dec["cfg"], dec["blob"], dec["ids"])
+            log(f"cpu decode: {cpu_dec['value']} tok/s on {cpu_dec['cores']} threads, "
+                f"{cpu_dec['single_thread']['value']} tok/s on one")
+        dec["blob"] = None
         g2 = bench_gpt2_decode()
         log(f"gpt2 decode: {g2['tok_s']:.1f} tok/s ({g2['ms_per_tok']:.3f} ms/token, "
             f"{g2['hbm_floor_frac']:.1%} of the HBM floor)")
@@ -452,12 +601,22 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),
                      "traffic": traffic.get("sgemm_opt256_4096")},
         "cpu_baseline": cpu,
+        "steady_state": {"kernel_ms": round(sg["steady_ms"], 4), "launches": sg["steady_launches"],
+                         "tflops": round(sg["flops"] / (sg["steady_ms"] * 1e-3) / 1e12, 3),
+                         "frac": round(sg["flops"] / (sg["steady_ms"] * 1e-3) / 1e12 / PEAK_FP32_MATRIX_TFLOPS, 4),
+                         "clock_settle_s": sg["settle_s"], "clock_settle_launches": sg["settle_launches"]},
         "gemv": {"kernel": "gemv_h (fp16 weights, fp32 x/y)", "shape": [151936, 896],
                  "us_per_call": round(gv["us"], 3), "gbps": round(gv["gbps"], 1),
                  "roofline": {"bound": "hbm", "achieved": round(gv["gbps"], 1), "peak": PEAK_HBM_GBPS,
                               "unit": "GB/s", "frac": round(gv["gbps"] / PEAK_HBM_GBPS, 4),
                               "traffic": traffic.get("gemv_h_lm_head")},
-                 "weight_copies_rotated": gv["copies"], "normwise_err": gv["err"]},
+                 "weight_copies_rotated": gv["copies"], "normwise_err": gv["err"], "cpu_baseline": cpu_gv},
+        "gemv_hh": {"kernel": "gemv_hh (fp16 weights, fp16 x, fp32 y)", "shape": [151936, 896],
+                    "us_per_call": round(gvh["us"], 3), "gbps": round(gvh["gbps"], 1),
+                    "roofline": {"bound": "hbm", "achieved": round(gvh["gbps"], 1), "peak": PEAK_HBM_GBPS,
+                                 "unit": "GB/s", "frac": round(gvh["gbps"] / PEAK_HBM_GBPS, 4),
+                                 "traffic": traffic.get("gemv_hh_lm_head")},
+                    "weight_copies_rotated": gvh["copies"], "normwise_err": gvh["err"]},
         "sgemm_sweep": sweep,
         "gemv_shapes": gshapes,
         "decode": None if dec is None else {
@@ -468,7 +627,8 @@ def main():
             "path": "fused kernels (5 per layer) replayed as a HIP graph, greedy argmax on the device",
             "prefill_ms": round(dec["prefill_ms"], 3),
             "tok_s_host_argmax_loop": round(dec["host_loop_graph"], 2),
-            "tok_s_reference_launch_sequence": round(dec["host_loop_reference"], 2)},
+            "tok_s_reference_launch_sequence": round(dec["host_loop_reference"], 2),
+            "cpu_baseline": cpu_dec},
         "gpt2_decode": None if g2 is None else {
             "model": "GPT-2 124M architecture, random-init fp32 weights ((frand()-0.5)*0.06)",
             "tok_s": round(g2["tok_s"], 2), "ms_per_token": round(g2["ms_per_tok"], 4),
@@ -477,6 +637,7 @@ def main():
             "path": "fused kernels (5 per layer) replayed as a HIP graph, greedy argmax on the device"},
         "sgemm_normwise_err": sg["err"],
         "device": props.name.decode(),
+        "host": host_info(),
     }
     print(json.dumps(out), flush=True)
 

@@ -8,8 +8,8 @@
 // Two shapes of kernel:
 //  * gemv_generic: a wave per row, lanes striding the row in 16-byte segments, x read
 //    through the vector L1.  Any K, any pointer alignment (scalar path when a row is not
-//    16-byte aligned), any grid (wave-granular grid-stride).  Backs the reference-named
-//    symbols so hosts that keep the reference's own launch geometry stay correct.
+//    16-byte aligned), any grid (wave-granular grid-stride).  The reference-named symbols
+//    (gemv_byname) fall back to it when the team kernel below cannot run.
 //  * gemv_xreg<LPR, S>: a team of LPR lanes per row (16, 64 or 256 = four waves split-K),
 //    each lane owning up to S fixed 16-byte segments of every row.  The lane's slice of x
 //    (S*VEC floats) is loaded once into VGPRs and reused for every row of a persistent
@@ -134,7 +134,18 @@ __device__ __forceinline__ void gemv_generic(const typename WT::elem* __restrict
         if (vec_ok) {
             const vec* rv = reinterpret_cast<const vec*>(row);
             int s = lane;
-            for (; s + 64 < nseg; s += 128) {         // two segments in flight per lane
+            for (; s + 192 < nseg; s += 256) {        // four segments in flight per lane
+                vec w[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) w[u] = sgpu_ldnt(rv + s + 64 * u);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    float xa[VEC];
+                    x_seg<VEC>(x, s + 64 * u, xa);
+                    acc = WT::dot(w[u], xa, acc);
+                }
+            }
+            for (; s + 64 < nseg; s += 128) {         // two
                 const vec w0 = sgpu_ldnt(rv + s), w1 = sgpu_ldnt(rv + s + 64);
                 float xa[VEC], xb[VEC];
                 x_seg<VEC>(x, s, xa);
@@ -201,20 +212,37 @@ struct XPlain {
     __device__ __forceinline__ void prepare(float (&)[S][VEC], const bool (&)[S], int, int, float*) {}
 };
 
-// x given as fp16 bit patterns (the fp16-x GEMV): each lane decodes its slice once into its
-// registers with the exact reference h2f (integer decode: subnormal codes +0, exponent-31
-// codes finite), so every dot product sees the operands gemv_h sees for x = h2f(x16).
-// load4(k) needs k % 4 == 0 and x 8-byte aligned.
+// x given as fp16 bit patterns (the fp16-x GEMV): each lane converts its slice once into its
+// registers with the hardware conversion, as the weights are converted (the code objects run
+// with fp16 denormals flushed: subnormal codes read as +-0, which sums exactly as the
+// reference's +0 does, since a running sum that starts at +0 never becomes -0).  Exponent-31
+// codes convert to inf/NaN instead of the reference's finite 2^16 (1 + m/1024), which makes
+// every row sum non-finite, and those rows are recomputed with the exact decode (at()).  So
+// every sum equals gemv_h's for x = h2f(x16).  load4(k) returns the four raw codes at k as two
+// dwords (slots 0, 1) and prepare() converts them after the whole slice is loaded: converting
+// inside each load made the compiler wait for every load in turn.  load4 needs k % 4 == 0 and
+// x 8-byte aligned.
 struct XHalf {
     const uint16_t* x;
     __device__ __forceinline__ sgpu_f32x4 load4(int k) const {
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         const u32x2 h = *reinterpret_cast<const u32x2*>(x + k);
-        return sgpu_f32x4{sgpu_h2f_lo(h[0]), sgpu_h2f_hi(h[0]), sgpu_h2f_lo(h[1]), sgpu_h2f_hi(h[1])};
+        return sgpu_f32x4{__uint_as_float(h[0]), __uint_as_float(h[1]), 0.0f, 0.0f};
     }
     __device__ __forceinline__ float at(int k) const { return sgpu_h2f(x[k]); }
     template <int LPR, int S, int VEC>
-    __device__ __forceinline__ void prepare(float (&)[S][VEC], const bool (&)[S], int, int, float*) {}
+    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const bool (&)[S], int, int, float*) {
+#pragma unroll
+        for (int j = 0; j < S; j++)
+#pragma unroll
+            for (int q = 0; q < VEC / 4; q++) {
+                const uint32_t u0 = __float_as_uint(xr[j][4 * q]), u1 = __float_as_uint(xr[j][4 * q + 1]);
+                xr[j][4 * q] = WF16::cvt(u0 & 0xffffu);         // zero codes (no segment) stay +0
+                xr[j][4 * q + 1] = WF16::cvt(u0 >> 16);
+                xr[j][4 * q + 2] = WF16::cvt(u1 & 0xffffu);
+                xr[j][4 * q + 3] = WF16::cvt(u1 >> 16);
+            }
+    }
 };
 
 // x'[k] = x[k] * inv * h2f(w[k]), inv = 1 / sqrt(mean(x^2) + eps): cpu_rms (qwen_engine.c:285-290)
@@ -335,9 +363,11 @@ __device__ __noinline__ float recompute_row_x(const typename WT::elem* __restric
     return acc;
 }
 
+// nblk: the blocks that take part (blocks 0..nblk-1 walk the row blocks with stride nblk; any
+// others return at once); 0 means the whole grid.
 template <class WT, int LPR, int S, int NR, class Pro, class Map, class Epi>
 __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ W, int K, int nteams, Pro pro,
-                                          Map map, Epi epi) {
+                                          Map map, Epi epi, int nblk = 0) {
     static_assert(LPR == 16 || LPR == 32 || LPR == 64 || LPR == 128 || LPR == 256, "team size");
     static_assert(NR == 1 || LPR <= 64, "multi-row teams must fit in one wave");
     typedef typename WT::vec vec;
@@ -377,6 +407,8 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
             epi.load(t, rows, pre);
         }
     };
+    const int nb = nblk > 0 ? nblk : (int)gridDim.x;
+    if ((int)blockIdx.x >= nb) return;                // block-uniform
     int rb = blockIdx.x;
     if (rb * TEAMS < nteams) fetch(rb);
 
@@ -394,7 +426,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
     }
     pro.template prepare<LPR, S, VEC>(xr, has, sub, K, red);
 
-    for (; rb * TEAMS < nteams; rb += gridDim.x) {    // block-uniform loop
+    for (; rb * TEAMS < nteams; rb += nb) {           // block-uniform loop
         const int t = rb * TEAMS + team;
         const bool cur_valid = valid;
         const typename Epi::Pre cur_pre = pre;
@@ -412,7 +444,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
                 for (int j = 0; j < S; j++)
                     if (has[j]) acc[r] = WT::dot(w[r][j], xr[j], acc[r]);
         }
-        if ((rb + (int)gridDim.x) * TEAMS < nteams) fetch(rb + gridDim.x);
+        if ((rb + nb) * TEAMS < nteams) fetch(rb + nb);
         if constexpr (LPR <= 64) {
 #pragma unroll
             for (int r = 0; r < NR; r++) acc[r] = sgpu_group_sum<LPR>(acc[r]);
@@ -451,6 +483,43 @@ template <int LPR, int S>
 __device__ __forceinline__ void gemv_xreg_hh(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
                                              const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
     gemv_team<WF16, LPR, S, 1>(W, K, N, XHalf{x}, MapRows{}, EpiStore{bias, y});
+}
+
+// The x source of the team GEMV for fp32 or fp16-bit x.
+__device__ __forceinline__ XPlain x_source(const float* x) { return XPlain{x}; }
+__device__ __forceinline__ XHalf x_source(const uint16_t* x) { return XHalf{x}; }
+
+// Body of the reference-named GEMV symbols (gemv, gemv4, gemv_warp, gemv_warp_b, gemv_h,
+// gemv_hh), which hosts launch by name with their own geometry -- (N+7)/8 or (N+255)/256
+// blocks of 256 in the reference callers.  When the launch has 1-D blocks of 256 threads and
+// 16-byte aligned rows, with at least one block per 8 rows, it runs the team GEMV on at most
+// kByNameBlocks blocks (a persistent
+// grid: those blocks walk the row blocks with the next one's weights in flight, surplus blocks
+// exit), with a team shape sized to the decoder rows: fp32 16 lanes x 12 segments (K <= 768),
+// 64 x 16 (K <= 4096); fp16 16 x 7 (K <= 896), 64 x 10 (K <= 5120); 256 x 8 beyond, up to 2048
+// segments.  Other launches (unaligned rows, other block shapes, longer rows) take the
+// wave-per-row kernel.  The choice is block-uniform.
+constexpr int kByNameBlocks = 2048;      // 8 per CU on MI355X's 256 CUs
+template <class WT, class XT>
+__device__ __forceinline__ void gemv_byname(const typename WT::elem* __restrict__ W, const XT* __restrict__ x,
+                                            const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
+    constexpr int VEC = WT::VEC;
+    constexpr bool H = VEC == 8;
+    // a grid of one thread per row or fewer ((N+255)/256 blocks, gemv_test.c:108) keeps a wave
+    // per row: with so few waves the team kernel's one row block in flight per block is slower
+    const bool team = blockDim.x == 256 && blockDim.y == 1 && blockDim.z == 1 && gridDim.y == 1 &&
+                      gridDim.z == 1 && K > 0 && K % VEC == 0 && ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0 &&
+                      (long long)gridDim.x * 8 >= N;
+    const int nseg = K / VEC, nb = min((int)gridDim.x, kByNameBlocks);
+    constexpr int S16 = H ? 7 : 12, S64 = H ? 10 : 16;
+    if (team && nseg <= 16 * S16)
+        gemv_team<WT, 16, S16, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
+    else if (team && nseg <= 64 * S64)
+        gemv_team<WT, 64, S64, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
+    else if (team && nseg <= 256 * 8)
+        gemv_team<WT, 256, 8, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
+    else
+        gemv_generic<WT, XT>(W, x, bias, y, K, N);
 }
 
 // ---------------------------------------------------------------------------------------

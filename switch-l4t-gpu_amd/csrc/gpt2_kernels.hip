@@ -37,14 +37,14 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 extern "C" {
 
-__global__ void gemv_warp(const float* __restrict__ W, const float* __restrict__ x, float* __restrict__ y,
+__global__ void __launch_bounds__(256) gemv_warp(const float* __restrict__ W, const float* __restrict__ x, float* __restrict__ y,
                           int K, int N) {
-    sgpu::gemv_generic<sgpu::WF32>(W, x, nullptr, y, K, N);
+    sgpu::gemv_byname<sgpu::WF32, float>(W, x, nullptr, y, K, N);
 }
 
-__global__ void gemv_warp_b(const float* __restrict__ W, const float* __restrict__ x,
+__global__ void __launch_bounds__(256) gemv_warp_b(const float* __restrict__ W, const float* __restrict__ x,
                             const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
-    sgpu::gemv_generic<sgpu::WF32>(W, x, bias, y, K, N);
+    sgpu::gemv_byname<sgpu::WF32, float>(W, x, bias, y, K, N);
 }
 
 // Matrix-core path (32-token x 32-row tiles) for whole-quad aligned rows, 256-thread blocks

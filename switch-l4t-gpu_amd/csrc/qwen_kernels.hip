@@ -14,7 +14,8 @@
 //   attn_softmax    (const float*scores, float*probs, int T, int NH)
 //   attn_mix_gqa    (const float*probs, const float*vc, float*out, int T, int NH, int KV, int HD)
 //   add2            (const float*a, const float*b, float*out, int n)
-// gemv_h takes any grid (see gemv_core.h).  The support kernels expect the geometry their
+// gemv_h / gemv_hh take any grid of blocks of up to 256 threads (gemv_core.h gemv_byname).
+// The support kernels expect the geometry their
 // launchers in the host library use (blocks of 256 threads; one wave per head for
 // attn_softmax).  Elementwise arithmetic is written with contraction off so it rounds like
 // the serial CPU golden; exp is the correctly-rounded-to-1-ulp device expf (the reference's
@@ -23,16 +24,16 @@
 
 extern "C" {
 
-__global__ void gemv_h(const uint16_t* __restrict__ W, const float* __restrict__ x,
+__global__ void __launch_bounds__(256) gemv_h(const uint16_t* __restrict__ W, const float* __restrict__ x,
                        const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
-    sgpu::gemv_generic<sgpu::WF16>(W, x, bias, y, K, N);
+    sgpu::gemv_byname<sgpu::WF16, float>(W, x, bias, y, K, N);
 }
 
 // y[n] = sum_k h2f(W[n*K+k]) * h2f(x[k]) + (bias ? bias[n] : 0): gemv_h's contract with x
 // stored as fp16 bits (half the x bytes; activations kept in fp16).  Any grid.
-__global__ void gemv_hh(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+__global__ void __launch_bounds__(256) gemv_hh(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
                         const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
-    sgpu::gemv_generic<sgpu::WF16, uint16_t>(W, x, bias, y, K, N);
+    sgpu::gemv_byname<sgpu::WF16, uint16_t>(W, x, bias, y, K, N);
 }
 
 // One block per row (grid = rows), blockDim a multiple of 64 (256 from the launcher).

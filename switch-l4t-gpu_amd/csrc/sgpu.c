@@ -263,6 +263,16 @@ int sgpu_get_device_props(int device, sgpu_device_props *props) {
     memset(props, 0, sizeof *props);
     snprintf(props->name, sizeof props->name, "%s", p.name);
     snprintf(props->arch, sizeof props->arch, "%.63s", p.gcnArchName);
+    if (!props->name[0] && (hipDeviceGetName(props->name, (int)sizeof props->name, device) != hipSuccess ||
+                            !props->name[0])) {
+        /* no marketing name from the driver (an empty name table on some hosts): name the
+         * device by its architecture and size instead of leaving the field empty */
+        char arch[64];
+        snprintf(arch, sizeof arch, "%s", props->arch);
+        arch[strcspn(arch, ":")] = 0;
+        snprintf(props->name, sizeof props->name, "AMD %s GPU, %d CUs", arch[0] ? arch : "(unknown arch)",
+                 p.multiProcessorCount);
+    }
     props->compute_units = p.multiProcessorCount;
     props->clock_khz = p.clockRate;
     props->memory_clock_khz = p.memoryClockRate;

@@ -265,7 +265,9 @@ int main(int argc, char **argv) {
             if (!ks[v].f) continue;
             printf(",\"%s\":[", keys[v]);
             for (int i = 0; i < 3; i++)
-                printf("%s{\"n\":%d,\"ms\":%.3f,\"gflops\":%.1f}", i ? "," : "", sizes[i], ms[v][i], gf[v][i]);
+                /* reference keys in the reference's %.1f; "us" (added) keeps the precision */
+                printf("%s{\"n\":%d,\"ms\":%.1f,\"gflops\":%.1f,\"us\":%.1f}", i ? "," : "", sizes[i], ms[v][i],
+                       gf[v][i], ms[v][i] * 1e3);
             printf("]");
         }
         if (ej) printf(",\"sgemm_extra\":[%s]", extra_json);
