@@ -74,6 +74,14 @@ static int verify(const float *A, const float *B, const float *C, int M, int N, 
     return bad;
 }
 
+/* A JSON string body: '"' and '\\' escaped, as the reference escapes the path (gpu_workload.c:224-227). */
+static void put_json_str(const char *p) {
+    for (; *p; p++) {
+        if (*p == '"' || *p == '\\') putchar('\\');
+        putchar(*p);
+    }
+}
+
 typedef struct { const char *name; hipFunction_t f; int ref_tile; } kern;
 
 static void launch(const kern *k, void *A, void *B, void *C, int M, int N, int K, int ref_geom) {
@@ -249,12 +257,14 @@ int main(int argc, char **argv) {
     }
 
     if (json_mode) {                                       /* schema of gpu_workload.c:222-251 */
+        sgpu_device_props props;
+        CHK(sgpu_get_device_props(0, &props));
+        char arch[64];
+        snprintf(arch, sizeof arch, "%s", props.arch);
+        arch[strcspn(arch, ":")] = 0;
         const char *path = co_path ? co_path : "(embedded switch_gpu)";
         printf("{\"ptx\":\"");
-        for (const char *p = path; *p; p++) {
-            if (*p == '"' || *p == '\\') putchar('\\');
-            putchar(*p);
-        }
+        put_json_str(path);
         printf("\",\"kernels\":{\"sgemm\":\"%s\"", v_sgemm ? v_sgemm : "NOT_RUN");
         if (v_naive) printf(",\"sgemm_naive\":\"%s\"", v_naive);
         if (v_tiled4) printf(",\"sgemm_tiled4\":\"%s\"", v_tiled4);
@@ -271,7 +281,12 @@ int main(int argc, char **argv) {
             printf("]");
         }
         if (ej) printf(",\"sgemm_extra\":[%s]", extra_json);
-        printf(",\"membw_gbps\":%.1f,\"membw_mb\":%ld,\"done\":true}\n", membw_gbs, membw_mb);
+        /* added keys: the buffer size, and the device, which selects a consumer's sanity bounds */
+        printf(",\"membw_gbps\":%.1f,\"membw_mb\":%ld,\"arch\":\"", membw_gbs, membw_mb);
+        put_json_str(arch);
+        printf("\",\"device\":\"");
+        put_json_str(props.name);
+        printf("\",\"done\":true}\n");
     } else {
         printf("WORKLOAD_DONE\n");
     }

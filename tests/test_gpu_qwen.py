@@ -5,7 +5,9 @@ qwen_engine.c:205-269) against the oracle's cpu_forward (og_qwen_forward).
 Bars: support kernels within fp32 rounding of float64 formulas; engine logits at every
 teacher-forced position within 1e-4 of the logit scale with the same argmax; full
 Qwen2.5-0.5B-architecture random-init model: greedy decode token-identical to the CPU golden
-for 64 tokens after a 32-token prompt."""
+for 64 tokens after a 32-token prompt (spec init, and a unit-norm-gain, projections-x2 variant whose greedy
+continuation does not cycle, 24+ distinct tokens), and 64 random ids teacher-forced with every position's logits
+within 1e-3 of scale and the same argmax (top-1/top-2 gaps printed)."""
 import json
 import os
 import subprocess
@@ -265,6 +267,149 @@ def test_engine_full_greedy_token_identical(gpu, og):
     assert len(tokens) == 96
     assert worst <= 1e-3
     say(f"greedy 64 tokens identical; min top-2 gap {min(gaps):.3e}, worst logit rel err {worst:.2e}")
+    eng.close()
+
+
+# ---- full-size parity that does not reduce to a few embeddings ----
+# With the spec's N(0, 0.02) RMSNorm gains every layer's contribution is scaled by ~0.02, the
+# residual stream is dominated by the current token's embedding, and greedy decoding falls
+# into a 2-token cycle (18885, 77186, 32852, 77186, ...).  Two checks avoid that: the spec model
+# teacher-forced over 64 seeded random ids (logits at every position), and a variant decoded
+# free-running: RMSNorm gains 1 + N(0, 0.02) and the four projection matrices (qkv, o, gate|up,
+# down) at twice the spec scale, so every layer mixes the history into the residual.
+# Measured on this model and prompt (GPU reference path against the CPU golden, 64 greedy
+# tokens): unit gains alone give 10 distinct tokens in 41 with long runs of one token;
+# projections x2, 64 of 64 with the logits within 1.8e-5 of scale and every top-1/top-2 gap at
+# least 16x the GPU/CPU difference.  Sharper variants amplify rounding differences through the
+# 24 layers: qkv x6 gives 63 distinct tokens but logits 2.2e-2 of scale apart.
+
+def full_cfgs(gpu, og):
+    c = gpu.qwen_default_cfg()
+    return c, og.qwen_cfg(c.V, c.C, c.NL, c.NH, c.NKV, c.HD, c.FC, c.CTX)
+
+
+def rich_variant(blob, c, seed=7, proj_scale=2.0):
+    """Every RMSNorm gain of the flat file set to fp16(1 + N(0, 0.02)), seeded, and the qkv, o,
+    gate|up and down weights multiplied by proj_scale (re-rounded to fp16): offsets of the
+    qwen_engine.c:61-75 layout -- embedding, RoPE tables, then per layer in_ln, qkv W, qkv b,
+    o W, post_ln, gate|up W, down W, then the final norm."""
+    h = blob.view(np.uint16)
+    qkv = c.C + 2 * c.NKV * c.HD
+    base = (c.V * c.C * 2 + 2 * c.CTX * (c.HD // 2) * 4) // 2
+    lstride = c.C + qkv * c.C + qkv + c.C * c.C + c.C + 2 * c.FC * c.C + c.C * c.FC
+    rng = np.random.default_rng(seed)
+    gain = lambda: (1.0 + 0.02 * rng.standard_normal(c.C)).astype(np.float16).view(np.uint16)
+
+    def scale(a, n):
+        w = h[a:a + n]
+        w[:] = (w.view(np.float16).astype(np.float32) * proj_scale).astype(np.float16).view(np.uint16)
+
+    for l in range(c.NL):
+        p = base + l * lstride
+        h[p:p + c.C] = gain()                          # input RMSNorm
+        p += c.C
+        scale(p, qkv * c.C)                            # qkv W
+        p += qkv * c.C + qkv
+        scale(p, c.C * c.C)                            # o W
+        p += c.C * c.C
+        h[p:p + c.C] = gain()                          # post-attention RMSNorm
+        p += c.C
+        scale(p, 2 * c.FC * c.C)                       # gate|up W
+        p += 2 * c.FC * c.C
+        scale(p, c.C * c.FC)                           # down W
+    e = base + c.NL * lstride
+    h[e:e + c.C] = gain()                              # final RMSNorm
+    return blob
+
+
+def check_position(p, got, ref, gaps, stats):
+    """Logits within 1e-3 of the logit scale; the argmax equal unless the reference's top two
+    are within 4x this position's largest difference (a near-tie; counted and printed)."""
+    err = np.abs(got - ref)
+    stats["worst"] = max(stats["worst"], float(err.max() / np.abs(ref).max()))
+    assert err.max() <= 1e-3 * np.abs(ref).max(), (p, float(err.max()), float(np.abs(ref).max()))
+    top2 = np.sort(ref)[-2:]
+    gaps.append(float(top2[1] - top2[0]))
+    g_tok, c_tok = int(np.argmax(got)), int(np.argmax(ref))
+    if g_tok != c_tok:
+        assert ref[c_tok] - ref[g_tok] <= 4 * float(err.max()), (p, g_tok, c_tok, gaps[-1])
+        stats["ties"] += 1
+    return g_tok
+
+
+@pytest.fixture(scope="module")
+def full_spec(gpu, og):
+    """The spec model (seed 2024, N(0, 0.02)) and the CPU golden's logits for 64 seeded random
+    ids fed one position at a time."""
+    c, oc = full_cfgs(gpu, og)
+    say("full spec model: building weights and 64 golden positions")
+    blob = gpu.qwen_random_blob(c, seed=2024, std=0.02)
+    ids = [int(v) for v in np.random.default_rng(64).integers(0, c.V, 64)]
+    gold = og.QwenGolden(oc, blob, NT)
+    logits = np.stack([gold.forward(t, p) for p, t in enumerate(ids)])
+    return c, blob, ids, logits
+
+
+@pytest.mark.parametrize("path", ["reference", "graph"])
+def test_engine_full_teacher_forced(gpu, full_spec, path):
+    """Full Qwen2.5-0.5B architecture (spec init), 64 random ids teacher-forced: the logits of
+    every position against the CPU golden (1e-3 of scale, argmax equal), on the reference
+    launch sequence and on the replayed graph."""
+    c, blob, ids, logits = full_spec
+    eng = gpu.QwenEngine(c, blob, PATHS[path])
+    gaps, stats = [], {"worst": 0.0, "ties": 0}
+    for p, t in enumerate(ids):
+        check_position(p, eng.forward(t, p, True).copy(), logits[p], gaps, stats)
+    eng.close()
+    say(f"{path}: 64 teacher-forced positions, worst logit error {stats['worst']:.2e} of scale, "
+        f"min top-1/top-2 gap {min(gaps):.3e}, median {np.median(gaps):.3e}, near-ties {stats['ties']}")
+    assert stats["ties"] <= 2
+
+
+@pytest.fixture(scope="module")
+def full_variant(gpu, og):
+    """The rich variant (unit RMSNorm gains, projections x2), 32-id prompt, and the CPU golden's own
+    greedy continuation of 64 tokens with the logits it took each one from."""
+    c, oc = full_cfgs(gpu, og)
+    say("full variant model: building weights and the golden's greedy run")
+    blob = rich_variant(gpu.qwen_random_blob(c, seed=2024, std=0.02), c)
+    prompt = [int(v) for v in np.random.default_rng(32).integers(0, c.V, 32)]
+    gold = og.QwenGolden(oc, blob, NT)
+    seq, logits = list(prompt), []
+    for p in range(32 + 64):
+        ref = gold.forward(seq[p], p, p >= 31)
+        if p >= 31:
+            logits.append(ref)
+            if len(seq) < 32 + 64 + 1:
+                seq.append(og.argmax(ref))
+    return c, blob, prompt, seq[32:], np.stack(logits)
+
+
+@pytest.mark.parametrize("path", ["reference", "graph"])
+def test_engine_full_variant_greedy(gpu, full_variant, path):
+    """Free-running greedy decode on the rich variant: 64 tokens token-identical to the CPU
+    golden's own greedy run, which does not cycle (at least 24 distinct tokens of 64).  The
+    reference path runs the host loop of the reference (logits to the host, argmax there,
+    each position's logits checked); the graph path runs sgpu_qwen_generate's on-device loop."""
+    c, blob, prompt, want, logits = full_variant
+    distinct = len(set(want[:64]))
+    say(f"golden greedy continuation: {want[:12]} ..., {distinct} distinct of 64")
+    assert distinct >= 24
+    eng = gpu.QwenEngine(c, blob, PATHS[path])
+    if path == "graph":
+        got = eng.generate(prompt, 64).tolist()
+        assert got == want[:65], next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
+    else:
+        gaps, stats = [], {"worst": 0.0, "ties": 0}
+        seq = list(prompt)
+        for p in range(32 + 64):
+            out = eng.forward(seq[p], p, p >= 31)
+            if p >= 31:
+                tok = check_position(p, out.copy(), logits[p - 31], gaps, stats)
+                assert tok == want[p - 31], (p, tok, want[p - 31])
+                seq.append(tok)
+        say(f"reference path: 64 greedy tokens identical, worst logit error {stats['worst']:.2e}, "
+            f"min top-1/top-2 gap {min(gaps):.3e}")
     eng.close()
 
 
