@@ -12,8 +12,9 @@
  *  - All buffer arguments are device pointers unless stated otherwise; sizes are element
  *    counts as in the reference kernels (ints, K before N in GEMV calls).  Sub-buffers
  *    are plain byte offsets from a device pointer.
- *  - The caller owns all memory; nothing here allocates except sgpu_malloc and the engine
- *    object (sgpu_qwen_*).  Outputs are fully overwritten (no accumulate-into-y/C).
+ *  - The caller owns all memory; nothing here allocates except sgpu_malloc, the engine
+ *    objects (sgpu_qwen_*, sgpu_gpt2_*) and the library's per-stream split-K workspaces (see
+ *    sgpu_sgemm_splitk).  Outputs are fully overwritten (no accumulate-into-y/C).
  *  - `stream` is a hipStream_t passed as void*; NULL is the default stream, as the
  *    reference's cuLaunchKernel(..., NULL, ...) calls use.  Launchers are asynchronous.
  *  - bias pointers are nullable wherever the reference kernel reads `bias ? bias[n] : 0`.
@@ -37,6 +38,8 @@ extern "C" {
 #define SGPU_ERR_NO_KERNEL (-3)      /* a code object lacks a kernel the call needs */
 #define SGPU_ERR_NO_DEVICE (-4)      /* no usable HIP device */
 #define SGPU_ERR_HOST_ALLOC (-5)     /* host memory exhausted */
+#define SGPU_ERR_NO_WORKSPACE (-6)   /* a split-K launch on a stream that has no workspace and cannot
+                                        get one now (being recorded, or 32 streams already hold one) */
 
 /* Replaces cuGetErrorString (cuda_drv.h:31).  Never NULL. */
 const char *sgpu_error_string(int status);
@@ -84,7 +87,7 @@ int sgpu_stream_synchronize(void *stream);
  * the default priority.  No reference counterpart (the reference launches one kernel per
  * host call). */
 int sgpu_stream_create(void **stream);
-int sgpu_stream_destroy(void *stream);
+int sgpu_stream_destroy(void *stream);              /* waits for the stream's work first */
 int sgpu_graph_begin(void *stream);                 /* stream must not be NULL */
 int sgpu_graph_end(void *stream, void **graph);     /* instantiated; *graph NULL on error */
 int sgpu_graph_launch(void *graph, void *stream);
@@ -134,11 +137,21 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 /* The sgemm_splitk member: 64x64 tiles with K split S ways (S >= 1; reduced so that every
  * split holds at least one 32-deep slice), each (tile, split) a block.  Every split writes its
- * partial tile to a library-owned per-device workspace (32 MB, allocated by sgpu_init) and the
- * last split of a tile sums all S partials in split order, so results do not depend on
- * arrival order.  Rejects problems needing more than 16384 tiles or S x tiles x 4096 floats
- * of workspace (SGPU_ERR_INVALID_ARG).  Launches on one device that overlap in time share
- * the workspace and must not run concurrently.  No counterpart in the reference. */
+ * partial tile to a library-owned workspace of the launch's stream and the last split of a
+ * tile sums all S partials in split order, so results do not depend on arrival order.
+ * Rejects problems needing more than 16384 tiles or S x tiles x 4096 floats (32 MB) of
+ * workspace (SGPU_ERR_INVALID_ARG).  No counterpart in the reference.
+ * Split-K workspaces (also used by sgpu_sgemm_opt and sgpu_gemv_multi when they split K): one
+ * per stream, so launches on different streams or from different host threads may overlap;
+ * launches on one stream run in order.  The null stream's is made by sgpu_init; another
+ * stream's on its first split launch (32 MB + 64 KB, at most 32 streams per device), kept
+ * until sgpu_stream_destroy releases it (streams not made by sgpu_stream_create keep theirs
+ * until the process ends).  A stream being recorded (sgpu_graph_begin) cannot get one: make
+ * its first split launch before recording, else sgpu_sgemm_splitk returns
+ * SGPU_ERR_NO_WORKSPACE and sgpu_sgemm_opt / sgpu_gemv_multi launch their unsplit kernels
+ * instead.  A recorded graph uses the workspace of the stream it was recorded on: do not
+ * replay it concurrently with itself or with other split launches on that stream, nor after
+ * that stream is destroyed. */
 int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream);
 /* The small-problem members sgemm_small16 / sgemm_small32 (tile = 16 or 32): one tile x tile
  * block of C per workgroup, A and B read straight into the matrix cores (no LDS staging), the

@@ -619,8 +619,10 @@ __device__ __forceinline__ void gemv_multi_xreg(const float* __restrict__ W, con
 // LDS region (row pitch 36 floats) and reads them back in the MFMA operand layout: lane
 // (i, h) (i = lane % 32, h = lane / 32) takes floats k0 + 16h + 4v .. +3 of row i as one
 // ds_read_b128 per v, and MFMA step s = 4v + e uses element e, so lane half h covers
-// k = k0 + 16h + s on both operands.  The region is private to the wave (in-order LDS
-// access, no block barrier).  The next chunk's global loads are issued before the current
+// k = k0 + 16h + s on both operands.  The region is private to the wave: a wave-level
+// barrier with wavefront-scope fences (wave_sync) orders the writes before the cross-lane
+// reads and the reads before the next chunk's writes; no block barrier.  The next chunk's
+// global loads are issued before the current
 // chunk's MFMAs.  Rows past T or N read a clamped (valid) row and are never stored; a K tail
 // chunk loads zeros past K.  Tiles are walked grid-stride over a linear block id (any grid of
 // 256-thread blocks); with one block per tile, block ids are regrouped so each XCD runs a
@@ -631,12 +633,21 @@ __device__ __forceinline__ void gemv_multi_xreg(const float* __restrict__ W, con
 // the MFMAs see the same operands as the CPU golden.
 // SPLIT: blocks are (tile, k-split) units, split-major; split s takes chunks
 // [s*nch/S, (s+1)*nch/S) and its four waves divide those.  Each unit's block-summed partial
-// tile goes to ws with device-coherent stores (written through to memory, waited for) before
-// the unit counts in on cnt[tile]; the last split of a tile sums the S partials in split
-// order (deterministic), adds the bias, writes Y and resets the counter.  ws holds
+// tile goes to ws and the unit counts in on cnt[tile] (the hand-off protocol of sgpu_device.h);
+// the last split of a tile sums the S partials in split order (deterministic), adds the bias,
+// writes Y and resets the counter.  ws holds
 // S * ntiles * 1024 * FN floats, cnt one zeroed counter per tile.  accum != 0 adds the
 // result to Y instead of overwriting it (Y[t][n] = Y[t][n] + (sum + bias), the residual
 // add of the decoders, in the order the separate add kernel computes it).
+// Lanes of one wave exchanging data through LDS: every LDS access of this wave before the
+// call happens before every access after it (wavefront-scope release, wave barrier, acquire;
+// no instructions beyond the ordering itself).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int FN, class WT = WF32, bool SPLIT = false>
 __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict__ W, const float* __restrict__ X,
                                              const float* __restrict__ bias, float* __restrict__ Y,
@@ -717,6 +728,7 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
                 *reinterpret_cast<sgpu_f32x4*>(&st[8 * q + lr][4 * lq]) = v;
             }
             if (more) load(cn);                             // next chunk in flight during the MFMAs
+            wave_sync();                                    // other lanes' stage writes are visible
             sgpu_f32x4 xa[4], wa[FN][4];
 #pragma unroll
             for (int v = 0; v < 4; v++) {
@@ -725,6 +737,7 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
                 for (int f = 0; f < FN; f++)
                     wa[f][v] = *reinterpret_cast<const sgpu_f32x4*>(&st[32 + 32 * f + i][16 * h + 4 * v]);
             }
+            wave_sync();                                    // reads done before the next chunk's writes
 #pragma unroll
             for (int s = 0; s < 16; s++)
 #pragma unroll
@@ -766,11 +779,13 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
 #pragma unroll
                 for (int rr = 0; rr < RPW; rr++)
                     __hip_atomic_store(rec + (f * RPW + rr) * 256, v[f][rr], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores have completed
+            __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores are acknowledged
             __syncthreads();
-            if (tid == 0)
+            if (tid == 0) {
                 last_s = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                          (unsigned)(nsplit - 1);
+                if (last_s) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // before the others' partials
+            }
             __syncthreads();
             if (!last_s) continue;                  // block-uniform; staging is free again
             // Partials come back U splits at a time, every load of a round issued before the

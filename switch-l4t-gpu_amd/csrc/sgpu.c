@@ -20,6 +20,7 @@
 #include "switch_gpu.h"
 
 #define SGPU_MAX_DEVICES 16
+#define SK_STREAMS 32        /* streams per device with their own split-K workspace */
 
 /* ---- embedded code objects (code_objects.S) ---- */
 extern const unsigned char sgpu_co_switch_gpu[], sgpu_co_switch_gpu_end[];
@@ -100,8 +101,16 @@ typedef struct {
     hipFunction_t dec_attn[3], dec_embed, dec_argmax_part, dec_argmax_embed;
     hipFunction_t dec_g2embed, dec_argmax_g2embed;
     hipFunction_t pf_embed, pf_gemm, pf_qkv_post, pf_attn[3], pf_swiglu;
-    float *sk_ws;          /* split-K partial tiles, SK_WS_FLOATS */
-    unsigned *sk_cnt;      /* split-K arrival counters, SK_MAX_TILES, zero between launches */
+    /* Split-K workspaces, one per stream that has launched split work (slot 0: the null
+     * stream, made with the device state): partial tiles (SK_WS_FLOATS) and arrival counters
+     * (SK_MAX_TILES, zero between launches).  Launches on one stream run in order, so a
+     * stream's split launches never overlap; concurrent streams have separate workspaces. */
+    struct {
+        void *stream;
+        float *ws;
+        unsigned *cnt;
+    } sk[SK_STREAMS];
+    int nsk;
 } devstate;
 
 static devstate g_dev[SGPU_MAX_DEVICES];
@@ -123,6 +132,9 @@ const char *sgpu_error_string(int status) {
     case SGPU_ERR_NO_KERNEL: return "kernel not found in the code object";
     case SGPU_ERR_NO_DEVICE: return "no usable HIP device";
     case SGPU_ERR_HOST_ALLOC: return "host allocation failed";
+    case SGPU_ERR_NO_WORKSPACE:
+        return "no split-K workspace for this stream (make the stream's first split-K call outside graph "
+               "capture; at most 32 streams per device have one)";
     default: break;
     }
     if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -135,36 +147,47 @@ const char *sgpu_error_string(int status) {
         if (e_ != hipSuccess) return (int)e_;    \
     } while (0)
 
+/* Unload what a failed load_device left behind, so a later call starts from nothing. */
+static void unload_device(devstate *d) {
+    for (int m = 0; m < NMOD; m++)
+        if (d->mod[m]) hipModuleUnload(d->mod[m]);
+    if (d->nsk > 0) {
+        hipFree(d->sk[0].ws);
+        hipFree(d->sk[0].cnt);
+    }
+    memset(d, 0, sizeof *d);
+}
+
 static int load_device(int dev) {
     devstate *d = &g_dev[dev];
-    if (d->ready) return SGPU_OK;
+    if (__atomic_load_n(&d->ready, __ATOMIC_ACQUIRE)) return SGPU_OK;
     int rc = SGPU_OK;
     pthread_mutex_lock(&g_lock);
-    if (d->ready) goto out;
+    if (__atomic_load_n(&d->ready, __ATOMIC_RELAXED)) goto out;
     hipDeviceProp_t p;
     hipError_t e = hipGetDeviceProperties(&p, dev);
     if (e != hipSuccess) { rc = (int)e; goto out; }
     d->cus = p.multiProcessorCount > 0 ? p.multiProcessorCount : 1;
     for (int m = 0; m < NMOD; m++) {
         e = hipModuleLoadData(&d->mod[m], g_cos[m].start);
-        if (e != hipSuccess) { rc = (int)e; goto out; }
+        if (e != hipSuccess) { d->mod[m] = NULL; rc = (int)e; goto fail; }
     }
     for (int k = 0; k < NKERN; k++) {
         e = hipModuleGetFunction(&d->fn[k], d->mod[g_kern[k].mod], g_kern[k].sym);
-        if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+        if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto fail; }
     }
     for (int i = 0; i < NLPR; i++)
         for (int j = 0; j < NSEG; j++) {
             char name[64];
             snprintf(name, sizeof name, "sgpu_gemv_f32_l%d_s%d", g_lpr[i], g_segs[j]);
             e = hipModuleGetFunction(&d->gemv_f32[i][j], d->mod[MOD_TUNED], name);
-            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto fail; }
             snprintf(name, sizeof name, "sgpu_gemv_h_l%d_s%d", g_lpr[i], g_segs[j]);
             e = hipModuleGetFunction(&d->gemv_h[i][j], d->mod[MOD_TUNED], name);
-            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto fail; }
             snprintf(name, sizeof name, "sgpu_gemv_hh_l%d_s%d", g_lpr[i], g_segs[j]);
             e = hipModuleGetFunction(&d->gemv_hh[i][j], d->mod[MOD_TUNED], name);
-            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto fail; }
         }
     for (int f = 0; f < NDECFAM; f++) {
         int n = dec_is_pair(f) ? NDEC_PAIR : NDEC_ALL;
@@ -172,52 +195,80 @@ static int load_device(int dev) {
             char name[64];
             snprintf(name, sizeof name, "sgpu_dec_%s_l%d_s%d", g_dec_fam[f], g_dec_cfg[j][0], g_dec_cfg[j][1]);
             e = hipModuleGetFunction(&d->dec[f][j], d->mod[MOD_DECODE], name);
-            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto out; }
+            if (e != hipSuccess) { rc = SGPU_ERR_NO_KERNEL; goto fail; }
         }
     }
     {
         const char *attn[3] = {"sgpu_dec_attn32", "sgpu_dec_attn64", "sgpu_dec_attn128"};
+        const char *pattn[3] = {"sgpu_pf_attn32", "sgpu_pf_attn64", "sgpu_pf_attn128"};
         for (int j = 0; j < 3; j++)
-            if (hipModuleGetFunction(&d->dec_attn[j], d->mod[MOD_DECODE], attn[j]) != hipSuccess) {
+            if (hipModuleGetFunction(&d->dec_attn[j], d->mod[MOD_DECODE], attn[j]) != hipSuccess ||
+                hipModuleGetFunction(&d->pf_attn[j], d->mod[MOD_DECODE], pattn[j]) != hipSuccess) {
                 rc = SGPU_ERR_NO_KERNEL;
-                goto out;
+                goto fail;
             }
         if (hipModuleGetFunction(&d->dec_embed, d->mod[MOD_DECODE], "sgpu_dec_embed") != hipSuccess ||
             hipModuleGetFunction(&d->dec_argmax_part, d->mod[MOD_DECODE], "sgpu_dec_argmax_part") != hipSuccess ||
             hipModuleGetFunction(&d->dec_argmax_embed, d->mod[MOD_DECODE], "sgpu_dec_argmax_embed") != hipSuccess ||
             hipModuleGetFunction(&d->dec_argmax_g2embed, d->mod[MOD_DECODE], "sgpu_dec_argmax_g2embed") != hipSuccess ||
-            hipModuleGetFunction(&d->dec_g2embed, d->mod[MOD_DECODE], "sgpu_dec_g2embed") != hipSuccess) {
-            rc = SGPU_ERR_NO_KERNEL;
-            goto out;
-        }
-        const char *pattn[3] = {"sgpu_pf_attn32", "sgpu_pf_attn64", "sgpu_pf_attn128"};
-        for (int j = 0; j < 3; j++)
-            if (hipModuleGetFunction(&d->pf_attn[j], d->mod[MOD_DECODE], pattn[j]) != hipSuccess) {
-                rc = SGPU_ERR_NO_KERNEL;
-                goto out;
-            }
-        if (hipModuleGetFunction(&d->pf_embed, d->mod[MOD_DECODE], "sgpu_pf_embed") != hipSuccess ||
+            hipModuleGetFunction(&d->dec_g2embed, d->mod[MOD_DECODE], "sgpu_dec_g2embed") != hipSuccess ||
+            hipModuleGetFunction(&d->pf_embed, d->mod[MOD_DECODE], "sgpu_pf_embed") != hipSuccess ||
             hipModuleGetFunction(&d->pf_gemm, d->mod[MOD_DECODE], "sgpu_pf_gemm") != hipSuccess ||
             hipModuleGetFunction(&d->pf_qkv_post, d->mod[MOD_DECODE], "sgpu_pf_qkv_post") != hipSuccess ||
             hipModuleGetFunction(&d->pf_swiglu, d->mod[MOD_DECODE], "sgpu_pf_swiglu") != hipSuccess) {
             rc = SGPU_ERR_NO_KERNEL;
-            goto out;
+            goto fail;
         }
     }
-    /* split-K workspace: allocated once per device, counters zeroed once (every launch
-     * leaves them at zero) */
-    e = hipMalloc((void **)&d->sk_ws, SK_WS_FLOATS * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&d->sk_cnt, SK_MAX_TILES * sizeof(unsigned));
-    if (e == hipSuccess) e = hipMemset(d->sk_cnt, 0, SK_MAX_TILES * sizeof(unsigned));
-    if (e != hipSuccess) {
-        hipFree(d->sk_ws);
-        hipFree(d->sk_cnt);
-        d->sk_ws = NULL;
-        d->sk_cnt = NULL;
-        rc = (int)e;
+    /* the null stream's split-K workspace, counters zeroed once (every launch leaves them at zero) */
+    d->nsk = 1;
+    d->sk[0].stream = NULL;
+    e = hipMalloc((void **)&d->sk[0].ws, SK_WS_FLOATS * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&d->sk[0].cnt, SK_MAX_TILES * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(d->sk[0].cnt, 0, SK_MAX_TILES * sizeof(unsigned));
+    if (e != hipSuccess) { rc = (int)e; goto fail; }
+    __atomic_store_n(&d->ready, 1, __ATOMIC_RELEASE);
+    goto out;
+fail:
+    unload_device(d);
+out:
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+/* The split-K workspace of `stream` on device state d: the stream's own, made on its first
+ * split launch outside graph capture and kept until sgpu_stream_destroy (streams made
+ * elsewhere: until the process ends).  SGPU_ERR_NO_WORKSPACE
+ * when the stream has none and cannot get one now (it is being recorded, or SK_STREAMS
+ * streams already hold one). */
+static int sk_workspace(devstate *d, void *stream, float **ws, unsigned **cnt) {
+    int rc = SGPU_ERR_NO_WORKSPACE;
+    pthread_mutex_lock(&g_lock);
+    for (int i = 0; i < d->nsk; i++)
+        if (d->sk[i].stream == stream) {
+            *ws = d->sk[i].ws;
+            *cnt = d->sk[i].cnt;
+            rc = SGPU_OK;
+            goto out;
+        }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (d->nsk >= SK_STREAMS || hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess ||
+        cs != hipStreamCaptureStatusNone)
+        goto out;
+    float *w = NULL;
+    unsigned *c = NULL;
+    if (hipMalloc((void **)&w, SK_WS_FLOATS * sizeof(float)) != hipSuccess ||
+        hipMalloc((void **)&c, SK_MAX_TILES * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(c, 0, SK_MAX_TILES * sizeof(unsigned)) != hipSuccess) {
+        hipFree(w);
+        hipFree(c);
         goto out;
     }
-    d->ready = 1;
+    d->sk[d->nsk].stream = stream;
+    d->sk[d->nsk].ws = *ws = w;
+    d->sk[d->nsk].cnt = *cnt = c;
+    d->nsk++;
+    rc = SGPU_OK;
 out:
     pthread_mutex_unlock(&g_lock);
     return rc;
@@ -241,7 +292,7 @@ static devstate *cur(int *rc) {
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) { *rc = (int)e; return NULL; }
     if (dev < 0 || dev >= SGPU_MAX_DEVICES) { *rc = SGPU_ERR_NO_DEVICE; return NULL; }
-    if (!g_dev[dev].ready) {
+    if (!__atomic_load_n(&g_dev[dev].ready, __ATOMIC_ACQUIRE)) {
         *rc = load_device(dev);
         if (*rc) return NULL;
     }
@@ -343,8 +394,27 @@ int sgpu_stream_create(void **stream) {
     *stream = (void *)st;
     return SGPU_OK;
 }
+/* Free the split-K workspaces of `stream` (its work finished) and drop them from the tables. */
+static void sk_release(void *stream) {
+    pthread_mutex_lock(&g_lock);
+    for (int dev = 0; dev < SGPU_MAX_DEVICES; dev++) {
+        devstate *d = &g_dev[dev];
+        if (!__atomic_load_n(&d->ready, __ATOMIC_RELAXED)) continue;
+        for (int i = 1; i < d->nsk; i++)
+            if (d->sk[i].stream == stream) {
+                hipFree(d->sk[i].ws);
+                hipFree(d->sk[i].cnt);
+                d->sk[i] = d->sk[--d->nsk];
+                break;
+            }
+    }
+    pthread_mutex_unlock(&g_lock);
+}
+
 int sgpu_stream_destroy(void *stream) {
     if (!stream) return SGPU_OK;
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    sk_release(stream);
     HIPCHK(hipStreamDestroy((hipStream_t)stream));
     return SGPU_OK;
 }
@@ -476,7 +546,8 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
     if (!kernel || !grid || !block || M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
     int dev = 0;
     const devstate *d = NULL;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < SGPU_MAX_DEVICES && g_dev[dev].ready)
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < SGPU_MAX_DEVICES &&
+        __atomic_load_n(&g_dev[dev].ready, __ATOMIC_ACQUIRE))
         d = &g_dev[dev];
     return geometry(d, kernel, M, N, K, grid, block);
 }
@@ -554,11 +625,11 @@ static int splitk_fits(int M, int N, int S) {
     return tiles <= SK_MAX_TILES && (unsigned long long)S * tiles * SK_TILE * SK_TILE <= SK_WS_FLOATS;
 }
 static int splitk_launch(devstate *d, const float *A, const float *B, float *C, int M, int N, int K, int S,
-                         void *stream) {
+                         float *ws, unsigned *cnt, void *stream) {
     const long long tiles = (long long)cdiv(M, SK_TILE) * cdiv(N, SK_TILE);
     if (!splitk_fits(M, N, S)) return SGPU_ERR_INVALID_ARG;
     unsigned g[3] = {(unsigned)(tiles * S), 1, 1}, b[3] = {256, 1, 1};
-    void *args[] = {&A, &B, &C, &M, &N, &K, &S, &d->sk_ws, &d->sk_cnt};
+    void *args[] = {&A, &B, &C, &M, &N, &K, &S, &ws, &cnt};
     return launch(d->fn[K_SGEMM_SPLITK], g, b, stream, args);
 }
 int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream) {
@@ -570,7 +641,10 @@ int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, in
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
-    return splitk_launch(d, A, B, C, M, N, K, S, stream);
+    float *ws;
+    unsigned *cnt;
+    if ((rc = sk_workspace(d, stream, &ws, &cnt))) return rc;
+    return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
 }
 /* When sgpu_sgemm_opt splits K (measured, warm, srand inputs: 512^3 13.0 -> 9.9 us at S = 4,
  * 1023x1025x997 41.6 -> 33.3 us at S = 4; 1024^3 and larger gain nothing): with fewer 64x64
@@ -658,7 +732,10 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
         if (t32 <= d->cus && K <= 1024) return small_launch(d, 32, A, B, C, M, N, K, stream);
     }
     const int S = K > 0 ? splitk_pick(M, N, K, d->cus) : 1;
-    if (S > 1) return splitk_launch(d, A, B, C, M, N, K, S, stream);
+    float *ws;
+    unsigned *cnt;
+    if (S > 1 && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
+        return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
     const int m = sgemm_pick(M, N, d->cus);
     return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }
@@ -812,7 +889,10 @@ int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y,
                     void *stream) {
     int rc;
     devstate *d = (N > 0 && T > 0 && K >= 0) ? cur(&rc) : NULL;
-    return sgpu_internal_gemv_multi(W, X, bias, Y, K, N, T, d ? d->sk_ws : NULL, d ? d->sk_cnt : NULL, stream);
+    float *ws = NULL;
+    unsigned *cnt = NULL;
+    if (d && sk_workspace(d, stream, &ws, &cnt) != SGPU_OK) ws = NULL, cnt = NULL;   /* unsplit kernels */
+    return sgpu_internal_gemv_multi(W, X, bias, Y, K, N, T, ws, cnt, stream);
 }
 
 /* ---- Qwen support kernels ---- */

@@ -288,19 +288,20 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, const floa
         if (slice == 0) out[(size_t)h * HD + d] = tot / sum;
         return;
     }
-    // Partials go out as device-coherent stores (written through to memory) and are read back
-    // the same way, so no L2 writeback or invalidate is needed: the stores are complete
-    // (waited for) before this block's count reaches the head's counter, and the last block
-    // reads them after seeing the full count.
+    // Partials go to the head's last block by the hand-off protocol of sgpu_device.h
+    // (device-coherent stores waited for, a per-head counter, an acquire by the last arriver).
     float* rec = ws + ((size_t)h * kAttnSplits + c) * WSTRIDE;
     if (slice == 0) __hip_atomic_store(rec + d, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
         __hip_atomic_store(rec + HD, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(rec + HD + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores have completed
+    __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores are acknowledged
     __syncthreads();
-    if (tid == 0) last_s = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    if (tid == 0) {
+        last_s = __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+        if (last_s) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // before the others' partials
+    }
     __syncthreads();
     if (!last_s) return;
     // All S partials of head h into LDS with one round of device-coherent loads, then

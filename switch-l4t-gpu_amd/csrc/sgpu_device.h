@@ -73,6 +73,20 @@ __device__ __forceinline__ float sgpu_wave_max(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Cross-block hand-off of partial results (split-K SGEMM, the split batched GEMM, the decode
+// attention's position chunks): the units of one output tile each write a partial record and
+// count in on the tile's counter; the last to arrive combines all records in a fixed order.
+//   writer: partials are written with agent-scope atomic stores (global_store ... sc1: written
+//           through to the device's coherence point past the per-XCD L2s), every wave waits for
+//           their acknowledgment (s_waitcnt vmcnt(0)), a block barrier, then thread 0 adds 1 to
+//           the counter (agent-scope atomic, relaxed);
+//   reader: the thread that sees the final count takes an agent-scope acquire fence (buffer_inv
+//           sc1) before a block barrier, then the block reads the records with agent-scope atomic
+//           loads (sc1) and resets the counter.
+// The writer side replaces an agent-scope release (buffer_wbl2 sc1 per unit) by the
+// acknowledgment of stores that bypass the L2 write-back: the release measured +55% on split
+// SGEMM (1023x1025x997 at 4 splits 31.7 -> 48.9 us, 1024x768x1024 21.8 -> 33.1) while the
+// acquire costs ~0.5 us per launch.
 // Linear thread index / block size for kernels that accept 1-D or 2-D blocks.
 __device__ __forceinline__ int sgpu_tid() { return threadIdx.x + threadIdx.y * blockDim.x; }
 __device__ __forceinline__ int sgpu_nthreads() { return blockDim.x * blockDim.y * blockDim.z; }

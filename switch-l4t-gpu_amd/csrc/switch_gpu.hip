@@ -377,10 +377,11 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
         k0 = SPLIT ? (u / ntiles) * per * BK : 0;
         kext = SPLIT ? min(K - k0, per * BK) : K;
     };
-    // A unit's result: with one split, straight to C; with several, each split's partial
-    // tile goes out as device-coherent stores (written through to memory, waited for before
-    // the tile's counter is incremented) and the last split to arrive sums all S partials in
-    // split order -- the same order whichever block is last -- and writes C.
+    // A unit's result: with one split, straight to C; with several, the split hands its
+    // partial tile to the tile's last split (the cross-block hand-off set out in
+    // sgpu_device.h: device-coherent stores waited for, a counter, an acquire by the last
+    // arriver), which sums all S in split order -- the same order whichever block is last --
+    // and writes C.
     __shared__ int last_s;
     auto finish = [&](int u, int m0, int n0, bool interior, sgpu_f32x16 (&acc)[T::FM][T::FN]) __attribute__((always_inline)) {
         if constexpr (SPLIT) {
@@ -396,11 +397,13 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
                         for (int r = 0; r < 16; r++)
                             __hip_atomic_store(rec + ((i * T::FN + j) * 16 + r) * T::NT, acc[i][j][r], __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
-                __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores have completed
+                __builtin_amdgcn_s_waitcnt(0);          // this wave's partial stores are acknowledged
                 __syncthreads();
-                if (th.tid == 0)
+                if (th.tid == 0) {
                     last_s = __hip_atomic_fetch_add(cnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                              (unsigned)(nsplit - 1);
+                    if (last_s) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // before the others' partials
+                }
                 __syncthreads();
                 if (!last_s) return;
                 // U splits per round, every load of a round issued before the first add (one

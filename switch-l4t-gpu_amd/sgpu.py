@@ -22,6 +22,7 @@ SGPU_ERR_NOT_INITIALIZED = -2
 SGPU_ERR_NO_KERNEL = -3
 SGPU_ERR_NO_DEVICE = -4
 SGPU_ERR_HOST_ALLOC = -5
+SGPU_ERR_NO_WORKSPACE = -6
 
 
 class SgpuError(RuntimeError):

@@ -140,7 +140,8 @@ def test_gemv_hh_special_x_codes(gpu, og):
 def test_recorded_launches_replay(gpu, og):
     """GEMV (fp16 and fp32 weights) and SGEMM launches recorded once on a stream and replayed:
     every replay, with new inputs copied in between (host work and synchronisation between
-    the replays), gives the same bits as the same launches run directly."""
+    the replays), gives the same bits as the same launches run directly on that stream (whose
+    split-K workspace was made before recording, so both take the split kernel)."""
     say("graph replay gemv_h + gemv_warp_b + sgemm_opt")
     N, K, M = 896, 4864, 64
     Wh = gpu.f32_to_f16(gpu.gen_normal(N * K, 3, 0.0, 0.02)[0])
@@ -157,6 +158,8 @@ def test_recorded_launches_replay(gpu, og):
         gpu.call("sgpu_sgemm_opt", dA.ptr, dWf.ptr, dC.ptr, M, N, K, st)
 
     st = gpu.Stream()
+    launches(st.h)                  # the stream's split-K workspace exists before recording
+    st.synchronize()
     with gpu.Graph(st) as g:
         launches(st.h)
     for rep in range(4):
@@ -164,8 +167,8 @@ def test_recorded_launches_replay(gpu, og):
         gpu.call("sgpu_memcpy_htod", dx.ptr, x.ctypes.data, K * 4)
         for d in (dyh, dyf, dC):
             d.fill_bytes(0xFF)
-        launches(None)
-        gpu.synchronize()
+        launches(st.h)              # the same launches on the same stream, run directly
+        st.synchronize()
         want = [d.to_host() for d in (dyh, dyf, dC)]
         for d in (dyh, dyf, dC):
             d.fill_bytes(0xFF)

@@ -163,6 +163,93 @@ def test_splitk_integer_exact(gpu, M, N, K, S):
         assert np.array_equal(dC.to_host(), want)
 
 
+def test_splitk_streams_overlap(gpu):
+    """Split-K launches on two streams, interleaved without synchronisation, and from two host
+    threads on their own streams: each stream has its own workspace, so every result is the
+    exact product (integer inputs) however the launches overlap on the device."""
+    import threading
+
+    M, N, K, S = 300, 260, 1100, 4
+    rng = np.random.default_rng(17)
+    mats = []
+    for i in range(2):
+        A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+        B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+        mats.append((gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N)),
+                     (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)))
+    streams = [gpu.Stream(), gpu.Stream()]
+    say("split-K on two streams, interleaved")
+    for _ in range(40):
+        for (dA, dB, dC, _), st in zip(mats, streams):
+            gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, S, st.h)
+            gpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
+    gpu.synchronize()
+    for dA, dB, dC, want in mats:
+        assert np.array_equal(dC.to_host(), want)
+    say("split-K from two host threads")
+    errs = []
+
+    def worker(i):
+        dA, dB, dC, _ = mats[i]
+        try:
+            for _ in range(40):
+                gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, S, streams[i].h)
+            streams[i].synchronize()
+        except Exception as e:          # reported below
+            errs.append(e)
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs, errs
+    for dA, dB, dC, want in mats:
+        assert np.array_equal(dC.to_host(), want)
+    for st in streams:
+        st.close()
+
+
+def test_splitk_recording_needs_a_workspace(gpu):
+    """A stream being recorded cannot get a workspace: on a fresh stream sgpu_sgemm_splitk
+    reports SGPU_ERR_NO_WORKSPACE and sgpu_sgemm_opt records its unsplit member; after one
+    split launch outside recording, the stream's workspace is recorded and every replay is
+    exact."""
+    M, N, K = 768, 768, 2048                                # sgpu_sgemm_opt splits this one 3 ways
+    rng = np.random.default_rng(19)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC, dD = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N)), \
+        gpu.DeviceArray((M, N))
+    st = gpu.Stream()
+    with gpu.Graph(st) as g:
+        rc = gpu.lib().sgpu_sgemm_splitk(dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, st.h)
+        gpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dD.ptr, M, N, K, st.h)
+    assert rc == gpu.SGPU_ERR_NO_WORKSPACE
+    assert "workspace" in gpu.error_string(rc)
+    for _ in range(3):
+        dD.fill_bytes(0xFF)
+        g.launch()
+        st.synchronize()
+        assert np.array_equal(dD.to_host(), want)
+    g.close()
+    gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, st.h)   # the stream's workspace
+    st.synchronize()
+    assert np.array_equal(dC.to_host(), want)
+    with gpu.Graph(st) as g2:
+        gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, st.h)
+        gpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dD.ptr, M, N, K, st.h)
+    for _ in range(3):
+        dC.fill_bytes(0xFF)
+        dD.fill_bytes(0xFF)
+        g2.launch()
+        st.synchronize()
+        assert np.array_equal(dC.to_host(), want) and np.array_equal(dD.to_host(), want)
+    g2.close()
+    st.close()
+
+
 SMALL_CASES = [(1, 1, 1), (16, 16, 16), (33, 17, 96), (7, 300, 13), (256, 256, 256), (512, 512, 512),
                (100, 70, 3000), (130, 260, 40), (257, 511, 1030), (1023, 1025, 997), (64, 48, 2)]
 
