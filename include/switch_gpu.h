@@ -40,6 +40,7 @@ extern "C" {
 #define SGPU_ERR_HOST_ALLOC (-5)     /* host memory exhausted */
 #define SGPU_ERR_NO_WORKSPACE (-6)   /* a split-K launch on a stream that has no workspace and cannot
                                         get one now (being recorded, or 32 streams already hold one) */
+#define SGPU_ERR_SCRATCH_LIMIT (-7)  /* more than the allocation-free entry point's fixed scratch */
 
 /* Replaces cuGetErrorString (cuda_drv.h:31).  Never NULL. */
 const char *sgpu_error_string(int status);
@@ -153,6 +154,18 @@ int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, in
  * replay it concurrently with itself or with other split launches on that stream, nor after
  * that stream is destroyed. */
 int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream);
+/* sgpu_sgemm_splitk that allocates nothing, for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same kernel and arguments, same results bit for bit; the
+ * partial tiles and tile counters live in a fixed scratch array compiled into the library,
+ * one copy per device, held until the process ends: at most 32 MiB of partial tiles
+ * (splits x 64x64 tiles x 4096 floats <= 8 Mi floats) and 16384 tiles, larger problems
+ * rejected with SGPU_ERR_SCRATCH_LIMIT.  The device must be set up by sgpu_init first
+ * (SGPU_ERR_NOT_INITIALIZED otherwise).  Every call on a device shares that device's scratch
+ * (counters zeroed at set-up; each launch leaves them at zero): calls that overlap in time
+ * on one device -- other streams, other host threads, a replayed graph -- race. */
+int sgpu_sgemm_splitk_noalloc(const float *A, const float *B, float *C, int M, int N, int K, int S,
+                              void *stream);
 /* The small-problem members sgemm_small16 / sgemm_small32 (tile = 16 or 32): one tile x tile
  * block of C per workgroup, A and B read straight into the matrix cores (no LDS staging), the
  * workgroup's four waves splitting K and summing their partials in a fixed order.  Any shape

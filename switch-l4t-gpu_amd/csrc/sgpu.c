@@ -19,7 +19,6 @@
 #include "sgpu_internal.h"
 #include "switch_gpu.h"
 
-#define SGPU_MAX_DEVICES 16
 #define SK_STREAMS 32        /* streams per device with their own split-K workspace */
 
 /* ---- embedded code objects (code_objects.S) ---- */
@@ -132,6 +131,9 @@ const char *sgpu_error_string(int status) {
     case SGPU_ERR_NO_KERNEL: return "kernel not found in the code object";
     case SGPU_ERR_NO_DEVICE: return "no usable HIP device";
     case SGPU_ERR_HOST_ALLOC: return "host allocation failed";
+    case SGPU_ERR_SCRATCH_LIMIT:
+        return "the problem needs more than the allocation-free entry point's fixed scratch (32 MiB of partial "
+               "tiles: splits x 64x64 tiles x 4096 floats, at most 16384 tiles)";
     case SGPU_ERR_NO_WORKSPACE:
         return "no split-K workspace for this stream (make the stream's first split-K call outside graph "
                "capture; at most 32 streams per device have one)";
@@ -227,6 +229,8 @@ static int load_device(int dev) {
     if (e == hipSuccess) e = hipMalloc((void **)&d->sk[0].cnt, SK_MAX_TILES * sizeof(unsigned));
     if (e == hipSuccess) e = hipMemset(d->sk[0].cnt, 0, SK_MAX_TILES * sizeof(unsigned));
     if (e != hipSuccess) { rc = (int)e; goto fail; }
+    /* the allocation-free entry point's fixed scratch: this device's copy resolved once */
+    if ((rc = sgpu_internal_scratch_setup(dev)) != SGPU_OK) goto fail;
     __atomic_store_n(&d->ready, 1, __ATOMIC_RELEASE);
     goto out;
 fail:
@@ -646,6 +650,30 @@ int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, in
     if ((rc = sk_workspace(d, stream, &ws, &cnt))) return rc;
     return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
 }
+/* sgpu_sgemm_splitk with the partials and counters in the library's fixed device scratch: no
+ * allocation on any path (the device must be set up by sgpu_init first; the launch itself
+ * allocates nothing), problems beyond the scratch rejected.  Calls that overlap on one device
+ * share the scratch and race. */
+int sgpu_sgemm_splitk_noalloc(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream) {
+    if (M < 0 || N < 0 || K < 0 || S < 1) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    S = K > 0 ? sk_splits(K, S) : 1;
+    const long long tiles = (long long)cdiv(M, SK_TILE) * cdiv(N, SK_TILE);
+    if (tiles > (long long)SGPU_SCRATCH_TILES ||
+        (unsigned long long)S * tiles * SK_TILE * SK_TILE > (unsigned long long)SGPU_SCRATCH_FLOATS)
+        return SGPU_ERR_SCRATCH_LIMIT;
+    if (!C || (K > 0 && (!A || !B))) return SGPU_ERR_INVALID_ARG;
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SGPU_MAX_DEVICES || !__atomic_load_n(&g_dev[dev].ready, __ATOMIC_ACQUIRE))
+        return SGPU_ERR_NOT_INITIALIZED;                  /* set-up (which allocates) is sgpu_init's */
+    float *ws;
+    unsigned *cnt;
+    int rc = sgpu_internal_scratch(dev, &ws, &cnt);
+    if (rc) return rc;
+    return splitk_launch(&g_dev[dev], A, B, C, M, N, K, S, ws, cnt, stream);
+}
+
 /* When sgpu_sgemm_opt splits K (measured, warm, srand inputs: 512^3 13.0 -> 9.9 us at S = 4,
  * 1023x1025x997 41.6 -> 33.3 us at S = 4; 1024^3 and larger gain nothing): with fewer 64x64
  * tiles than half the CUs, into about CUs / tiles splits (a power of two, at most 8); with a K

@@ -3,6 +3,12 @@
 #define SGPU_INTERNAL_H
 #include <stdint.h>
 
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGPU_MAX_DEVICES 16
+
 /* x[i] = h2f(emb[token*C + i]) on the device (sgpu_embed_h in the tuned code object). */
 __attribute__((visibility("hidden"))) int sgpu_internal_embed_h(const uint16_t *emb, int token, float *x, int C,
                                                                 void *stream);
@@ -69,4 +75,17 @@ SGPU_HIDDEN int sgpu_internal_g2_lmhead(const float *W, int K, int N, const floa
                                         const float *lnb, float eps, float *y, void *stream);
 SGPU_HIDDEN int sgpu_internal_g2_embed(const float *wte, const float *wpe, int token, int pos, float *x, int C,
                                        int *step, void *stream);
+/* The allocation-free split-K entry point's fixed device scratch (sgpu_scratch.hip): room for
+ * SGPU_SCRATCH_FLOATS floats of partial tiles (32 MiB: S x tiles x 4096 <= 8 Mi) and
+ * SGPU_SCRATCH_TILES tile counters, one copy per device.  setup resolves the current device's
+ * copy and zeroes its counters (once per device, from the library's device set-up); scratch
+ * returns the device's pointers, SGPU_ERR_NOT_INITIALIZED before setup. */
+#define SGPU_SCRATCH_FLOATS (8u << 20)
+#define SGPU_SCRATCH_TILES 16384u
+SGPU_HIDDEN int sgpu_internal_scratch_setup(int dev);
+SGPU_HIDDEN int sgpu_internal_scratch(int dev, float **ws, unsigned **cnt);
+
+#ifdef __cplusplus
+}
+#endif
 #endif

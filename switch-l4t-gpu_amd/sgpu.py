@@ -23,6 +23,7 @@ SGPU_ERR_NO_KERNEL = -3
 SGPU_ERR_NO_DEVICE = -4
 SGPU_ERR_HOST_ALLOC = -5
 SGPU_ERR_NO_WORKSPACE = -6
+SGPU_ERR_SCRATCH_LIMIT = -7
 
 
 class SgpuError(RuntimeError):
@@ -74,6 +75,7 @@ _SIGS = {
     "sgpu_sgemm_opt": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_opt256": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_splitk": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "sgpu_sgemm_splitk_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_sgemm_small": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_sgemm_naive": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_membw_read4": (_I, [_P, _P, _I, _I, ct.POINTER(_I), _P]),
