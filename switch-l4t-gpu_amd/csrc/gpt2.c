@@ -87,6 +87,13 @@ struct sgpu_gpt2 {
 
 void sgpu_gpt2_destroy(sgpu_gpt2 *e) {
     if (!e) return;
+    /* the stream's work finishes, then the graphs that reference the buffers go, then the
+     * buffers, then the stream */
+    if (e->stream) hipStreamSynchronize(e->stream);
+    if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
+    if (e->g_layers) hipGraphDestroy(e->g_layers);
+    if (e->ge_step) hipGraphExecDestroy(e->ge_step);
+    if (e->g_step) hipGraphDestroy(e->g_step);
     float *bufs[] = {e->w, e->x, e->ln1, e->qkv, e->att, e->y, e->ln2, e->fc, e->scores, e->probs, e->logits,
                      e->x2, e->xT, e->ln1T, e->qkvT, e->attT, e->yT, e->ln2T, e->fcT, e->d_q, e->d_amax_v,
                      e->d_attn_ws, e->d_split_ws};
@@ -96,10 +103,6 @@ void sgpu_gpt2_destroy(sgpu_gpt2 *e) {
     sgpu_free(e->d_amax_i);
     sgpu_free(e->d_attn_cnt);
     sgpu_free(e->d_split_cnt);
-    if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
-    if (e->g_layers) hipGraphDestroy(e->g_layers);
-    if (e->ge_step) hipGraphExecDestroy(e->ge_step);
-    if (e->g_step) hipGraphDestroy(e->g_step);
     for (int l = 0; l < e->cfg.NL; l++) {
         if (e->kc) sgpu_free(e->kc[l]);
         if (e->vc) sgpu_free(e->vc[l]);

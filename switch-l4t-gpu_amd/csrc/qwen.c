@@ -133,6 +133,13 @@ static int dalloc(void **p, size_t bytes, const void *src) {
 
 void sgpu_qwen_destroy(sgpu_qwen *e) {
     if (!e) return;
+    /* the stream's work finishes, then the graphs that reference the buffers go, then the
+     * buffers, then the stream */
+    if (e->stream) hipStreamSynchronize(e->stream);
+    if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
+    if (e->g_layers) hipGraphDestroy(e->g_layers);
+    if (e->ge_step) hipGraphExecDestroy(e->ge_step);
+    if (e->g_step) hipGraphDestroy(e->g_step);
     const int NL = e->cfg.NL;
     void **single[] = {(void **)&e->d_emb, (void **)&e->d_lnfw, (void **)&e->d_cos, (void **)&e->d_sin,
                        (void **)&e->d_x, (void **)&e->d_ln1, (void **)&e->d_qkv, (void **)&e->d_att,
@@ -160,10 +167,6 @@ void sgpu_qwen_destroy(sgpu_qwen *e) {
     sgpu_free(e->d_pf_ids);
     float *pf[] = {e->d_pf_x, e->d_pf_xn, e->d_pf_qkv, e->d_pf_att, e->d_pf_y, e->d_pf_g};
     for (size_t i = 0; i < sizeof pf / sizeof pf[0]; i++) sgpu_free(pf[i]);
-    if (e->ge_layers) hipGraphExecDestroy(e->ge_layers);
-    if (e->g_layers) hipGraphDestroy(e->g_layers);
-    if (e->ge_step) hipGraphExecDestroy(e->ge_step);
-    if (e->g_step) hipGraphDestroy(e->g_step);
     if (e->stream) hipStreamDestroy(e->stream);
     free(e);
 }
