@@ -28,6 +28,7 @@ decode, also on one thread in the reference's serial form.
 """
 import argparse
 import ctypes as ct
+import itertools
 import json
 import os
 import sys
@@ -175,13 +176,31 @@ GEMV_SHAPES += [("fp16x", name, N, K) for wt, name, N, K in GEMV_SHAPES if wt ==
 ROTATE_BYTES = 600e6     # weight copies rotated per shape, up to 64: past the 256 MB MALL where that fits
 
 
-def bench_sgemm_sweep(reps=100, warm=50, graphs=True):
+def warm_for(launch, sync, min_launches, min_s):
+    """Run `launch` at least min_launches times and for at least min_s seconds of wall time,
+    synchronising every 10 launches: the clock climbs from idle over tens of milliseconds,
+    and a count-only warm-up of small launches ends before it has (2048^3 timed 142 us per
+    launch from a host loop after 50 launches, 128 us after a further second of work)."""
+    n, t0 = 0, time.perf_counter()
+    while n < min_launches or time.perf_counter() - t0 < min_s:
+        for _ in range(10):
+            launch()
+        n += 10
+        sync()
+    return n
+
+
+def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1):
     """sgpu_sgemm_opt over the SGEMM size sweep (square 256..4096 and the ragged 1023x1025x997),
-    reference-generator inputs; HIP-event time per launch after warm-up, normwise error of
-    sampled rows against a float64 product.  graphs=False skips the recorded-graph timing
-    (a kernel trace of graph replay is not taken by the profiler)."""
+    reference-generator inputs; HIP-event time per launch after a warm-up of at least `warm`
+    launches and `warm_s` seconds, normwise error of sampled rows against a float64 product.
+    graphs=False skips the recorded-graph timing (a kernel trace of graph replay is not taken
+    by the profiler)."""
     out = []
+    cus = sgpu.device_props().compute_units
     for M, N, K in SWEEP_SHAPES:
+        S = ct.c_int()
+        launch = f"{sgpu.lib().sgpu_sgemm_opt_plan(M, N, K, cus, ct.byref(S)).decode()} S={S.value}"
         A, B = sgpu.gen_sgemm_inputs(max(M * K, K * N), 42)
         A, B = A[:M * K], B[:K * N]
         dA, dB, dC = sgpu.DeviceArray.from_host(A), sgpu.DeviceArray.from_host(B), sgpu.DeviceArray((M, N))
@@ -193,7 +212,8 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True):
         ref = A.reshape(M, K)[rows].astype(np.float64) @ B.reshape(K, N).astype(np.float64)
         err = float(np.abs(C[rows] - ref).max() / np.abs(ref).max())
         ev = sgpu.Events()
-        for _ in range(warm):
+        warm_for(run, sgpu.synchronize, warm, warm_s)
+        for _ in range(10):
             run()
         ev.record_start(None)
         for _ in range(reps):
@@ -201,17 +221,22 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True):
         ev.record_stop(None)
         us = ev.elapsed_ms() * 1e3 / reps
         if not graphs:
-            out.append({"M": M, "N": N, "K": K, "us_host_loop": round(us, 2), "normwise_err": err})
+            out.append({"M": M, "N": N, "K": K, "launch": launch, "us_host_loop": round(us, 2), "normwise_err": err})
             for d in (dA, dB, dC):
                 d.close()
             continue
-        # the same launches recorded once and replayed: no host submission cost per launch
+        # the same launches recorded once and replayed: no host submission cost per launch.
+        # One launch on the stream before recording gives it its split-K workspace (a stream
+        # being recorded cannot get one, and sgpu_sgemm_opt would record its unsplit member).
         st = sgpu.Stream()
+        sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
+        st.synchronize()
         per_graph = 10
         with sgpu.Graph(st) as g:
             for _ in range(per_graph):
                 sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
-        for _ in range(max(1, warm // per_graph)):
+        warm_for(g.launch, st.synchronize, max(1, warm // per_graph), warm_s)
+        for _ in range(2):
             g.launch()
         ev.record_start(st.h)
         for _ in range(max(1, reps // per_graph)):
@@ -221,7 +246,7 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True):
         g.close()
         st.close()
         tf = 2.0 * M * N * K / (us_g * 1e-6) / 1e12
-        out.append({"M": M, "N": N, "K": K, "us_in_graph": round(us_g, 2), "us_host_loop": round(us, 2),
+        out.append({"M": M, "N": N, "K": K, "launch": launch, "us_in_graph": round(us_g, 2), "us_host_loop": round(us, 2),
                     "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MATRIX_TFLOPS, 4), "normwise_err": err})
         for d in (dA, dB, dC):
             d.close()
@@ -267,8 +292,8 @@ def bench_gemv_shapes(reps=50, warm=100):
             ref = ref + bias[rows].astype(np.float64)
         err = float(np.abs(y[rows] - ref).max() / np.abs(ref).max())
         ev = sgpu.Events()
-        for i in range(warm):
-            run(i)
+        launches = itertools.count()
+        warm_for(lambda: run(next(launches)), sgpu.synchronize, warm, 0.05)
         ev.record_start(None)
         for i in range(reps * copies):
             run(i)
@@ -279,8 +304,7 @@ def bench_gemv_shapes(reps=50, warm=100):
         with sgpu.Graph(strm) as g:
             for i in range(copies):
                 run(i, strm.h)
-        for _ in range(max(1, warm // copies)):
-            g.launch()
+        warm_for(g.launch, strm.synchronize, max(1, warm // copies), 0.05)
         ev.record_start(strm.h)
         for _ in range(reps):
             g.launch()

@@ -126,12 +126,19 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * tile's area over the member's sustained rate.  Problems whose 16x16 tiles fit the CUs in
  * one round go to sgemm_small16 (K <= 2048, or K <= 4096 with a quarter of the CUs' tiles
  * or one row or column of tiles), else those whose 32x32 tiles do (K <= 1024) to
- * sgemm_small32; of the rest, problems with fewer 64x64 tiles than half the CUs, small ones
- * whose K is not a multiple of 32, and one-round ones where a 2-4 way split shortens the
- * busiest CU's run of k-slices, go to sgemm_splitk. */
+ * sgemm_small32; of the rest, problems of at most two rounds of 64x64 tiles go to
+ * sgemm_splitk when a cost model of the busiest CU's k-slices, masked tail slices and split
+ * hand-offs prefers a 2-8 way split (16 for a few tiles of tall K) to none. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+/* The symbol sgpu_sgemm_opt launches for an M x N x K problem on a device of `cus` compute
+ * units ("sgemm_small16", "sgemm_splitk", "sgemm_opt256", ...), with the split count in
+ * *splits (1 unless "sgemm_splitk"); a pure function, no device needed.  NULL when nothing
+ * is launched (M or N < 1) or an argument is invalid.  sgpu_sgemm_opt launches the unsplit
+ * member instead of "sgemm_splitk" on a stream being recorded that has no workspace yet.
+ * No counterpart in the reference (its sgemm_opt is one kernel). */
+const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits);
 /* The sgemm_opt256 member alone (any shape; masked loads on edge tiles).  No
  * counterpart in the reference: an added member of the same family, with the same
  * (A, B, C, M, N, K) symbol arguments, for hosts that launch members by name. */

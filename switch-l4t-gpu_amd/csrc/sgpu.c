@@ -674,43 +674,42 @@ int sgpu_sgemm_splitk_noalloc(const float *A, const float *B, float *C, int M, i
     return splitk_launch(&g_dev[dev], A, B, C, M, N, K, S, ws, cnt, stream);
 }
 
-/* When sgpu_sgemm_opt splits K (measured, warm, srand inputs: 512^3 13.0 -> 9.9 us at S = 4,
- * 1023x1025x997 41.6 -> 33.3 us at S = 4; 1024^3 and larger gain nothing): with fewer 64x64
- * tiles than half the CUs, into about CUs / tiles splits (a power of two, at most 8); with a K
- * tail (every unsplit tile on the masked pipeline) and at most two tiles per CU, into 4 (the
- * splits before the tail run the dwordx4 pipeline).  Splits keep at least two slices.
+/* When sgpu_sgemm_opt splits K, and how many ways: the count (1 = unsplit, up to 8; 16 for
+ * a problem of at most half the CUs' tiles whose splits still hold 512 of K each) with the
+ * least modelled time, over problems of at most two rounds of 64x64 tiles.  Each CU runs
+ * ceil(tiles * S / CUs) units of `per` = ceil(nk / S) 32-deep k-slices; the model charges,
+ * in hundredths of a first-round slice:
+ *   100 per slice of the first round,
+ *    89 per slice of each further round (co-resident blocks overlap their latencies),
+ *    36 per first-round slice on the masked pipeline (with a K tail: the unsplit tile's
+ *       slices, or the last split's),
+ *   220 per round of split hand-offs (partials written, the last split's sum).
+ * Fitted to graph-replayed timings of sgemm_tiled and sgemm_splitk S = 2..8 at 26 shapes of
+ * 100 to 512 tiles (640^2 to 2048x1024, K 997 to 4096): the pick's time is within 0.7% of
+ * the fastest measured on average and 4.1% at worst (e.g. 1088x1024x1024 S = 4 29.5 us vs
+ * 36.7 unsplit, 1200x1200x1024 S = 2 35.2 vs 42.6, 768x768x1000 S = 5 18.8 vs 27.6,
+ * 2048x1024x1000 unsplit 41.2 vs 47.5 at S = 4).  Every split keeps at least two slices.
  * Returns 1 for no split. */
 static int splitk_pick(int M, int N, int K, int cus) {
     const long long tiles = (long long)cdiv(M, SK_TILE) * cdiv(N, SK_TILE);
     const int nk = cdiv(K, SK_BK);
-    int S = 1;
-    if (tiles * 2 <= cus) {
-        /* up to 8 splits, 16 when each split still holds 512 of K (one or two tiles of a
-         * tall-K problem: 64x64x8192 20.0 vs 25.3 us at 8, 32x32x16384 33.3 vs 52.1) */
-        const long long r = cus / tiles;
-        const int cap = K / 16 >= 512 ? 16 : 8;
-        while (S < cap && S * 2 <= r) S *= 2;
-    } else if (K % SK_BK && tiles <= 2LL * cus) {
-        S = 4;
-    } else if (tiles <= cus) {
-        /* One round of tiles that half-fills to fills the CUs: split when it shortens the
-         * busiest CU's run of slices, ceil(tiles * S / CUs) * ceil(nk / S), by more than the
-         * hand-off costs (taken as 15%).  Measured, recorded graphs: 768x768x2048 30.0 us at
-         * S=3 vs 40.3 unsplit, 768^3 15.8 vs 17.5, 1024x768x1024 21.0 at S=4 vs 22.9; 896^3
-         * and 960^3, where no split shortens the run, stay unsplit. */
-        long long best = (long long)cdiv(nk, 1) * 100;
-        for (int s = 2; s <= 4; s++) {
-            const long long c = ((tiles * s + cus - 1) / cus) * (long long)cdiv(nk, s) * 115;
-            if (c < best) {
-                best = c;
-                S = s;
-            }
+    if (cus < 1 || tiles > 2LL * cus) return 1;
+    const int cap = tiles * 2 <= cus && K / 16 >= 512 ? 16 : 8;
+    const int tail = K % SK_BK != 0;
+    int best_s = 1;
+    long long best = 0;
+    for (int s = 1; s <= cap && s <= nk / 2; s++) {
+        const int S = sk_splits(K, s), per = cdiv(nk, S);
+        if (S != s || (S > 1 && !splitk_fits(M, N, S))) continue;   /* same split as a smaller s */
+        const long long rounds = (tiles * S + cus - 1) / cus;
+        const long long c = 100LL * per + 89LL * per * (rounds - 1) + (tail ? 36LL * per : 0) +
+                            (S > 1 ? 220LL * rounds : 0);
+        if (s == 1 || c < best) {
+            best = c;
+            best_s = S;
         }
     }
-    if (S > nk / 2) S = nk / 2;
-    if (S < 2) return 1;
-    S = sk_splits(K, S);
-    return splitk_fits(M, N, S) ? S : 1;
+    return best_s;
 }
 
 /* sgemm_small16 / sgemm_small32: one 16x16 / 32x32 tile of C per block, operands read through
@@ -740,13 +739,12 @@ int sgpu_sgemm_small(const float *A, const float *B, float *C, int M, int N, int
     return small_launch(d, tile, A, B, C, M, N, K, stream);
 }
 
-int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
-    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
-    if (M == 0 || N == 0) return SGPU_OK;
-    if (!C || (K > 0 && (!A || !B))) return SGPU_ERR_INVALID_ARG;
-    int rc;
-    devstate *d = cur(&rc);
-    if (!d) return rc;
+/* The launch sgpu_sgemm_opt makes for an M x N x K problem on `cus` CUs: PLAN_SMALL16 /
+ * PLAN_SMALL32, PLAN_SPLITK with *S splits (the unsplit member is launched instead when the
+ * stream has no workspace), or an index into g_sgemm_members. */
+enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3 };
+static int opt_plan(int M, int N, int K, int cus, int *S) {
+    *S = 1;
     /* Problems whose 16x16 (32x32) tiles fit the CUs in one round go to the small members
      * (measured in recorded graphs, srand inputs: 256^3 4.0 vs 7.7 us, 512^3 7.6 vs 9.7,
      * 256x256x2048 9.4 vs 13.7, 100x70x3000 11.3 vs 16.0, 1x4096x4096 23.6 vs 27.8); past
@@ -755,16 +753,39 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
      * column of tiles, and past K 4096 (1024 for 32x32) it always does. */
     if (small_fits(M, N, K)) {
         const long long t16 = (long long)cdiv(M, 16) * cdiv(N, 16), t32 = (long long)cdiv(M, 32) * cdiv(N, 32);
-        if (t16 <= d->cus && K <= 4096 && (K <= 2048 || t16 * 4 <= d->cus || M <= 16 || N <= 16))
-            return small_launch(d, 16, A, B, C, M, N, K, stream);
-        if (t32 <= d->cus && K <= 1024) return small_launch(d, 32, A, B, C, M, N, K, stream);
+        if (t16 <= cus && K <= 4096 && (K <= 2048 || t16 * 4 <= cus || M <= 16 || N <= 16)) return PLAN_SMALL16;
+        if (t32 <= cus && K <= 1024) return PLAN_SMALL32;
     }
-    const int S = K > 0 ? splitk_pick(M, N, K, d->cus) : 1;
+    if (K > 0 && (*S = splitk_pick(M, N, K, cus)) > 1) return PLAN_SPLITK;
+    *S = 1;
+    return sgemm_pick(M, N, cus);
+}
+const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits) {
+    if (M < 1 || N < 1 || K < 0 || cus < 1) return NULL;
+    int S;
+    const int p = opt_plan(M, N, K, cus, &S);
+    if (splits) *splits = S;
+    if (p == PLAN_SMALL16) return "sgemm_small16";
+    if (p == PLAN_SMALL32) return "sgemm_small32";
+    if (p == PLAN_SPLITK) return "sgemm_splitk";
+    return g_sgemm_members[p].name;
+}
+
+int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    if (!C || (K > 0 && (!A || !B))) return SGPU_ERR_INVALID_ARG;
+    int rc;
+    devstate *d = cur(&rc);
+    if (!d) return rc;
+    int S;
+    const int p = opt_plan(M, N, K, d->cus, &S);
+    if (p == PLAN_SMALL16 || p == PLAN_SMALL32) return small_launch(d, p == PLAN_SMALL16 ? 16 : 32, A, B, C, M, N, K, stream);
     float *ws;
     unsigned *cnt;
-    if (S > 1 && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
+    if (p == PLAN_SPLITK && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
         return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
-    const int m = sgemm_pick(M, N, d->cus);
+    const int m = p >= 0 ? p : sgemm_pick(M, N, d->cus);
     return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }
 int sgpu_sgemm_naive(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {

@@ -104,12 +104,14 @@ DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 
                    (2048, 4096, 64), (2048, 4096, 96), (256, 256, 64), (192, 320, 40),
                    (4096, 4096, 96), (4096, 4352, 64), (4352, 4096, 160),
                    # sgpu_sgemm_opt's small-member and split-K regimes: one row or column of
-                   # tiles (the 16x16 member at 4096 wide, split-K at 8192), and the largest
-                   # K-tailed problem the 4-way split takes (484 tiles, 31 MB of partials)
+                   # tiles (the 16x16 member at 4096 wide, split-K at 8192), two rounds of
+                   # K-tailed 64x64 tiles left unsplit, and a 7-way split of 289 tiles (2023
+                   # partial tiles, 31.6 MB: near the workspace's 2048)
                    (1, 4096, 4096), (4096, 1, 2048), (1, 8192, 4096), (8192, 1, 2048), (1408, 1408, 997),
+                   (1087, 1085, 2000),
                    # the small members' K bounds and the 16-way split of one tall-K tile
                    (256, 256, 4096), (100, 70, 3000), (16, 4096, 4096), (64, 64, 8192),
-                   # one round of 64x64 tiles split 3 and 4 ways
+                   # one round of 64x64 tiles split 5 and 4 ways
                    (768, 768, 2048), (1024, 768, 1024)]
 
 
@@ -122,6 +124,43 @@ def test_tile_paths_integer_exact(gpu, fn, M, N, K):
     B = rng.integers(-2, 3, (K, N)).astype(np.float32)
     C = run_sgemm(gpu, fn, A, B, M, N, K)
     assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+
+
+# sgpu_sgemm_opt launches what sgpu_sgemm_opt_plan names for this device: on float inputs its
+# C equals the named launch's bit for bit.  A split sums its partials in split order, so a
+# split C differs from the unsplit member's, and a different split count would differ too.
+PLAN_SHAPES = [(1023, 1025, 997), (768, 768, 2048), (1000, 1000, 1000), (1088, 1024, 1024),
+               (2048, 1024, 1000), (640, 640, 4096), (64, 64, 8192), (256, 256, 256), (512, 512, 512),
+               (1024, 1024, 1024), (2048, 2048, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", PLAN_SHAPES)
+def test_opt_launches_its_plan(gpu, M, N, K):
+    import ctypes as ct
+
+    cus = gpu.device_props().compute_units
+    S = ct.c_int()
+    name = gpu.lib().sgpu_sgemm_opt_plan(M, N, K, cus, ct.byref(S)).decode()
+    say(f"sgemm_opt plan {M}x{N}x{K} on {cus} CUs: {name} S={S.value}")
+    A, B = ref_inputs(M, N, K)
+    dA, dB = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B)
+    dC, dD = gpu.DeviceArray((M, N)), gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    dD.fill_bytes(0xFF)
+    gpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+    if name == "sgemm_splitk":
+        gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dD.ptr, M, N, K, S.value, None)
+    elif name in ("sgemm_small16", "sgemm_small32"):
+        gpu.call("sgpu_sgemm_small", dA.ptr, dB.ptr, dD.ptr, M, N, K, int(name[-2:]), None)
+    else:
+        gpu.call("sgpu_" + name, dA.ptr, dB.ptr, dD.ptr, M, N, K, None)
+    gpu.synchronize()
+    C = dC.to_host()
+    assert np.array_equal(C, dD.to_host())
+    if name == "sgemm_splitk":
+        gpu.call("sgpu_sgemm_tiled", dA.ptr, dB.ptr, dD.ptr, M, N, K, None)
+        gpu.synchronize()
+        assert not np.array_equal(C, dD.to_host())
 
 
 # Shapes whose edge tiles take the clamped-address path: an A tile (BM rows of K floats) or a
@@ -215,7 +254,7 @@ def test_splitk_recording_needs_a_workspace(gpu):
     reports SGPU_ERR_NO_WORKSPACE and sgpu_sgemm_opt records its unsplit member; after one
     split launch outside recording, the stream's workspace is recorded and every replay is
     exact."""
-    M, N, K = 768, 768, 2048                                # sgpu_sgemm_opt splits this one 3 ways
+    M, N, K = 768, 768, 2048                                # sgpu_sgemm_opt splits this one 5 ways
     rng = np.random.default_rng(19)
     A = rng.integers(-2, 3, (M, K)).astype(np.float32)
     B = rng.integers(-2, 3, (K, N)).astype(np.float32)

@@ -1,0 +1,100 @@
+"""sgpu_sgemm_opt's launch plan (sgpu_sgemm_opt_plan), host logic only: no device is touched.
+
+The pinned table holds the picks at MI355X's 256 CUs.  The split counts there come from the
+library's cost model, whose measured basis is in the comment above splitk_pick in
+csrc/sgpu.c, so a change to the model or a rule shows up here.  The invariants are what every
+plan must satisfy at any CU count.  One of them, the split-K workspace bound, is what
+sgpu_sgemm_splitk itself enforces."""
+import ctypes as ct
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "switch-l4t-gpu_amd"))
+
+import sgpu  # noqa: E402
+
+PINNED_256 = [
+    # large problems: the member whose busiest CU has the least work
+    (4096, 4096, 4096, "sgemm_opt256", 1),
+    (8192, 8192, 8192, "sgemm_opt256", 1),
+    (2048, 2048, 2048, "sgemm_tiled4", 1),
+    (3072, 3072, 3072, "sgemm_tiled", 1),
+    (4097, 4097, 4097, "sgemm_tiled", 1),
+    # one round of 64x64 tiles, K a multiple of 32: unsplit wins at 1024^3, splits elsewhere
+    (1024, 1024, 1024, "sgemm_tiled", 1),
+    (768, 768, 2048, "sgemm_splitk", 5),
+    (1024, 768, 1024, "sgemm_splitk", 4),
+    (1088, 1024, 1024, "sgemm_splitk", 4),
+    # K tails
+    (1023, 1025, 997, "sgemm_splitk", 4),
+    (1000, 1000, 1000, "sgemm_splitk", 2),
+    (640, 640, 1000, "sgemm_splitk", 5),
+    (1087, 1085, 2000, "sgemm_splitk", 7),
+    (1408, 1408, 997, "sgemm_tiled", 1),
+    (2048, 1024, 1000, "sgemm_tiled", 1),
+    # few tiles: tall K splits up to 16 ways, one row or column of tiles
+    (64, 64, 8192, "sgemm_splitk", 16),
+    (32, 32, 16384, "sgemm_splitk", 16),
+    (256, 256, 4096, "sgemm_splitk", 8),
+    (8192, 1, 2048, "sgemm_splitk", 2),
+    (1, 8192, 4096, "sgemm_splitk", 4),
+    # the small members
+    (256, 256, 256, "sgemm_small16", 1),
+    (512, 512, 512, "sgemm_small32", 1),
+    (1, 4096, 4096, "sgemm_small16", 1),
+    (16, 4096, 4096, "sgemm_small16", 1),
+    (100, 70, 3000, "sgemm_small16", 1),
+]
+
+
+def plan(M, N, K, cus):
+    s = ct.c_int(-1)
+    name = sgpu.lib().sgpu_sgemm_opt_plan(M, N, K, cus, ct.byref(s))
+    return (name.decode() if name else None), s.value
+
+
+@pytest.mark.parametrize("M,N,K,name,S", PINNED_256)
+def test_plan_pinned_at_256_cus(M, N, K, name, S):
+    assert plan(M, N, K, 256) == (name, S)
+
+
+def cdiv(a, b):
+    return -(-a // b)
+
+
+@pytest.mark.parametrize("cus", [1, 80, 104, 256, 304])
+def test_plan_invariants(cus):
+    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled"}
+    for M in (1, 17, 64, 300, 1023, 2048):
+        for N in (1, 64, 511, 1025, 4096):
+            for K in (0, 1, 31, 64, 997, 2048, 8192):
+                name, S = plan(M, N, K, cus)
+                tiles = cdiv(M, 64) * cdiv(N, 64)
+                nk = cdiv(K, 32)
+                if name == "sgemm_splitk":
+                    assert 2 <= S <= 16 and K > 0
+                    per = cdiv(nk, S)
+                    assert cdiv(nk, per) == S            # S is already the reduced split count
+                    assert per >= 2                       # every split holds two slices or more
+                    assert S * tiles * 4096 <= 8 << 20    # the 32 MB workspace
+                    assert tiles <= 2 * cus
+                    assert S <= 8 or (tiles * 2 <= cus and K // 16 >= 512)
+                else:
+                    assert S == 1
+                    if name == "sgemm_small16":
+                        assert cdiv(M, 16) * cdiv(N, 16) <= cus and K <= 4096
+                    elif name == "sgemm_small32":
+                        assert cdiv(M, 32) * cdiv(N, 32) <= cus and K <= 1024
+                    else:
+                        assert name in members
+
+
+def test_plan_rejects():
+    assert plan(0, 4, 4, 256) == (None, -1)
+    assert plan(4, 0, 4, 256) == (None, -1)
+    assert plan(4, 4, -1, 256) == (None, -1)
+    assert plan(4, 4, 4, 0) == (None, -1)
+    assert sgpu.lib().sgpu_sgemm_opt_plan(64, 64, 64, 256, None) is not None
