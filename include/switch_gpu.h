@@ -277,6 +277,11 @@ void sgpu_gpt2_destroy(sgpu_gpt2 *engine);
 /* gpu_forward (gpt2_engine.c:174-264): fused != 0 takes the --fused path (gemv_warp_b),
  * otherwise gemv_warp + add_bias.  Logits (V floats) copied to logits_host if want_logits. */
 int sgpu_gpt2_forward(sgpu_gpt2 *engine, int token, int pos, int want_logits, float *logits_host, int fused);
+/* The reference launch sequence (fused = its --fused variant), whatever the engine's path,
+ * copying the residual stream after each layer to trace_host (NL x C floats): the per-layer
+ * trace of the reference's self-test (gpt2_engine.c:478-494).  Logits to logits_host when it
+ * is not NULL.  Synchronous; the KV cache gains `pos` as with sgpu_gpt2_forward. */
+int sgpu_gpt2_forward_trace(sgpu_gpt2 *engine, int token, int pos, float *logits_host, float *trace_host, int fused);
 /* gpu_prefill (gpt2_engine.c:269-326): all T prompt positions through the layers with the
  * weight-stationary gemv_multi; fills cache positions 0..T-1; logits of the last row. */
 int sgpu_gpt2_prefill(sgpu_gpt2 *engine, const int *ids, int T, float *logits_host);
@@ -324,6 +329,12 @@ void sgpu_qwen_destroy(sgpu_qwen *engine);
  * If want_logits, the V logits are copied to host `logits_host` (may be NULL to leave them on
  * the device).  Synchronous when logits are requested, asynchronous otherwise. */
 int sgpu_qwen_forward(sgpu_qwen *engine, int token, int pos, int want_logits, float *logits_host);
+/* sgpu_qwen_forward on the REFERENCE launch sequence, whatever the engine's path, copying the
+ * residual stream after each layer to trace_host (NL x C floats): the layer trace the
+ * reference's self-test compares against its CPU forward (cpu_forward's trace argument,
+ * qwen_engine.c:355; gpt2_engine.c:478-494).  Logits to logits_host when it is not NULL.
+ * Synchronous.  The KV cache gains `pos` as with sgpu_qwen_forward. */
+int sgpu_qwen_forward_trace(sgpu_qwen *engine, int token, int pos, float *logits_host, float *trace_host);
 /* Execution paths of sgpu_qwen_forward / sgpu_qwen_generate.  All compute the same
  * function (checked against the CPU golden); they differ in launch structure:
  *  REFERENCE -- the reference's per-layer sequence above, 14 launches + 2 copies per layer

@@ -287,14 +287,11 @@ static int forward_fused(sgpu_gpt2 *e, int token, int pos, int want_logits, floa
     return sgpu_stream_synchronize((void *)e->stream);
 }
 
-int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host, int fused) {
-    if (!e) return SGPU_ERR_INVALID_ARG;
-    if (e->path != SGPU_GPT2_PATH_REFERENCE) {
-        if (token < 0 || token >= e->cfg.V || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
-        return forward_fused(e, token, pos, want_logits, logits_host);
-    }
+/* gpu_forward (gpt2_engine.c:174-264), `fused` = its --fused variant.  With trace_host, the
+ * residual after each layer is copied there (NL x C floats, gpu_forward's trace argument). */
+static int forward_reference(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host, int fused,
+                             float *trace_host) {
     const sgpu_gpt2_cfg *c = &e->cfg;
-    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
     const int C = c->C, FC = c->FC, T = pos + 1;
     const float eps = c->eps, scale = 0.125f;   /* 1/sqrt(64), gpt2_engine.c:75 */
     void *s = (void *)e->stream;
@@ -319,9 +316,28 @@ int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *
         TRY(sgpu_gelu(e->fc, e->fc, FC, s));
         TRY(proj(b + e->L.projw, e->fc, b + e->L.projb, e->y, FC, C, fused, s));
         TRY(sgpu_add2(e->x, e->y, e->x, C, s));
+        if (trace_host) {
+            hipError_t he = hipMemcpyAsync(trace_host + (size_t)l * C, e->x, (size_t)C * 4, hipMemcpyDeviceToHost,
+                                           e->stream);
+            if (he != hipSuccess) return (int)he;
+        }
     }
+    if (trace_host) TRY(sgpu_stream_synchronize(s));
 #undef TRY
     return want_logits ? logits_out(e, e->x, logits_host) : SGPU_OK;
+}
+
+int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host, int fused) {
+    if (!e) return SGPU_ERR_INVALID_ARG;
+    if (token < 0 || token >= e->cfg.V || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
+    if (e->path != SGPU_GPT2_PATH_REFERENCE) return forward_fused(e, token, pos, want_logits, logits_host);
+    return forward_reference(e, token, pos, want_logits, logits_host, fused, NULL);
+}
+
+int sgpu_gpt2_forward_trace(sgpu_gpt2 *e, int token, int pos, float *logits_host, float *trace_host, int fused) {
+    if (!e || !trace_host) return SGPU_ERR_INVALID_ARG;
+    if (token < 0 || token >= e->cfg.V || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
+    return forward_reference(e, token, pos, logits_host != NULL, logits_host, fused, trace_host);
 }
 
 /* gpu_prefill's layer loop: all T prompt rows through each layer, cache positions 0..T-1

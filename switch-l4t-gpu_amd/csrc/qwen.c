@@ -249,8 +249,11 @@ fail:
 
 const float *sgpu_qwen_device_logits(const sgpu_qwen *e) { return e ? e->d_logits : NULL; }
 
-/* The reference per-layer launch sequence (gpu_forward, qwen_engine.c:205-269). */
-static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host) {
+/* The reference per-layer launch sequence (gpu_forward, qwen_engine.c:205-269).  With
+ * trace_host, the residual after each layer is copied there (NL x C floats, the layer
+ * trace of cpu_forward, qwen_engine.c:355). */
+static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host,
+                             float *trace_host) {
     const sgpu_qwen_cfg *c = &e->cfg;
     const int C = c->C, NH = c->NH, NKV = c->NKV, HD = c->HD, FC = c->FC;
     const int KVD = e->L.kvd, QKVD = e->L.qkvd, Tp = pos + 1;
@@ -277,7 +280,13 @@ static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, 
         TRY(sgpu_swiglu(e->d_gate, e->d_gate + FC, e->d_down, FC, s));
         TRY(sgpu_gemv_h(e->d_downw[l], e->d_down, NULL, e->d_y, FC, C, s));
         TRY(sgpu_add2(e->d_x, e->d_y, e->d_x, C, s));
+        if (trace_host) {
+            hipError_t he = hipMemcpyAsync(trace_host + (size_t)l * C, e->d_x, (size_t)C * 4, hipMemcpyDeviceToHost,
+                                           e->stream);
+            if (he != hipSuccess) return (int)he;
+        }
     }
+    if (trace_host) TRY(sgpu_stream_synchronize(s));
     if (!want_logits) return SGPU_OK;
     TRY(sgpu_rmsnorm(e->d_x, e->d_lnfw, e->d_x2, C, eps, 1, s));
     TRY(sgpu_gemv_h(e->d_emb, e->d_x2, NULL, e->d_logits, C, c->V, s));
@@ -383,12 +392,19 @@ int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *
     if (!e) return SGPU_ERR_INVALID_ARG;
     const sgpu_qwen_cfg *c = &e->cfg;
     if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
-    if (e->path == SGPU_QWEN_PATH_REFERENCE) return forward_reference(e, token, pos, want_logits, logits_host);
+    if (e->path == SGPU_QWEN_PATH_REFERENCE) return forward_reference(e, token, pos, want_logits, logits_host, NULL);
     int rc = sgpu_internal_dec_embed(e->d_emb, token, pos, e->d_x, c->C, e->d_step, (void *)e->stream);
     if (!rc) rc = run_layers(e);
     if (rc || !want_logits) return rc;
     if ((rc = lm_head(e))) return rc;
     return logits_to_host(e, logits_host);
+}
+
+int sgpu_qwen_forward_trace(sgpu_qwen *e, int token, int pos, float *logits_host, float *trace_host) {
+    if (!e || !trace_host) return SGPU_ERR_INVALID_ARG;
+    const sgpu_qwen_cfg *c = &e->cfg;
+    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
+    return forward_reference(e, token, pos, logits_host != NULL, logits_host, trace_host);
 }
 
 /* ---- batched prompt prefill: the prompt's rows go through each layer together, so each
@@ -478,14 +494,14 @@ int sgpu_qwen_generate(sgpu_qwen *e, const int *prompt, int T, int n_gen, int *o
     if (e->path == SGPU_QWEN_PATH_REFERENCE) {       /* host-driven loop, the reference's own */
         float *logits = malloc(sizeof(float) * (size_t)c->V);
         if (!logits) return SGPU_ERR_HOST_ALLOC;
-        for (int p = 0; p < T && !(rc = forward_reference(e, prompt[p], p, p == T - 1, logits)); p++) {
+        for (int p = 0; p < T && !(rc = forward_reference(e, prompt[p], p, p == T - 1, logits, NULL)); p++) {
         }
         for (int g = 0; !rc && g <= n_gen; g++) {
             int b = 0;
             for (int i = 1; i < c->V; i++)
                 if (logits[i] > logits[b]) b = i;
             out_tokens[g] = b;
-            if (g < n_gen) rc = forward_reference(e, b, T + g, 1, logits);
+            if (g < n_gen) rc = forward_reference(e, b, T + g, 1, logits, NULL);
         }
         free(logits);
         return rc;

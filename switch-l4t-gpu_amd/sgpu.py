@@ -112,6 +112,7 @@ _SIGS = {
     "sgpu_gpt2_create": (_I, [ct.POINTER(_P), ct.POINTER(Gpt2Cfg), _P]),
     "sgpu_gpt2_destroy": (None, [_P]),
     "sgpu_gpt2_forward": (_I, [_P, _I, _I, _I, _P, _I]),
+    "sgpu_gpt2_forward_trace": (_I, [_P, _I, _I, _P, _P, _I]),
     "sgpu_gpt2_prefill": (_I, [_P, _P, _I, _P]),
     "sgpu_gpt2_set_path": (_I, [_P, _I]),
     "sgpu_gpt2_generate": (_I, [_P, _P, _I, _I, _P]),
@@ -121,6 +122,7 @@ _SIGS = {
     "sgpu_qwen_create": (_I, [ct.POINTER(_P), ct.POINTER(QwenCfg), _P]),
     "sgpu_qwen_destroy": (None, [_P]),
     "sgpu_qwen_forward": (_I, [_P, _I, _I, _I, _P]),
+    "sgpu_qwen_forward_trace": (_I, [_P, _I, _I, _P, _P]),
     "sgpu_qwen_device_logits": (_P, [_P]),
     "sgpu_qwen_set_path": (_I, [_P, _I]),
     "sgpu_qwen_generate": (_I, [_P, _P, _I, _I, _P]),
@@ -404,6 +406,12 @@ class QwenEngine:
              self.logits.ctypes.data if want_logits else None)
         return self.logits if want_logits else None
 
+    def forward_trace(self, token: int, pos: int):
+        """The reference launch sequence for one position: (logits, residual after each layer)."""
+        trace = np.empty((self.cfg.NL, self.cfg.C), np.float32)
+        call("sgpu_qwen_forward_trace", self.h, token, pos, self.logits.ctypes.data, trace.ctypes.data)
+        return self.logits, trace
+
     def prefill(self, ids) -> np.ndarray:
         """Positions 0..len(ids)-1 in one batched pass; logits of the last row."""
         a = np.ascontiguousarray(ids, np.int32)
@@ -467,6 +475,12 @@ class Gpt2Engine:
         call("sgpu_gpt2_forward", self.h, token, pos, int(want_logits),
              self.logits.ctypes.data if want_logits else None, int(fused))
         return self.logits if want_logits else None
+
+    def forward_trace(self, token: int, pos: int, fused: bool = False):
+        """The reference launch sequence for one position: (logits, residual after each layer)."""
+        trace = np.empty((self.cfg.NL, self.cfg.C), np.float32)
+        call("sgpu_gpt2_forward_trace", self.h, token, pos, self.logits.ctypes.data, trace.ctypes.data, int(fused))
+        return self.logits, trace
 
     def prefill(self, ids):
         a = np.ascontiguousarray(ids, np.int32)

@@ -341,3 +341,66 @@ def test_engine_cli_json(gpu):
         runs[" ".join(extra)] = d["ids"]
     # the device-side greedy loop emits the same ids as the host loop (no EOT in 5 steps)
     assert runs["--path graph"] == runs[""][:len(runs["--path graph"])]
+
+
+# ---- the CLI's own self-test (--selftest / --debug, gpt2_engine.c:474-535) ----
+TRACE_RE = r"trace p0 L(\d+): max\|d\|=([0-9.]+) \(\|gpu\|~([0-9.]+)\)"
+
+
+def check_selftest_output(text, NL):
+    import re
+
+    traces = re.findall(TRACE_RE, text)
+    assert [int(t[0]) for t in traces] == list(range(NL)), text[-2000:]
+    for layer, d, g in traces:
+        assert float(d) <= 1e-4 * max(float(g), 1.0), (layer, d, g)
+    assert "SELFTEST: PASS" in text and "MATCH" in text, text[-2000:]
+    assert text.count("top-5 ids:") == 2
+
+
+@pytest.mark.parametrize("extra", [[], ["--fused"], ["--batch-prefill"], ["--path", "graph"]])
+def test_cli_selftest(gpu, extra, tmp_path):
+    """bin/gpt2_engine --selftest 4 on the full random-init model (fp32 weights): the per-layer
+    residual trace at position 0 and the logits at position 3 against the program's own serial
+    CPU forward, on the chosen launch form, then a normal run."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "gpt2_engine")
+    say(f"gpt2_engine --selftest 4 {' '.join(extra)}")
+    out = subprocess.run([exe, "--random", "3", "--selftest", "4", "--gen", "4"] + extra,
+                         capture_output=True, text=True, timeout=600, cwd=tmp_path)
+    assert out.returncode == 0, out.stderr[-2000:]
+    check_selftest_output(out.stdout, 12)
+    assert ("[batched]" in out.stdout) == ("--batch-prefill" in extra)
+    assert "ENGINE_DONE" in out.stdout
+
+
+def test_cli_selftest_debug(gpu, tmp_path):
+    """--debug adds the CPU forward's layer-0 stage lines and writes both layer traces."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "gpt2_engine")
+    say("gpt2_engine --selftest 2 --debug")
+    out = subprocess.run([exe, "--random", "4", "--selftest", "2", "--debug", "--gen", "1"],
+                         capture_output=True, text=True, timeout=600, cwd=tmp_path)
+    assert out.returncode == 0, out.stderr[-2000:]
+    check_selftest_output(out.stdout, 12)
+    for tag in ("embed", "ln1", "qkv", "ao", "res1", "ln2", "fc", "gelu", "proj", "res2"):
+        assert f"c.{tag}" in out.stdout
+    g = np.fromfile(tmp_path / "trace_g.bin", np.float32)
+    c = np.fromfile(tmp_path / "trace_c.bin", np.float32)
+    assert g.size == c.size == 12 * 768
+    assert np.abs(g - c).max() <= 1e-4 * max(np.abs(g).max(), 1.0)
+
+
+def test_forward_trace_is_the_reference_forward(gpu):
+    """sgpu_gpt2_forward_trace computes what the reference path computes, bit for bit (plain
+    and --fused launch forms), on an engine of any path."""
+    c = gpu.gpt2_cfg(V=1000, NL=2, CTX=64)
+    w = gpu.gpt2_random_weights(c, seed=21)
+    ref = gpu.Gpt2Engine(c, w, gpu.GPT2_PATH_REFERENCE)
+    tr_eng = gpu.Gpt2Engine(c, w, gpu.GPT2_PATH_GRAPH)
+    for fused in (False, True):
+        for p, t in enumerate([3, 999, 42, 7]):
+            want = ref.forward(t, p, fused=fused).copy()
+            got, trace = tr_eng.forward_trace(t, p, fused=fused)
+            assert np.array_equal(got, want), (fused, p)
+            assert trace.shape == (2, 768) and np.all(np.isfinite(trace))
+    ref.close()
+    tr_eng.close()

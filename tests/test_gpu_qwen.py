@@ -458,3 +458,66 @@ def test_engine_serve_protocol(gpu):
         stop = next((i for i, t in enumerate(want) if t in (151643, 151645)), None)
         assert cont == (want if stop is None else want[:stop + 1]), (cont, want)
     eng.close()
+
+
+# ---- the CLI's own self-test (--selftest / --debug, qwen_engine.c:446-521) ----
+TRACE_RE = r"trace p0 L(\d+): max\|d\|=([0-9.]+) \(\|gpu\|~([0-9.]+)\)"
+
+
+def check_selftest_output(text, NL):
+    import re
+
+    traces = re.findall(TRACE_RE, text)
+    assert [int(t[0]) for t in traces] == list(range(NL)), text[-2000:]
+    for layer, d, g in traces:
+        assert float(d) <= 1e-3 * max(float(g), 1.0), (layer, d, g)
+    assert "SELFTEST: PASS" in text and "argmax" in text and "MATCH" in text, text[-2000:]
+    assert text.count("top-5 ids:") == 2
+
+
+@pytest.mark.parametrize("path", ["reference", "graph"])
+def test_cli_selftest(gpu, path, tmp_path):
+    """bin/qwen_engine --selftest 3 on the full random-init model: the per-layer residual trace at
+    position 0 and the logits at position 2 against the program's own serial CPU forward, then
+    priming continues from position 3 and generation runs to the end."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
+    say(f"qwen_engine --selftest 3 --path {path}")
+    out = subprocess.run([exe, "--random", "2024", "--selftest", "3", "--gen", "4", "--path", path],
+                         capture_output=True, text=True, timeout=600, cwd=tmp_path)
+    assert out.returncode == 0, out.stderr[-2000:]
+    check_selftest_output(out.stdout, 24)
+    assert "positions 0..2 by the self-test" in out.stdout and "ENGINE_DONE" in out.stdout
+    assert not (tmp_path / "trace_g.bin").exists()
+
+
+def test_cli_selftest_debug(gpu, tmp_path):
+    """--debug adds the CPU forward's layer-0 stage lines and writes both layer traces."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
+    say("qwen_engine --selftest 1 --debug")
+    out = subprocess.run([exe, "--random", "7", "--selftest", "1", "--debug", "--gen", "1"],
+                         capture_output=True, text=True, timeout=600, cwd=tmp_path)
+    assert out.returncode == 0, out.stderr[-2000:]
+    check_selftest_output(out.stdout, 24)
+    for tag in ("embed", "ln1", "qkv", "ao", "res1"):
+        assert f"c.{tag}" in out.stdout
+    g = np.fromfile(tmp_path / "trace_g.bin", np.float32)
+    c = np.fromfile(tmp_path / "trace_c.bin", np.float32)
+    assert g.size == c.size == 24 * 896
+    assert np.abs(g - c).max() <= 1e-3 * max(np.abs(g).max(), 1.0)
+
+
+def test_forward_trace_is_the_reference_forward(gpu):
+    """sgpu_qwen_forward_trace computes what the reference path computes, bit for bit, on an
+    engine of any path, and its last layer's trace is the residual the logits come from."""
+    c = gpu.qwen_cfg(V=512, C=128, NL=3, NH=4, NKV=2, HD=32, FC=256, CTX=64)
+    blob = gpu.qwen_random_blob(c, seed=11, std=0.15)
+    ref = gpu.QwenEngine(c, blob, gpu.QWEN_PATH_REFERENCE)
+    tr_eng = gpu.QwenEngine(c, blob, gpu.QWEN_PATH_GRAPH)
+    ids = [5, 77, 301, 2, 9]
+    for p, t in enumerate(ids):
+        want = ref.forward(t, p).copy()
+        got, trace = tr_eng.forward_trace(t, p)
+        assert np.array_equal(got, want), p
+        assert trace.shape == (3, 128) and np.all(np.isfinite(trace))
+    ref.close()
+    tr_eng.close()
