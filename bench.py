@@ -502,14 +502,19 @@ def pmc_probe():
     W = sgpu.f32_to_f16(sgpu.gen_normal(N * K, 42, 0.0, 0.02)[0])
     dW, dx, dy = sgpu.DeviceArray.from_host(W), sgpu.DeviceArray(K), sgpu.DeviceArray(N)
     dx.fill_bytes(0)
-    sgpu.synchronize()
-    sgpu.call("sgpu_gemv_h", dW.ptr, dx.ptr, None, dy.ptr, K, N, None)
-    sgpu.synchronize()
     dxh = sgpu.DeviceArray(K, np.uint16)
     dxh.fill_bytes(0)
+    # a 1 GiB read sweep before each GEMV evicts the 256 MB MALL, so neither reads the other's
+    # (or the upload's) lines from it
+    flush = sgpu.DeviceArray(1 << 28)
+    flush.fill_bytes(0)
+    fout = sgpu.DeviceArray(1 << 20)
     sgpu.synchronize()
-    sgpu.call("sgpu_gemv_hh", dW.ptr, dxh.ptr, None, dy.ptr, K, N, None)
-    sgpu.synchronize()
+    for fn, xv in (("sgpu_gemv_h", dx), ("sgpu_gemv_hh", dxh)):
+        sgpu.call("sgpu_membw_read4", flush.ptr, fout.ptr, (1 << 28) // 4, 1, None, None)
+        sgpu.synchronize()
+        sgpu.call(fn, dW.ptr, xv.ptr, None, dy.ptr, K, N, None)
+        sgpu.synchronize()
     print(json.dumps({"add2_read": 2 * 4 * n, "add2_write": 4 * n,
                       "sgemm_read_min": 2 * 4 * N4 * N4, "sgemm_write": 4 * N4 * N4,
                       "gemv_h_read": 2 * N * K + 4 * K, "gemv_h_write": 4 * N,
