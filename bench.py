@@ -190,12 +190,14 @@ def warm_for(launch, sync, min_launches, min_s):
     return n
 
 
-def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1):
+def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1, cpu=False):
     """sgpu_sgemm_opt over the SGEMM size sweep (square 256..4096 and the ragged 1023x1025x997),
     reference-generator inputs; HIP-event time per launch after a warm-up of at least `warm`
     launches and `warm_s` seconds, normwise error of sampled rows against a float64 product.
     graphs=False skips the recorded-graph timing (a kernel trace of graph replay is not taken
-    by the profiler)."""
+    by the profiler).  cpu=True adds, at the reference's own sizes (up to 1024, and the ragged
+    shape), the oracle's serial SGEMM on one thread -- the reference CPU golden's form
+    (gpu_workload.c:97-98) -- timed on the same inputs."""
     out = []
     cus = sgpu.device_props().compute_units
     for M, N, K in SWEEP_SHAPES:
@@ -211,6 +213,12 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1):
         rows = np.linspace(0, M - 1, 8).astype(int)
         ref = A.reshape(M, K)[rows].astype(np.float64) @ B.reshape(K, N).astype(np.float64)
         err = float(np.abs(C[rows] - ref).max() / np.abs(ref).max())
+        cpu_row = {}
+        if cpu and max(M, N, K) <= 1025:
+            t = time.perf_counter()
+            _oracle().sgemm_rows(A, B, M, N, K, 0, M, 1)
+            dt = time.perf_counter() - t
+            cpu_row = {"cpu_1thread_ms": round(dt * 1e3, 1), "cpu_1thread_gflops": round(2.0 * M * N * K / dt / 1e9, 3)}
         ev = sgpu.Events()
         warm_for(run, sgpu.synchronize, warm, warm_s)
         for _ in range(10):
@@ -221,7 +229,8 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1):
         ev.record_stop(None)
         us = ev.elapsed_ms() * 1e3 / reps
         if not graphs:
-            out.append({"M": M, "N": N, "K": K, "launch": launch, "us_host_loop": round(us, 2), "normwise_err": err})
+            out.append({"M": M, "N": N, "K": K, "launch": launch, "us_host_loop": round(us, 2), "normwise_err": err,
+                        **cpu_row})
             for d in (dA, dB, dC):
                 d.close()
             continue
@@ -247,17 +256,20 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1):
         st.close()
         tf = 2.0 * M * N * K / (us_g * 1e-6) / 1e12
         out.append({"M": M, "N": N, "K": K, "launch": launch, "us_in_graph": round(us_g, 2), "us_host_loop": round(us, 2),
-                    "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MATRIX_TFLOPS, 4), "normwise_err": err})
+                    "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MATRIX_TFLOPS, 4), "normwise_err": err,
+                    **cpu_row})
         for d in (dA, dB, dC):
             d.close()
     return out
 
 
-def bench_gemv_shapes(reps=50, warm=100):
+def bench_gemv_shapes(reps=50, warm=100, cpu=False):
     """The per-projection GEMV shapes of both decoders: GPT-2 fp32 through sgpu_gemv_warp_b
     (zero bias, the engine's call), Qwen fp16 through sgpu_gemv_h (fp32 x; the fused qkv shape
     with its bias) and through sgpu_gemv_hh (fp16 x, rows "fp16x").  Weights N(0, 0.02),
-    x N(0, 1); copies of W are rotated so consecutive launches read different memory."""
+    x N(0, 1); copies of W are rotated so consecutive launches read different memory.
+    cpu=True adds the oracle's serial GEMV of the same W and x on one thread (the reference
+    CPU goldens' form, gemv_test.c:85-90 and qwen_engine.c:276-284), best of 3."""
     out = []
     st = 7
     for wt, name, N, K in GEMV_SHAPES:
@@ -314,10 +326,25 @@ def bench_gemv_shapes(reps=50, warm=100):
         strm.close()
         algo = wbytes + (2.0 if wt == "fp16x" else 4.0) * K + 4.0 * N + (4.0 * N if dz is not None else 0.0)
         gbps = algo / (us_g * 1e-6) / 1e9
+        cpu_row = {}
+        if cpu:
+            og = _oracle()
+            if wt == "fp32":
+                fcpu = lambda: og.gemv(W, x, np.zeros(N, np.float32), K, N, 1)
+            elif wt == "fp16x":
+                fcpu = lambda: og.gemv_hh(W, xin, bias, K, N, 1)
+            else:
+                fcpu = lambda: og.gemv_h_fbias(W, x, bias, K, N, 1)
+            best = 1e9
+            for _ in range(3):
+                t = time.perf_counter()
+                fcpu()
+                best = min(best, time.perf_counter() - t)
+            cpu_row = {"cpu_1thread_us": round(best * 1e6, 1), "cpu_1thread_gbps": round(algo / best / 1e9, 3)}
         out.append({"shape": [N, K], "name": name, "weights": "fp16" if half else "fp32",
                     "x": "fp16" if wt == "fp16x" else "fp32", "us_in_graph": round(us_g, 3),
                     "us_host_loop": round(us, 3), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
-                    "rotated_mb": round(copies * wbytes / 1e6, 1), "normwise_err": err})
+                    "rotated_mb": round(copies * wbytes / 1e6, 1), "normwise_err": err, **cpu_row})
         for d in dWs + [dx, dy] + ([dz] if dz is not None else []):
             d.close()
         del dWs
@@ -588,9 +615,9 @@ def main():
     del gv["W"], gv["x"], gvh["W"], gvh["x"]
     sweep = gshapes = None
     if not args.no_sweep:
-        sweep = bench_sgemm_sweep()
+        sweep = bench_sgemm_sweep(cpu=not args.no_cpu)
         log("sgemm sweep (in-graph): " + ", ".join(f"{r['M']}x{r['N']}x{r['K']} {r['tflops']:.1f} TF" for r in sweep))
-        gshapes = bench_gemv_shapes()
+        gshapes = bench_gemv_shapes(cpu=not args.no_cpu)
         log("gemv shapes (in-graph): " + ", ".join(f"{r['name']} {r['us_in_graph']:.2f} us" for r in gshapes))
     dec = g2 = cpu_dec = None
     if not args.no_decode:
