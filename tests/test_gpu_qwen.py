@@ -126,6 +126,39 @@ def test_engine_small_teacher_forced(gpu, og, std, path):
     eng.close()
 
 
+def wo_offset(c, layer):
+    """Half-index of layer `layer`'s o-projection weights in the flat file (qwen_engine.c:61-75:
+    embedding, RoPE tables, then per layer in_ln, qkv W, qkv b, o W, ...)."""
+    qkv = c["C"] + 2 * c["NKV"] * c["HD"]
+    base = (c["V"] * c["C"] * 2 + 2 * c["CTX"] * (c["HD"] // 2) * 4) // 2
+    lstride = c["C"] + qkv * c["C"] + qkv + c["C"] * c["C"] + c["C"] + 2 * c["FC"] * c["C"] + c["C"] * c["FC"]
+    return base + layer * lstride + c["C"] + qkv * c["C"] + qkv
+
+
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_engine_exponent31_weights(gpu, og, path):
+    """fp16 codes with exponent 31 in the o projection (the reference's h2f decodes them to the
+    finite +-2^16(1+m/1024); the hardware conversion gives inf/NaN): every launch structure
+    matches the CPU golden, teacher-forced, including the fused attention + o projection."""
+    cfg = SMALL
+    blob = gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=23, std=0.15)
+    h = blob.view(np.uint16)
+    o = wo_offset(cfg, 0)
+    C, HD = cfg["C"], cfg["HD"]
+    for r, k, code in ((5, 0, 0x7C00), (5, HD + 3, 0xFC01), (C - 1, C - 1, 0x7C10), (17, 2 * HD, 0xFFFF)):
+        h[o + r * C + k] = code
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob, PATHS[path])
+    gold = og.QwenGolden(og.qwen_cfg(**cfg), blob, NT)
+    ids = [int(v) for v in np.random.default_rng(8).integers(0, cfg["V"], 12)]
+    for p, t in enumerate(ids):
+        got = eng.forward(t, p).copy()
+        want = gold.forward(t, p)
+        assert np.all(np.isfinite(want)) and np.all(np.isfinite(got)), p
+        scale = np.abs(want).max()
+        assert np.abs(got - want).max() <= 1e-4 * scale, (p, np.abs(got - want).max(), scale)
+    eng.close()
+
+
 # Long teacher-forced runs on the fused path, head dims 32 and 128: the attention kernel's
 # score and mix loops take several passes past 64 (32) positions per pass, past 256 positions
 # a head's cache is cut into chunks whose partials are combined, and past 7936 the chunk count
