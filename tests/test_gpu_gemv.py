@@ -319,3 +319,54 @@ def test_membw_read4_sums(gpu, groups, extra):
         seg = row[j:j + nthr]
         want[:seg.size] += seg
     assert np.array_equal(out, (iters * want).astype(np.float32))
+
+
+# ---- NaN / Inf inside the operands: IEEE propagation as the reference's serial loop has it ----
+def _nonfinite(rows, cols, K, seed):
+    """A (rows x K) with a NaN in row rows//2 and a 0 at [rows//2 + 1, K-1]; B (K x cols) with
+    +Inf at [K-1, cols//2] and -Inf at [0, cols//2]; and the product the reference's serial
+    fp32 loops give (gemv_test.c:85-90): the NaN row all NaN, in column cols//2
+    A[i,K-1]*Inf + A[i,0]*(-Inf) is NaN when a multiplier is 0 or the infinities' signs differ,
+    else that infinity; the rest the exact integer sum."""
+    rng = np.random.default_rng(seed)
+    A = rng.integers(-2, 3, (rows, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, cols)).astype(np.float32)
+    ia, kb, jb, iz = rows // 2, K - 1, cols // 2, (rows // 2 + 1) % rows
+    A[iz, kb] = 0.0
+    Af, Bf = A.copy(), B.copy()
+    A[ia, K // 3] = np.nan
+    B[kb, jb], B[0, jb] = np.inf, -np.inf
+    Bf[kb, jb] = Bf[0, jb] = 0.0
+    want = (Af.astype(np.float64) @ Bf.astype(np.float64)).astype(np.float32)
+    t1, t2 = np.sign(A[:, kb]), -np.sign(A[:, 0])
+    with np.errstate(invalid="ignore"):
+        want[:, jb] = np.where((t1 == 0) | (t2 == 0) | (t1 != t2), np.nan, t1 * np.inf)
+    want[ia, :] = np.nan
+    return A, B, want
+
+
+@pytest.mark.parametrize("N,K", [(2304, 768), (768, 3072), (1000, 997)])
+@pytest.mark.parametrize("fn,x_off", [("sgpu_gemv", 0), ("sgpu_gemv_warp_b", 0), ("sgpu_gemv_warp_b", 1)])
+def test_fp32_gemv_nonfinite_propagate(gpu, fn, x_off, N, K):
+    """NaN in a weight row and +-Inf in x come out of the team and the wave-per-row GEMVs
+    (x_off = 1: unaligned x) as IEEE arithmetic has them; the finite rows stay exact."""
+    say(f"gemv non-finite {fn} x_off={x_off} {N}x{K}")
+    W, xcol, want = _nonfinite(N, 1, K, N + K + x_off)
+    got = gemv_dev(gpu, fn, W, xcol[:, 0], None, K, N, x_off)
+    assert np.array_equal(got, want[:, 0], equal_nan=True)
+
+
+@pytest.mark.parametrize("K,N,T", [(768, 2304, 3), (768, 2304, 8), (768, 3072, 20), (3072, 768, 64), (997, 300, 5)])
+def test_gemv_multi_nonfinite_propagate(gpu, K, N, T):
+    """The batched GEMV (register, matrix-core, split and vector forms): a NaN weight row is NaN
+    for every token; +-Inf in one token's X row reaches only that token's outputs."""
+    say(f"gemv_multi non-finite K={K} N={N} T={T}")
+    W, XT, want = _nonfinite(N, T, K, K + N + T)
+    dW = gpu.DeviceArray.from_host(W)
+    dX = gpu.DeviceArray.from_host(np.ascontiguousarray(XT.T))
+    dY = gpu.DeviceArray((T, N))
+    for _ in range(2):
+        dY.fill_bytes(0xFF)
+        gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, None, dY.ptr, K, N, T, None)
+        gpu.synchronize()
+        assert np.array_equal(dY.to_host(), want.T, equal_nan=True)

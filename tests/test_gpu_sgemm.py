@@ -346,6 +346,56 @@ def test_operands_followed_by_nan_integer_exact(gpu, M, N, K, launcher, a_off):
         assert np.array_equal(dC.to_host(), want)
 
 
+NONFINITE_CASES = [(7, 300, 13), (100, 70, 3000), (130, 190, 65), (256, 256, 256), (1023, 1025, 997)]
+
+
+def nonfinite_operands(M, N, K, seed):
+    """Small integers plus: NaN at A[ia, ka]; +Inf at B[kb, jb] and -Inf at B[0, jb]; a zero
+    at A[iz, kb].  Returns A, B and the IEEE product the reference's serial fp32 loop
+    (gpu_workload.c:97-98) yields: row ia all NaN (NaN times anything); in column jb,
+    A[i,kb]*Inf + A[i,0]*(-Inf) is NaN when either multiplier is 0 (Inf * 0) or the two
+    infinities have opposite signs, else that infinity; everything else the exact integer sum."""
+    rng = np.random.default_rng(seed)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    ia, ka, kb, jb, iz = M // 2, K // 3, K - 1, N // 2, (M // 2 + 1) % M
+    A[iz, kb] = 0.0
+    Af, Bf = A.copy(), B.copy()
+    A[ia, ka] = np.nan
+    B[kb, jb], B[0, jb] = np.inf, -np.inf
+    Bf[kb, jb] = Bf[0, jb] = 0.0
+    want = (Af.astype(np.float64) @ Bf.astype(np.float64)).astype(np.float32)
+    t1 = np.sign(A[:, kb])                 # sign of A[i,kb] * +Inf (0: NaN)
+    t2 = -np.sign(A[:, 0])                 # sign of A[i,0] * -Inf (0: NaN)
+    with np.errstate(invalid="ignore"):
+        col = np.where((t1 == 0) | (t2 == 0) | (t1 != t2), np.nan, t1 * np.inf).astype(np.float32)
+    want[:, jb] = col
+    want[ia, :] = np.nan
+    return A, B, want
+
+
+@pytest.mark.parametrize("launcher", ["small16", "small32", "splitk4", "sgpu_sgemm_opt", "sgpu_sgemm_tiled",
+                                      "sgpu_sgemm_tiled4", "sgpu_sgemm_opt256"])
+@pytest.mark.parametrize("M,N,K", NONFINITE_CASES)
+def test_nonfinite_inputs_propagate(gpu, M, N, K, launcher):
+    """NaN and Inf inside A and B come out of every launch form as the reference's IEEE
+    fp32 arithmetic has them (no path zeroes, clamps or skips an in-bounds element), and the
+    finite elements stay exact."""
+    say(f"sgemm {launcher} non-finite {M}x{N}x{K}")
+    A, B, want = nonfinite_operands(M, N, K, M + 7 * N + 3 * K)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    if launcher.startswith("small"):
+        gpu.call("sgpu_sgemm_small", dA.ptr, dB.ptr, dC.ptr, M, N, K, int(launcher[5:]), None)
+    elif launcher == "splitk4":
+        gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, None)
+    else:
+        gpu.call(launcher, dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+    gpu.synchronize()
+    got = dC.to_host()
+    assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])
+
+
 @pytest.mark.parametrize("tile", [16, 32])
 def test_small_reference_generator_unaligned_and_k_zero(gpu, og, tile):
     """Reference-generator inputs within the normwise bar of the oracle with A one float past
