@@ -128,7 +128,9 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * or one row or column of tiles), else those whose 32x32 tiles do (K <= 1024) to
  * sgemm_small32; of the rest, problems of at most two rounds of 64x64 tiles go to
  * sgemm_splitk when a cost model of the busiest CU's k-slices, masked tail slices and split
- * hand-offs prefers a 2-8 way split (16 for a few tiles of tall K) to none. */
+ * hand-offs prefers a 2-8 way split (16 for a few tiles of tall K) to none -- except that
+ * problems of whole 64x64 tiles filling 3/4 to all of the CUs in one round, with K a
+ * multiple of 32 and at least 1024 (and 16-byte aligned A and B), go to sgemm_kwave. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
@@ -143,6 +145,12 @@ const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits);
  * counterpart in the reference: an added member of the same family, with the same
  * (A, B, C, M, N, K) symbol arguments, for hosts that launch members by name. */
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+/* The sgemm_kwave member: 64x64 tiles of C, each computed by a block of four waves that
+ * split K four ways, every wave accumulating the whole tile from its own LDS staging, the
+ * four partial tiles summed in wave order.  M and N multiples of 64, K a multiple of 32, A
+ * and B 16-byte aligned (SGPU_ERR_INVALID_ARG otherwise).  No counterpart in the reference:
+ * an added member of the family with the (A, B, C, M, N, K) symbol arguments. */
+int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 /* The sgemm_splitk member: 64x64 tiles with K split S ways (S >= 1; reduced so that every
  * split holds at least one 32-deep slice), each (tile, split) a block.  Every split writes its
  * partial tile to a library-owned workspace of the launch's stream and the last split of a

@@ -45,7 +45,7 @@ static const struct {
 /* Every kernel the launchers use: (module, symbol). */
 enum {
     K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_SMALL16, K_SGEMM_SMALL32,
-    K_SGEMM_NAIVE, K_MEMBW,
+    K_SGEMM_KWAVE, K_SGEMM_NAIVE, K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK, K_GEMV_MULTI_X8_64,
     K_GEMV_MULTI_X8_256,
     K_GEMV_H, K_GEMV_HH, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
@@ -59,7 +59,7 @@ static const struct {
 } g_kern[NKERN] = {
     {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
     {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_splitk"}, {MOD_SWITCH, "sgemm_small16"},
-    {MOD_SWITCH, "sgemm_small32"}, {MOD_SWITCH, "sgemm_naive"},
+    {MOD_SWITCH, "sgemm_small32"}, {MOD_SWITCH, "sgemm_kwave"}, {MOD_SWITCH, "sgemm_naive"},
     {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
@@ -497,6 +497,7 @@ static int sgemm_tile(const char *k, int *tn) {
     if (!strcmp(k, "sgemm_tiled4")) return *tn = 128, 128;
     if (!strcmp(k, "sgemm_opt")) return *tn = 256, 128;
     if (!strcmp(k, "sgemm_opt256")) return *tn = 256, 256;
+    if (!strcmp(k, "sgemm_kwave")) return *tn = 64, 64;
     return *tn = 0, 0;
 }
 
@@ -583,6 +584,15 @@ int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, in
 }
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     return sgemm_common(K_SGEMM_OPT256, "sgemm_opt256", A, B, C, M, N, K, stream);
+}
+/* sgemm_kwave's problems: M, N multiples of 64, K a multiple of 32 (the operands' 16-byte
+ * alignment is the launcher's check). */
+static int kwave_shape(int M, int N, int K) { return M > 0 && N > 0 && K > 0 && M % 64 == 0 && N % 64 == 0 && K % 32 == 0; }
+int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    if (!kwave_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B) & 15)) return SGPU_ERR_INVALID_ARG;
+    return sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
 }
 /* The optimised entry picks the member with the least work on its busiest CU: tiles are one
  * block each, dealt over the CUs, so a launch lasts about ceil(tiles / CUs) tile times, and a
@@ -742,7 +752,7 @@ int sgpu_sgemm_small(const float *A, const float *B, float *C, int M, int N, int
 /* The launch sgpu_sgemm_opt makes for an M x N x K problem on `cus` CUs: PLAN_SMALL16 /
  * PLAN_SMALL32, PLAN_SPLITK with *S splits (the unsplit member is launched instead when the
  * stream has no workspace), or an index into g_sgemm_members. */
-enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3 };
+enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3, PLAN_KWAVE = -4 };
 static int opt_plan(int M, int N, int K, int cus, int *S) {
     *S = 1;
     /* Problems whose 16x16 (32x32) tiles fit the CUs in one round go to the small members
@@ -756,6 +766,18 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
         if (t16 <= cus && K <= 4096 && (K <= 2048 || t16 * 4 <= cus || M <= 16 || N <= 16)) return PLAN_SMALL16;
         if (t32 <= cus && K <= 1024) return PLAN_SMALL32;
     }
+    /* Whole 64x64 tiles filling 3/4 to all of the CUs in one round, K a multiple of 32 and
+     * at least 1024: the 64x64 tile with K split over its four waves (no block-wide slice
+     * barrier in the k loop).  Recorded graphs, srand inputs, us: 1024^3 20.0 vs 20.8 for the
+     * 64x64 member; 1024x1024x2048 35.8 vs 38.2; 1024x1024x4096 66.6 vs 74.0 for the split
+     * pick (S = 2); 1024x1024x8192 128.6 vs 140.1 (S = 2); 768x1024x1024 19.9 vs 20.7
+     * (S = 4).  With fewer tiles the K splits across blocks win (512x1024x1024 15.4 at S = 2
+     * vs 19.7; 768x768x2048 28.0 at S = 5 vs 35.4), and at K = 512 the two 64x64 forms tie
+     * (1024x1024x512 12.2 vs 12.2). */
+    if (kwave_shape(M, N, K) && K >= 1024) {
+        const long long tiles = (long long)(M / 64) * (N / 64);
+        if (tiles <= cus && 4 * tiles >= 3LL * cus) return PLAN_KWAVE;
+    }
     if (K > 0 && (*S = splitk_pick(M, N, K, cus)) > 1) return PLAN_SPLITK;
     *S = 1;
     return sgemm_pick(M, N, cus);
@@ -768,6 +790,7 @@ const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits) {
     if (p == PLAN_SMALL16) return "sgemm_small16";
     if (p == PLAN_SMALL32) return "sgemm_small32";
     if (p == PLAN_SPLITK) return "sgemm_splitk";
+    if (p == PLAN_KWAVE) return "sgemm_kwave";
     return g_sgemm_members[p].name;
 }
 
@@ -785,6 +808,8 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     unsigned *cnt;
     if (p == PLAN_SPLITK && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
         return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
+    if (p == PLAN_KWAVE && !(((uintptr_t)A | (uintptr_t)B) & 15))          /* else: the 64x64 member */
+        return sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
     const int m = p >= 0 ? p : sgemm_pick(M, N, d->cus);
     return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }

@@ -7,8 +7,9 @@
 //   membw_read4                          : (const float4*buf, float*out, int n4, int iters)
 // plus sgemm_opt256, a larger-tile member with the same arguments, sgemm_splitk
 //   (A, B, C, M, N, K, int S, float* ws, unsigned* cnt), the 64x64 tile with K split S ways,
-// and sgemm_small16 / sgemm_small32 (same arguments as the reference members), one 16x16 /
-// 32x32 tile per block with the operands read straight into MFMA registers, no LDS staging.
+// sgemm_small16 / sgemm_small32 (same arguments as the reference members), one 16x16 /
+// 32x32 tile per block with the operands read straight into MFMA registers, no LDS staging,
+// and sgemm_kwave (same arguments), the 64x64 tile with K split over the block's waves.
 //
 // C = A*B, fp32, row-major (A: MxK stride K, B: KxN stride N, C: MxN stride N), overwrite
 // (alpha 1, beta 0).  Unlike the reference kernels, every shape is accepted: interior tiles
@@ -622,6 +623,163 @@ __device__ __forceinline__ void sgemm_small(const float* __restrict__ A, const f
     else sgemm_small_tiles<TS, U, false>(A, B, C, M, N, K, red);
 }
 
+// Lanes of one wave exchanging data through LDS: every LDS access of this wave before the
+// call happens before every access after it.
+__device__ __forceinline__ void kw_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// sgemm_kwave: a 64x64 tile of C per block of four waves, each wave computing the WHOLE tile
+// (2x2 blocks of 32x32 MFMA accumulators) over its own quarter of the 32-deep k-slices, in
+// its own double-buffered LDS staging.  No barrier is shared by the waves inside the k loop:
+// a wave's slice pipeline waits only for its own loads and LDS traffic, so one wave per SIMD
+// runs its MFMAs without the block-wide slice barrier the 64x64 member pays every 16 MFMAs
+// (here 64 MFMAs separate a wave's slice boundaries).  The four partial tiles are summed in
+// wave order through LDS at the end (deterministic).  Problems: M, N multiples of 64, K a
+// multiple of 32, A and B 16-byte aligned (any other shape is left to the other members:
+// the kernel returns without writing C).
+//   Staging per wave and slice: A rows 8q + lane/8, float4 lane%8 (m-major, pitch 36); B
+//   k-rows 4q + lane/16, float4 lane%16 (pitch 72); the MFMA operands are read in 8-deep
+//   groups exactly as the LDS-staged members read theirs (lane half h, step t -> k = 8g+4h+t).
+//   Inside a slice: group g's 16 MFMAs run while group g+1's operands are read; the next
+//   slice (already in registers) is stored to the other buffer during group 1 and the loads
+//   of the slice after it are issued during group 2; group 3 starts with a wave sync and reads
+//   the next slice's first group.  Memory instructions are dealt out one per MFMA.
+constexpr int KW_BK = 32, KW_PA = KW_BK + 4, KW_PB = 64 + 8;
+struct KwaveLds {
+    float As[2][64][KW_PA];
+    float Bs[2][KW_BK][KW_PB];
+};
+__device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, const float* __restrict__ B,
+                                                 float* __restrict__ C, int N, int K, int m0, int n0,
+                                                 KwaveLds& L, sgpu_f32x4* __restrict__ red) {
+    const int lane = sgpu_tid() & 63, wave = sgpu_tid() >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int nk = K / KW_BK;
+    const int s0 = wave * nk / 4, s1 = (wave + 1) * nk / 4;      // this wave's slices
+    const float* pa = A + (size_t)(m0 + (lane >> 3)) * K + 4 * (lane & 7);
+    const float* pb = B + (size_t)(lane >> 4) * N + n0 + 4 * (lane & 15);
+    const size_t astep = (size_t)8 * K, bstep = (size_t)4 * N;
+    sgpu_f32x4 ra[8], rb[8];
+    auto load = [&](int s) __attribute__((always_inline)) {
+        const float* a = pa + (size_t)s * KW_BK;
+        const float* b = pb + (size_t)s * KW_BK * N;
+#pragma unroll
+        for (int q = 0; q < 8; q++) ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a + q * astep);
+#pragma unroll
+        for (int q = 0; q < 8; q++) rb[q] = *reinterpret_cast<const sgpu_f32x4*>(b + q * bstep);
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            *reinterpret_cast<sgpu_f32x4*>(&L.As[buf][8 * q + (lane >> 3)][4 * (lane & 7)]) = ra[q];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            *reinterpret_cast<sgpu_f32x4*>(&L.Bs[buf][4 * q + (lane >> 4)][4 * (lane & 15)]) = rb[q];
+    };
+    sgpu_f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    sgpu_f32x4 a[2][2], b[2][2];                                  // [operand set][block]
+    auto read_group = [&](int buf, int g, auto set_c) __attribute__((always_inline)) {
+        constexpr int RS = decltype(set_c)::value;
+        const int kc = 8 * g + 4 * h;
+#pragma unroll
+        for (int i = 0; i < 2; i++) a[RS][i] = *reinterpret_cast<const sgpu_f32x4*>(&L.As[buf][i * 32 + l32][kc]);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) b[RS][j][t] = L.Bs[buf][kc + t][j * 32 + l32];
+    };
+    using Z = std::integral_constant<int, 0>;
+    using O = std::integral_constant<int, 1>;
+    // ST: this slice stores the next one (and reads its first group); LD: it loads slice s+2.
+    auto slice = [&](int s, auto st_c, auto ld_c) __attribute__((always_inline)) {
+        constexpr bool ST = decltype(st_c)::value, LD = decltype(ld_c)::value;
+        const int buf = (s - s0) & 1;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            if (g == 3 && ST) kw_wave_sync();                     // the next slice's stores are visible
+            __builtin_amdgcn_sched_barrier(0);
+            if (g + 1 < 4) {
+                if (g & 1) read_group(buf, g + 1, Z{});
+                else read_group(buf, g + 1, O{});
+            } else if (ST) {
+                read_group(buf ^ 1, 0, Z{});
+            }
+            if (g == 1 && ST) store(buf ^ 1);
+            if (g == 2 && LD) load(s + 2);
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        if (g & 1)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[1][i][t], b[1][j][t], acc[i][j], 0, 0, 0);
+                        else
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0][i][t], b[0][j][t], acc[i][j], 0, 0, 0);
+                    }
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // 1 MFMA
+                if ((g + 1 < 4 || ST) && q < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // operand read
+                if (g == 1 && ST) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                // LDS store
+                if (g == 2 && LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // global load
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if (s0 < s1) {
+        load(s0);
+        store(0);
+        if (s0 + 1 < s1) load(s0 + 1);
+        kw_wave_sync();
+        read_group(0, 0, Z{});
+        int s = s0;
+        for (; s + 2 < s1; s++) slice(s, std::true_type{}, std::true_type{});
+        if (s + 1 < s1) {
+            slice(s, std::true_type{}, std::false_type{});
+            s++;
+        }
+        slice(s, std::false_type{}, std::false_type{});
+    }
+    // Partial tiles: lane l's accumulator registers 4rq..4rq+3 of block (i, j) at
+    // red[((w*4 + 2i+j)*4 + rq)*64 + l]; wave w then finishes block (w/2, w%2), summing the
+    // four waves' partials in wave order.  D layout: lane l, register r -> row
+    // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the block.
+    __syncthreads();                                              // every wave is done with its staging
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++)
+                red[((wave * 4 + i * 2 + j) * 4 + rq) * 64 + lane] =
+                    sgpu_f32x4{acc[i][j][4 * rq], acc[i][j][4 * rq + 1], acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]};
+    __syncthreads();
+    const int bi = wave >> 1, bj = wave & 1, blk = wave;
+    sgpu_f32x4 p[4][4];
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) p[w][rq] = red[((w * 4 + blk) * 4 + rq) * 64 + lane];
+#pragma unroll
+    for (int rq = 0; rq < 4; rq++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float v = ((p[0][rq][e] + p[1][rq][e]) + p[2][rq][e]) + p[3][rq][e];
+            C[(size_t)(m0 + bi * 32 + 8 * rq + 4 * h + e) * N + n0 + bj * 32 + l32] = v;
+        }
+    __syncthreads();                                              // the staging is reused by the next tile
+}
+
 }  // namespace
 
 extern "C" {
@@ -679,6 +837,27 @@ sgemm_small16(const float* __restrict__ A, const float* __restrict__ B, float* _
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 sgemm_small32(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     sgemm_small<32, 4>(A, B, C, M, N, K);
+}
+
+// sgemm_kwave: the 64x64 tile with K split over the block's four waves, for problems with M,
+// N multiples of 64, K a multiple of 32 and 16-byte aligned A and B (any other problem, or a
+// block size other than 256, returns without writing C).  Grid-stride over tiles, one block
+// per tile remapped XCD-compact as the other members; 144 KB of LDS, one block per CU.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgemm_kwave(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) KwaveLds L[4];
+    static_assert(sizeof(L) >= 4 * 4 * 4 * 64 * sizeof(sgpu_f32x4), "the partial tiles fit the staging");
+    if (sgpu_nthreads() != 256 || M <= 0 || N <= 0 || K <= 0 || M % 64 || N % 64 || K % KW_BK ||
+        ((((uintptr_t)A) | ((uintptr_t)B)) & 15))
+        return;
+    const int ntm = M / 64, ntn = N / 64, ntiles = ntm * ntn;
+    const int nb = sgpu_nblocks();
+    const bool remap = nb == ntiles && ntiles % kXcds == 0;
+    for (int t = sgpu_bid(); t < ntiles; t += nb) {
+        int tm, tn;
+        sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+        sgemm_kwave_tile(A, B, C, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6], reinterpret_cast<sgpu_f32x4*>(&L[0]));
+    }
 }
 
 // One output per thread, direct global reads, bounds-checked (switch_gpu.cu:139-152 role:

@@ -111,7 +111,7 @@ DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 
                    (1087, 1085, 2000),
                    # the small members' K bounds and the 16-way split of one tall-K tile
                    (256, 256, 4096), (100, 70, 3000), (16, 4096, 4096), (64, 64, 8192),
-                   # one round of 64x64 tiles split 5 and 4 ways
+                   # one round of 64x64 tiles split 5 ways, and one on the K-over-waves member
                    (768, 768, 2048), (1024, 768, 1024)]
 
 
@@ -311,6 +311,61 @@ def test_small_integer_exact(gpu, M, N, K, tile):
         assert np.array_equal(dC.to_host(), want)
 
 
+# sgemm_kwave splits each tile's 32-deep slices over the block's four waves: one slice (three
+# waves idle), three (one idle), uneven quarters, and up to 32 slices per wave.
+KWAVE_CASES = [(64, 64, 32), (64, 64, 96), (64, 128, 160), (128, 192, 1024), (256, 320, 544),
+               (512, 1024, 2048), (64, 64, 4096), (1024, 1024, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", KWAVE_CASES)
+def test_kwave_integer_exact(gpu, M, N, K):
+    """sgemm_kwave gives the exact product on integer inputs, twice in a row."""
+    say(f"sgemm kwave integer {M}x{N}x{K}")
+    rng = np.random.default_rng(M * 13 + N * 7 + K)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    for _ in range(2):
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_kwave", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+        gpu.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+
+
+def test_kwave_reference_inputs(gpu, og):
+    """Reference-generator inputs at 1024^3 within the normwise bar of the oracle."""
+    n = 1024
+    say(f"sgemm kwave n={n} reference inputs")
+    A, B = ref_inputs(n, n, n)
+    C = run_sgemm(gpu, "sgpu_sgemm_kwave", A, B, n, n, n)
+    ref = ref_golden(n, n, n)
+    assert np.abs(C.astype(np.float64) - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    assert og.sgemm_verdict_bad(C, ref, n, n) == 0
+
+
+def test_kwave_rejects_other_shapes(gpu):
+    """Shapes sgemm_kwave does not take, and operands off 16-byte alignment, are refused
+    before any launch; M or N = 0 is a no-op."""
+    dA, dB, dC = gpu.DeviceArray(64 * 4096 + 4), gpu.DeviceArray(4096 * 128 + 4), gpu.DeviceArray(64 * 128)
+    L = gpu.lib()
+    for M, N, K in ((63, 64, 64), (64, 96, 64), (64, 64, 48), (64, 64, 0), (-64, 64, 64)):
+        assert L.sgpu_sgemm_kwave(dA.ptr, dB.ptr, dC.ptr, M, N, K, None) == gpu.SGPU_ERR_INVALID_ARG, (M, N, K)
+    assert L.sgpu_sgemm_kwave(dA.offset(1), dB.ptr, dC.ptr, 64, 64, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave(dA.ptr, dB.offset(2), dC.ptr, 64, 64, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave(dA.ptr, dB.ptr, dC.ptr, 0, 64, 64, None) == 0
+
+
+def test_opt_unaligned_kwave_shape_takes_the_tiled_member(gpu):
+    """sgpu_sgemm_opt plans sgemm_kwave for 1024^3; with A off 16-byte alignment it launches
+    the 64x64 member instead, whose C it then equals bit for bit."""
+    M = N = K = 1024
+    A, B = ref_inputs(M, N, K)
+    C = run_sgemm(gpu, "sgpu_sgemm_opt", A, B, M, N, K, a_off=1)
+    D = run_sgemm(gpu, "sgpu_sgemm_tiled", A, B, M, N, K, a_off=1)
+    assert np.array_equal(C, D)
+
+
 NAN_PAD_CASES = [(7, 300, 13), (100, 70, 3000), (33, 17, 96), (64, 48, 2), (257, 511, 1030)]
 
 
@@ -391,6 +446,20 @@ def test_nonfinite_inputs_propagate(gpu, M, N, K, launcher):
         gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, None)
     else:
         gpu.call(launcher, dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+    gpu.synchronize()
+    got = dC.to_host()
+    assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (128, 192, 1024), (1024, 1024, 1024)])
+def test_kwave_nonfinite_inputs_propagate(gpu, M, N, K):
+    """The same non-finite operands through sgemm_kwave (whole tiles, K a multiple of 32):
+    the wave holding the NaN's or an infinity's k-quarter carries it into the tile's sum."""
+    say(f"sgemm kwave non-finite {M}x{N}x{K}")
+    A, B, want = nonfinite_operands(M, N, K, M + 7 * N + 3 * K)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    gpu.call("sgpu_sgemm_kwave", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
     gpu.synchronize()
     got = dC.to_host()
     assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])

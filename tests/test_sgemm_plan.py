@@ -23,10 +23,15 @@ PINNED_256 = [
     (2048, 2048, 2048, "sgemm_tiled4", 1),
     (3072, 3072, 3072, "sgemm_tiled", 1),
     (4097, 4097, 4097, "sgemm_tiled", 1),
-    # one round of 64x64 tiles, K a multiple of 32: unsplit wins at 1024^3, splits elsewhere
-    (1024, 1024, 1024, "sgemm_tiled", 1),
+    # one round of 64x64 tiles, K a multiple of 32: whole tiles filling 3/4 of the CUs or more
+    # with K >= 1024 take the K-over-waves member; fewer tiles split K across blocks
+    (1024, 1024, 1024, "sgemm_kwave", 1),
+    (1024, 1024, 4096, "sgemm_kwave", 1),
+    (1024, 768, 1024, "sgemm_kwave", 1),
+    (1024, 1024, 992, "sgemm_tiled", 1),
+    (1024, 1024, 512, "sgemm_tiled", 1),
     (768, 768, 2048, "sgemm_splitk", 5),
-    (1024, 768, 1024, "sgemm_splitk", 4),
+    (512, 1024, 1024, "sgemm_splitk", 2),
     (1088, 1024, 1024, "sgemm_splitk", 4),
     # K tails
     (1023, 1025, 997, "sgemm_splitk", 4),
@@ -67,7 +72,7 @@ def cdiv(a, b):
 
 @pytest.mark.parametrize("cus", [1, 80, 104, 256, 304])
 def test_plan_invariants(cus):
-    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled"}
+    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled", "sgemm_kwave"}
     for M in (1, 17, 64, 300, 1023, 2048):
         for N in (1, 64, 511, 1025, 4096):
             for K in (0, 1, 31, 64, 997, 2048, 8192):
@@ -88,6 +93,9 @@ def test_plan_invariants(cus):
                         assert cdiv(M, 16) * cdiv(N, 16) <= cus and K <= 4096
                     elif name == "sgemm_small32":
                         assert cdiv(M, 32) * cdiv(N, 32) <= cus and K <= 1024
+                    elif name == "sgemm_kwave":
+                        assert M % 64 == 0 and N % 64 == 0 and K % 32 == 0 and K >= 1024
+                        assert tiles <= cus and 4 * tiles >= 3 * cus
                     else:
                         assert name in members
 
