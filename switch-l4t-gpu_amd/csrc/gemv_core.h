@@ -693,8 +693,6 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
             for (int r = 0; r < 16; r++) acc[f][r] = 0.0f;
         // Staged chunk in registers: fp32 rows as loaded; fp16 rows as their raw codes, decoded
         // only when written to LDS, so the loads stay in flight under the previous chunk's MFMAs.
-        // Staged chunk in registers: fp32 rows as loaded; fp16 rows as their raw codes, decoded
-        // only when written to LDS, so the loads stay in flight under the previous chunk's MFMAs.
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         constexpr bool H = sizeof(typename WT::elem) == 2;
         sgpu_f32x4 g[H ? 4 : NI];
