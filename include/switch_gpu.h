@@ -130,7 +130,10 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * sgemm_splitk when a cost model of the busiest CU's k-slices, masked tail slices and split
  * hand-offs prefers a 2-8 way split (16 for a few tiles of tall K) to none -- except that
  * problems of whole 64x64 tiles filling 3/4 to all of the CUs in one round, with K a
- * multiple of 32 and at least 1024 (and 16-byte aligned A and B), go to sgemm_kwave. */
+ * multiple of 32 and at least 1024, go to sgemm_kwave (to sgemm_kwave_edge when A or B is
+ * off 16-byte alignment), and other problems whose sgemm_kwave_edge tiles fill 3/4 to all
+ * of the CUs in one round, with K >= 384 (K >= 128 when the 64x64 tiles would not fit the
+ * CUs in one round), go to sgemm_kwave_edge. */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
@@ -151,6 +154,15 @@ int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, in
  * and B 16-byte aligned (SGPU_ERR_INVALID_ARG otherwise).  No counterpart in the reference:
  * an added member of the family with the (A, B, C, M, N, K) symbol arguments. */
 int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+/* The sgemm_kwave_edge member: sgemm_kwave's structure for any M >= 64, N >= 64, K >= 1 and
+ * float-aligned A, B, C (SGPU_ERR_INVALID_ARG otherwise; M or N == 0 is a no-op).  A partial
+ * last row or column of tiles is computed as the 64 rows or columns ending at the last one
+ * and stored from its first new row or column on; a partial last k-slice reads zeros past K.
+ * With N % 64 == 1 the last column is computed by the last column of whole tiles alongside
+ * their MFMAs, so ceil(M/64) * (N/64) blocks; otherwise ceil(M/64) * ceil(N/64).  No
+ * counterpart in the reference: an added member of the family with the (A, B, C, M, N, K)
+ * symbol arguments. */
+int sgpu_sgemm_kwave_edge(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 /* The sgemm_splitk member: 64x64 tiles with K split S ways (S >= 1; reduced so that every
  * split holds at least one 32-deep slice), each (tile, split) a block.  Every split writes its
  * partial tile to a library-owned workspace of the launch's stream and the last split of a

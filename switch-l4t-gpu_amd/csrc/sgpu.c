@@ -45,7 +45,7 @@ static const struct {
 /* Every kernel the launchers use: (module, symbol). */
 enum {
     K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_SMALL16, K_SGEMM_SMALL32,
-    K_SGEMM_KWAVE, K_SGEMM_NAIVE, K_MEMBW,
+    K_SGEMM_KWAVE, K_SGEMM_KWAVE_EDGE, K_SGEMM_NAIVE, K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK, K_GEMV_MULTI_X8_64,
     K_GEMV_MULTI_X8_256,
     K_GEMV_H, K_GEMV_HH, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
@@ -59,7 +59,8 @@ static const struct {
 } g_kern[NKERN] = {
     {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
     {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_splitk"}, {MOD_SWITCH, "sgemm_small16"},
-    {MOD_SWITCH, "sgemm_small32"}, {MOD_SWITCH, "sgemm_kwave"}, {MOD_SWITCH, "sgemm_naive"},
+    {MOD_SWITCH, "sgemm_small32"}, {MOD_SWITCH, "sgemm_kwave"}, {MOD_SWITCH, "sgemm_kwave_edge"},
+    {MOD_SWITCH, "sgemm_naive"},
     {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
@@ -490,6 +491,10 @@ const void *sgpu_code_object(const char *name, size_t *size) {
 /* ---- geometry ---- */
 static unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
 static unsigned umin(unsigned a, unsigned b) { return a < b ? a : b; }
+/* sgemm_kwave_edge's blocks: the column past N/64 whole tiles (N % 64 == 1) rides on them. */
+static long long kwave_edge_tiles(int M, int N) {
+    return (long long)cdiv(M, 64) * (N % 64 == 1 ? (long long)(N / 64) : (long long)cdiv(N, 64));
+}
 
 /* Tile shape (rows x columns of C) of each tiled member; 0 for other kernels. */
 static int sgemm_tile(const char *k, int *tn) {
@@ -506,6 +511,12 @@ static int geometry(const devstate *d, const char *kernel, int M, int N, int K, 
     const unsigned cus = d ? (unsigned)d->cus : 256u;
     g[0] = g[1] = g[2] = 1;
     b[0] = b[1] = b[2] = 1;
+    if (!strcmp(kernel, "sgemm_kwave_edge")) {
+        long long nt = kwave_edge_tiles(M, N);
+        g[0] = (unsigned)(nt > 0 ? nt : 1);
+        b[0] = 256;
+        return SGPU_OK;
+    }
     int tile_n, tile = sgemm_tile(kernel, &tile_n);
     if (tile) {
         long long nt = (long long)cdiv(M, tile) * cdiv(N, tile_n);
@@ -593,6 +604,17 @@ int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int
     if (M == 0 || N == 0) return SGPU_OK;
     if (!kwave_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B) & 15)) return SGPU_ERR_INVALID_ARG;
     return sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
+}
+/* sgemm_kwave_edge's problems: M, N at least 64 (a partial last row or column of tiles is the
+ * 64 rows or columns ending at the last one), K at least 1, float-aligned operands. */
+static int kwave_edge_shape(int M, int N, int K) { return M >= 64 && N >= 64 && K >= 1; }
+
+int sgpu_sgemm_kwave_edge(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    if (!kwave_edge_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 3))
+        return SGPU_ERR_INVALID_ARG;
+    return sgemm_common(K_SGEMM_KWAVE_EDGE, "sgemm_kwave_edge", A, B, C, M, N, K, stream);
 }
 /* The optimised entry picks the member with the least work on its busiest CU: tiles are one
  * block each, dealt over the CUs, so a launch lasts about ceil(tiles / CUs) tile times, and a
@@ -752,7 +774,7 @@ int sgpu_sgemm_small(const float *A, const float *B, float *C, int M, int N, int
 /* The launch sgpu_sgemm_opt makes for an M x N x K problem on `cus` CUs: PLAN_SMALL16 /
  * PLAN_SMALL32, PLAN_SPLITK with *S splits (the unsplit member is launched instead when the
  * stream has no workspace), or an index into g_sgemm_members. */
-enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3, PLAN_KWAVE = -4 };
+enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3, PLAN_KWAVE = -4, PLAN_KWAVE_EDGE = -5 };
 static int opt_plan(int M, int N, int K, int cus, int *S) {
     *S = 1;
     /* Problems whose 16x16 (32x32) tiles fit the CUs in one round go to the small members
@@ -778,6 +800,19 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
         const long long tiles = (long long)(M / 64) * (N / 64);
         if (tiles <= cus && 4 * tiles >= 3LL * cus) return PLAN_KWAVE;
     }
+    /* Any other problem whose edge-member tiles (M and N rounded up to 64, or N rounded down
+     * when N % 64 == 1) fill 3/4 to all of the CUs in one round: the same structure with
+     * clamped edge tiles and a zero-padded last k-slice, from K 384, or from K 128 when the
+     * 64x64 member would need a second round (N % 64 == 1 past the CUs).  Recorded graphs,
+     * srand inputs, us, against the best of the 64x64 member and S = 2..6 splits:
+     * 1023x1025x997 23.5 vs 31.1 (S = 4); 1023x1025x128 7.2 vs 8.3; 1023x1025x64 6.9 vs 5.9;
+     * 1000x1000x1000 22.6 vs 26.9 (S = 3); 1000x1000x384 11.5 vs 12.5; 1000x1000x320 11.3 vs
+     * 10.9; 1000x1000x192 9.1 vs 8.0; 900x900x900 23.6 vs 24.5 (S = 3); 8192x128x1000 23.3
+     * vs 26.9 (S = 3). */
+    if (kwave_edge_shape(M, N, K) && !kwave_shape(M, N, K) && K >= 128) {
+        const long long tiles = kwave_edge_tiles(M, N), tiles64 = (long long)cdiv(M, 64) * cdiv(N, 64);
+        if (tiles <= cus && 4 * tiles >= 3LL * cus && (K >= 384 || tiles64 > cus)) return PLAN_KWAVE_EDGE;
+    }
     if (K > 0 && (*S = splitk_pick(M, N, K, cus)) > 1) return PLAN_SPLITK;
     *S = 1;
     return sgemm_pick(M, N, cus);
@@ -791,6 +826,7 @@ const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits) {
     if (p == PLAN_SMALL32) return "sgemm_small32";
     if (p == PLAN_SPLITK) return "sgemm_splitk";
     if (p == PLAN_KWAVE) return "sgemm_kwave";
+    if (p == PLAN_KWAVE_EDGE) return "sgemm_kwave_edge";
     return g_sgemm_members[p].name;
 }
 
@@ -808,8 +844,10 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     unsigned *cnt;
     if (p == PLAN_SPLITK && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
         return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
-    if (p == PLAN_KWAVE && !(((uintptr_t)A | (uintptr_t)B) & 15))          /* else: the 64x64 member */
+    if (p == PLAN_KWAVE && !(((uintptr_t)A | (uintptr_t)B) & 15))
         return sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
+    if ((p == PLAN_KWAVE || p == PLAN_KWAVE_EDGE) && !(((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 3))
+        return sgemm_common(K_SGEMM_KWAVE_EDGE, "sgemm_kwave_edge", A, B, C, M, N, K, stream);   /* rows of any float alignment */
     const int m = p >= 0 ? p : sgemm_pick(M, N, d->cus);
     return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }

@@ -647,29 +647,79 @@ __device__ __forceinline__ void kw_wave_sync() {
 //   slice (already in registers) is stored to the other buffer during group 1 and the loads
 //   of the slice after it are issued during group 2; group 3 starts with a wave sync and reads
 //   the next slice's first group.  Memory instructions are dealt out one per MFMA.
+// EDGE (sgemm_kwave_edge): any M, N >= 64, any K >= 1, rows of any float alignment.  A partial
+//   last row of tiles is computed as the 64 rows ending at row M-1 and stored from row m0 on;
+//   a partial last column of tiles likewise.  A partial last k-slice reads zeros past K (A's
+//   elements element-wise past the last whole quad, B's rows past K not at all); it can only
+//   be the last slice of wave 3, loaded by that wave's third-last slice or by its prologue.
+// TH (with EDGE, N % 64 == 1, the last column of whole tiles): the tile also computes column
+//   N-1 of its rows.  Lane l stages that column's element of k-row s*32 + l%32 in Bt; each
+//   group's A operands already in registers (rows l32 and 32+l32, k = 8g+4h+t) meet it in 8
+//   VALU FMAs, and the four waves' partials are summed at the end.  One column costs a few
+//   VALU FMAs per MFMA group instead of a 64-column tile of MFMAs.
 constexpr int KW_BK = 32, KW_PA = KW_BK + 4, KW_PB = 64 + 8;
 struct KwaveLds {
     float As[2][64][KW_PA];
     float Bs[2][KW_BK][KW_PB];
 };
+struct KwaveLdsEdge : KwaveLds {
+    float Bt[2][KW_BK];           // column N-1 of the slice's k-rows (TH tiles)
+};
+template <bool EDGE, bool TH, class Lds>
 __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, const float* __restrict__ B,
-                                                 float* __restrict__ C, int N, int K, int m0, int n0,
-                                                 KwaveLds& L, sgpu_f32x4* __restrict__ red) {
-    const int lane = sgpu_tid() & 63, wave = sgpu_tid() >> 6;
+                                                 float* __restrict__ C, int M, int N, int K, int m0, int n0,
+                                                 Lds& L, sgpu_f32x4* __restrict__ red) {
+    static_assert(EDGE || !TH, "the extra column is an edge case");
+    const int lane = sgpu_tid() & 63;
+    const int wave = EDGE ? __builtin_amdgcn_readfirstlane(sgpu_tid() >> 6) : sgpu_tid() >> 6;
     const int l32 = lane & 31, h = lane >> 5;
-    const int nk = K / KW_BK;
+    const int nk = EDGE ? (K + KW_BK - 1) / KW_BK : K / KW_BK;
+    const int tail_s = K % KW_BK ? nk - 1 : nk;                  // the partial last slice, if any
     const int s0 = wave * nk / 4, s1 = (wave + 1) * nk / 4;      // this wave's slices
-    const float* pa = A + (size_t)(m0 + (lane >> 3)) * K + 4 * (lane & 7);
-    const float* pb = B + (size_t)(lane >> 4) * N + n0 + 4 * (lane & 15);
+    const int mt = EDGE ? min(m0, M - 64) : m0;                  // the tile's first computed row
+    const int nt = EDGE ? min(n0, N - 64) : n0;                  // and column
+    const float* pa = A + (size_t)(mt + (lane >> 3)) * K + 4 * (lane & 7);
+    const float* pb = B + (size_t)(lane >> 4) * N + nt + 4 * (lane & 15);
     const size_t astep = (size_t)8 * K, bstep = (size_t)4 * N;
     sgpu_f32x4 ra[8], rb[8];
-    auto load = [&](int s) __attribute__((always_inline)) {
+    float tb = 0.0f;                                             // TH: B[s*32 + l%32][N-1]
+    const float* pt = B + (size_t)l32 * N + (N - 1);
+    auto load_whole = [&](int s) __attribute__((always_inline)) {
         const float* a = pa + (size_t)s * KW_BK;
         const float* b = pb + (size_t)s * KW_BK * N;
 #pragma unroll
         for (int q = 0; q < 8; q++) ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a + q * astep);
 #pragma unroll
         for (int q = 0; q < 8; q++) rb[q] = *reinterpret_cast<const sgpu_f32x4*>(b + q * bstep);
+        if constexpr (TH) tb = pt[(size_t)s * KW_BK * N];
+    };
+    // the partial last slice: elements past K read as zero, nothing past A or B is touched
+    auto load_tail = [&](int s) __attribute__((always_inline)) {
+        const int kq = s * KW_BK + 4 * (lane & 7);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const float* a = pa + q * astep + (size_t)s * KW_BK;
+            if (kq + 3 < K) {
+                ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) ra[q][e] = kq + e < K ? a[e] : 0.0f;
+            }
+        }
+        const int kr = s * KW_BK + (lane >> 4);
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            rb[q] = kr + 4 * q < K ? *reinterpret_cast<const sgpu_f32x4*>(pb + (size_t)(s * KW_BK + 4 * q) * N)
+                                   : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (TH) {
+            const int k = s * KW_BK + l32;
+            const float v = B[(size_t)min(k, K - 1) * N + (N - 1)];
+            tb = k < K ? v : 0.0f;
+        }
+    };
+    auto load = [&](int s) __attribute__((always_inline)) {
+        if (EDGE && s == tail_s) load_tail(s);
+        else load_whole(s);
     };
     auto store = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -678,6 +728,7 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
 #pragma unroll
         for (int q = 0; q < 8; q++)
             *reinterpret_cast<sgpu_f32x4*>(&L.Bs[buf][4 * q + (lane >> 4)][4 * (lane & 15)]) = rb[q];
+        if constexpr (TH) L.Bt[buf][l32] = tb;                   // lanes l and l+32 store the same value
     };
     sgpu_f32x16 acc[2][2];
 #pragma unroll
@@ -687,6 +738,8 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
     sgpu_f32x4 a[2][2], b[2][2];                                  // [operand set][block]
+    float tacc[2] = {0.0f, 0.0f};                                 // TH: rows l32, 32+l32 of column N-1
+    sgpu_f32x4 tk[2];                                             // TH: [operand set] column N-1, k = kc..kc+3
     auto read_group = [&](int buf, int g, auto set_c) __attribute__((always_inline)) {
         constexpr int RS = decltype(set_c)::value;
         const int kc = 8 * g + 4 * h;
@@ -696,12 +749,18 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int j = 0; j < 2; j++) b[RS][j][t] = L.Bs[buf][kc + t][j * 32 + l32];
+        if constexpr (TH) tk[RS] = *reinterpret_cast<const sgpu_f32x4*>(&L.Bt[buf][kc]);
     };
     using Z = std::integral_constant<int, 0>;
     using O = std::integral_constant<int, 1>;
-    // ST: this slice stores the next one (and reads its first group); LD: it loads slice s+2.
+    using L0 = std::integral_constant<int, 0>;
+    using L1 = std::integral_constant<int, 1>;
+    using L2 = std::integral_constant<int, 2>;
+    // ST: this slice stores the next one (and reads its first group); LD: it loads slice s+2
+    // (0 no, 1 a whole slice, 2 the wave's last slice, which may be the partial one).
     auto slice = [&](int s, auto st_c, auto ld_c) __attribute__((always_inline)) {
-        constexpr bool ST = decltype(st_c)::value, LD = decltype(ld_c)::value;
+        constexpr bool ST = decltype(st_c)::value;
+        constexpr int LD = decltype(ld_c)::value;
         const int buf = (s - s0) & 1;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -714,7 +773,8 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
                 read_group(buf ^ 1, 0, Z{});
             }
             if (g == 1 && ST) store(buf ^ 1);
-            if (g == 2 && LD) load(s + 2);
+            if (g == 2 && LD == 1) load_whole(s + 2);
+            if (g == 2 && LD == 2) load(s + 2);
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -726,12 +786,23 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
                         else
                             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0][i][t], b[0][j][t], acc[i][j], 0, 0, 0);
                     }
+            if constexpr (TH) {
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+                        tacc[i] = (g & 1) ? __builtin_fmaf(a[1][i][t], tk[1][t], tacc[i])
+                                          : __builtin_fmaf(a[0][i][t], tk[0][t], tacc[i]);
+            }
+            // TH adds one operand read per group, one LDS store and one global load per slice
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // 1 MFMA
-                if ((g + 1 < 4 || ST) && q < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // operand read
+                if ((g + 1 < 4 || ST) && q < (TH ? 7 : 6)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // operand read
                 if (g == 1 && ST) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                // LDS store
-                if (g == 2 && LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // global load
+                if (g == 1 && ST && TH && q == 15) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                if (g == 2 && LD == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);           // global load
+                if (g == 2 && LD == 1 && TH && q == 15) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -743,12 +814,20 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
         kw_wave_sync();
         read_group(0, 0, Z{});
         int s = s0;
-        for (; s + 2 < s1; s++) slice(s, std::true_type{}, std::true_type{});
+        if constexpr (EDGE) {
+            for (; s + 3 < s1; s++) slice(s, std::true_type{}, L1{});  // loads s+2 < s1-1: whole slices
+            if (s + 2 < s1) {                                             // loads s1-1, possibly the partial one
+                slice(s, std::true_type{}, L2{});
+                s++;
+            }
+        } else {
+            for (; s + 2 < s1; s++) slice(s, std::true_type{}, L1{});
+        }
         if (s + 1 < s1) {
-            slice(s, std::true_type{}, std::false_type{});
+            slice(s, std::true_type{}, L0{});
             s++;
         }
-        slice(s, std::false_type{}, std::false_type{});
+        slice(s, std::false_type{}, L0{});
     }
     // Partial tiles: lane l's accumulator registers 4rq..4rq+3 of block (i, j) at
     // red[((w*4 + 2i+j)*4 + rq)*64 + l]; wave w then finishes block (w/2, w%2), summing the
@@ -763,7 +842,22 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
             for (int rq = 0; rq < 4; rq++)
                 red[((wave * 4 + i * 2 + j) * 4 + rq) * 64 + lane] =
                     sgpu_f32x4{acc[i][j][4 * rq], acc[i][j][4 * rq + 1], acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]};
+    // TH: the column's partials after the tile partials, tred[(w*2 + h)*64 + row]; wave 0 sums
+    // them in (wave, h) order
+    float* tred = reinterpret_cast<float*>(red + 4 * 4 * 4 * 64);
+    if constexpr (TH) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) tred[(wave * 2 + h) * 64 + i * 32 + l32] = tacc[i];
+    }
     __syncthreads();
+    if constexpr (TH) {
+        if (wave == 0) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; w++) v += tred[w * 64 + lane];
+            if (mt + lane >= m0) C[(size_t)(mt + lane) * N + (N - 1)] = v;
+        }
+    }
     const int bi = wave >> 1, bj = wave & 1, blk = wave;
     sgpu_f32x4 p[4][4];
 #pragma unroll
@@ -775,7 +869,12 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const float v = ((p[0][rq][e] + p[1][rq][e]) + p[2][rq][e]) + p[3][rq][e];
-            C[(size_t)(m0 + bi * 32 + 8 * rq + 4 * h + e) * N + n0 + bj * 32 + l32] = v;
+            if constexpr (EDGE) {
+                const int gm = mt + bi * 32 + 8 * rq + 4 * h + e, gn = nt + bj * 32 + l32;
+                if (gm >= m0 && gn >= n0) C[(size_t)gm * N + gn] = v;
+            } else {
+                C[(size_t)(m0 + bi * 32 + 8 * rq + 4 * h + e) * N + n0 + bj * 32 + l32] = v;
+            }
         }
     __syncthreads();                                              // the staging is reused by the next tile
 }
@@ -856,7 +955,37 @@ sgemm_kwave(const float* __restrict__ A, const float* __restrict__ B, float* __r
     for (int t = sgpu_bid(); t < ntiles; t += nb) {
         int tm, tn;
         sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
-        sgemm_kwave_tile(A, B, C, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6], reinterpret_cast<sgpu_f32x4*>(&L[0]));
+        sgemm_kwave_tile<false, false>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6],
+                                       reinterpret_cast<sgpu_f32x4*>(&L[0]));
+    }
+}
+
+// sgemm_kwave_edge: sgemm_kwave for any M >= 64, N >= 64 and K >= 1, rows of any float
+// alignment.  A partial last row or column of tiles is computed as the 64 rows (columns)
+// ending at the last one and stored from its first new row (column) on; a partial last
+// k-slice reads zeros past K.  N % 64 == 1 (one column past the last whole tile) is computed
+// by the last column of whole tiles alongside their MFMAs (TH) rather than by a column of
+// 64-wide tiles; every other N rounds the tile columns up.  Tiles: ceil(M/64) times N/64
+// (N % 64 == 1) or ceil(N/64); grid-stride as sgemm_kwave; 145 KB of LDS, one block per CU.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgemm_kwave_edge(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) KwaveLdsEdge L[4];
+    static_assert(sizeof(L) >= 4 * 4 * 4 * 64 * sizeof(sgpu_f32x4) + 8 * 64 * sizeof(float),
+                  "the partial tiles and the extra column's partials fit the staging");
+    if (sgpu_nthreads() != 256 || M < 64 || N < 64 || K < 1) return;
+    const bool th = N % 64 == 1;
+    const int ntm = (M + 63) / 64, ntn = th ? N / 64 : (N + 63) / 64, ntiles = ntm * ntn;
+    const int nb = sgpu_nblocks();
+    const bool remap = nb == ntiles && ntiles % kXcds == 0;
+    for (int t = sgpu_bid(); t < ntiles; t += nb) {
+        int tm, tn;
+        sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+        if (th && tn == ntn - 1)
+            sgemm_kwave_tile<true, true>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6],
+                                         reinterpret_cast<sgpu_f32x4*>(&L[0]));
+        else
+            sgemm_kwave_tile<true, false>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6],
+                                          reinterpret_cast<sgpu_f32x4*>(&L[0]));
     }
 }
 

@@ -111,8 +111,9 @@ DISPATCH_SHAPES = [(2048, 8192, 48), (2048, 8192, 32), (2047, 8191, 50), (4096, 
                    (1087, 1085, 2000),
                    # the small members' K bounds and the 16-way split of one tall-K tile
                    (256, 256, 4096), (100, 70, 3000), (16, 4096, 4096), (64, 64, 8192),
-                   # one round of 64x64 tiles split 5 ways, and one on the K-over-waves member
-                   (768, 768, 2048), (1024, 768, 1024)]
+                   # one round of 64x64 tiles split 5 ways, one on the K-over-waves member and
+                   # three on its edge form (one column past the whole tiles; clamped edges)
+                   (768, 768, 2048), (1024, 768, 1024), (1023, 1025, 997), (1000, 1000, 1000), (8192, 128, 1000)]
 
 
 @pytest.mark.parametrize("M,N,K", DISPATCH_SHAPES)
@@ -129,7 +130,8 @@ def test_tile_paths_integer_exact(gpu, fn, M, N, K):
 # sgpu_sgemm_opt launches what sgpu_sgemm_opt_plan names for this device: on float inputs its
 # C equals the named launch's bit for bit.  A split sums its partials in split order, so a
 # split C differs from the unsplit member's, and a different split count would differ too.
-PLAN_SHAPES = [(1023, 1025, 997), (768, 768, 2048), (1000, 1000, 1000), (1088, 1024, 1024),
+PLAN_SHAPES = [(1023, 1025, 997), (768, 768, 2048), (1000, 1000, 1000), (1088, 1024, 1024), (1024, 1024, 1000),
+               (8192, 128, 1000), (1023, 1025, 128),
                (2048, 1024, 1000), (640, 640, 4096), (64, 64, 8192), (256, 256, 256), (512, 512, 512),
                (1024, 1024, 1024), (2048, 2048, 2048)]
 
@@ -383,14 +385,131 @@ def test_kwave_rejects_other_shapes(gpu):
     assert L.sgpu_sgemm_kwave(dA.ptr, dB.ptr, dC.ptr, 0, 64, 64, None) == 0
 
 
-def test_opt_unaligned_kwave_shape_takes_the_tiled_member(gpu):
+def test_opt_unaligned_kwave_shape_takes_the_edge_member(gpu):
     """sgpu_sgemm_opt plans sgemm_kwave for 1024^3; with A off 16-byte alignment it launches
-    the 64x64 member instead, whose C it then equals bit for bit."""
+    sgemm_kwave_edge instead (rows of any float alignment), whose C it then equals bit for
+    bit."""
     M = N = K = 1024
     A, B = ref_inputs(M, N, K)
     C = run_sgemm(gpu, "sgpu_sgemm_opt", A, B, M, N, K, a_off=1)
-    D = run_sgemm(gpu, "sgpu_sgemm_tiled", A, B, M, N, K, a_off=1)
+    D = run_sgemm(gpu, "sgpu_sgemm_kwave_edge", A, B, M, N, K, a_off=1)
     assert np.array_equal(C, D)
+
+
+# sgemm_kwave_edge: M, N >= 64 with partial last rows and columns of tiles (computed as the 64
+# ending at the last one), N % 64 == 1 (the column computed by the last column of whole tiles:
+# one such column, many), K tails of 1..31 and K < 4 (element-wise A loads), one slice (three
+# waves idle), uneven quarters, up to 130 slices per wave, and rows of any float alignment.
+EDGE_CASES = [(64, 64, 1), (64, 65, 37), (130, 64, 33), (127, 129, 131), (64, 64, 5), (200, 191, 3),
+              (64, 127, 100), (100, 100, 2), (65, 4097, 64), (300, 1025, 2047), (64, 65, 4103),
+              (1023, 1025, 997), (1024, 1024, 1000), (1023, 1000, 997), (8192, 128, 1000)]
+
+
+@pytest.mark.parametrize("a_off,b_off", [(0, 0), (1, 3)])
+@pytest.mark.parametrize("M,N,K", EDGE_CASES)
+def test_kwave_edge_integer_exact(gpu, M, N, K, a_off, b_off):
+    """sgemm_kwave_edge gives the exact product on integer inputs, twice in a row, with C
+    pre-filled with NaN (an unwritten element shows) and A, B at any float offset."""
+    say(f"sgemm kwave_edge integer {M}x{N}x{K} a_off={a_off} b_off={b_off}")
+    rng = np.random.default_rng(M * 17 + N * 5 + K + a_off)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    for _ in range(2):
+        assert np.array_equal(run_sgemm(gpu, "sgpu_sgemm_kwave_edge", A, B, M, N, K, a_off, b_off), want)
+
+
+@pytest.mark.parametrize("M,N,K", [(1023, 1025, 997), (1000, 1000, 1000)])
+def test_kwave_edge_reference_inputs(gpu, og, M, N, K):
+    """Reference-generator inputs within the normwise bar of the oracle and its verdict clean,
+    on the reference's ragged shape (one column past 16 whole tiles) and on clamped edge tiles."""
+    say(f"sgemm kwave_edge {M}x{N}x{K} reference inputs")
+    A, B = ref_inputs(M, N, K)
+    C = run_sgemm(gpu, "sgpu_sgemm_kwave_edge", A, B, M, N, K)
+    ref = ref_golden(M, N, K)
+    assert np.abs(C.astype(np.float64) - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    assert og.sgemm_verdict_bad(C, ref, M, N) == 0
+
+
+@pytest.mark.parametrize("a_off", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(100, 70, 3000), (257, 511, 1030), (64, 65, 37), (1023, 1025, 997)])
+def test_kwave_edge_operands_followed_by_nan(gpu, M, N, K, a_off):
+    """A and B at the start of larger NaN-filled allocations, as for the other members: the
+    edge member's partial last slice, its clamped edge tiles and the extra column's loads
+    read nothing past either operand."""
+    say(f"sgemm kwave_edge nan-padded {M}x{N}x{K} a_off={a_off}")
+    rng = np.random.default_rng(M * 5 + N * 3 + K + 1)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    ha = np.full(a_off + M * K + K + 512, np.nan, np.float32)
+    ha[a_off:a_off + M * K] = A.reshape(-1)
+    hb = np.full((K + 512) * N, np.nan, np.float32)
+    hb[:K * N] = B.reshape(-1)
+    dA, dB, dC = gpu.DeviceArray.from_host(ha), gpu.DeviceArray.from_host(hb), gpu.DeviceArray((M, N))
+    for _ in range(2):
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_kwave_edge", dA.offset(a_off), dB.ptr, dC.ptr, M, N, K, None)
+        gpu.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+
+
+@pytest.mark.parametrize("last_col", [False, True])
+@pytest.mark.parametrize("M,N,K", [(127, 129, 131), (64, 65, 37), (1023, 1025, 997), (1000, 1000, 1000)])
+def test_kwave_edge_nonfinite_inputs_propagate(gpu, M, N, K, last_col):
+    """The non-finite operands of the other members through sgemm_kwave_edge, the infinities
+    in B's row K-1 (the partial last slice where K % 32 != 0) and row 0, in column N/2 or in
+    column N-1 (with N % 64 == 1 the column the last whole tiles compute by VALU FMAs)."""
+    say(f"sgemm kwave_edge non-finite {M}x{N}x{K} last_col={last_col}")
+    A, B, want = nonfinite_operands(M, N, K, M + 7 * N + 3 * K, jb=N - 1 if last_col else None)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    gpu.call("sgpu_sgemm_kwave_edge", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+    gpu.synchronize()
+    got = dC.to_host()
+    assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])
+
+
+def test_kwave_edge_graph_replay(gpu):
+    """sgemm_kwave_edge recorded once in a graph and replayed with new inputs copied in
+    between: every replay equals the direct launch bit for bit."""
+    M, N, K = 1023, 1025, 997
+    say(f"sgemm kwave_edge graph replay {M}x{N}x{K}")
+    dA, dB, dC, dD = gpu.DeviceArray((M, K)), gpu.DeviceArray((K, N)), gpu.DeviceArray((M, N)), gpu.DeviceArray((M, N))
+    st = gpu.Stream()
+    with gpu.Graph(st) as g:
+        gpu.call("sgpu_sgemm_kwave_edge", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
+    for rep in range(4):
+        rng = np.random.default_rng(700 + rep)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = rng.standard_normal((K, N)).astype(np.float32)
+        gpu.call("sgpu_memcpy_htod", dA.ptr, A.ctypes.data, A.nbytes)
+        gpu.call("sgpu_memcpy_htod", dB.ptr, B.ctypes.data, B.nbytes)
+        gpu.call("sgpu_sgemm_kwave_edge", dA.ptr, dB.ptr, dD.ptr, M, N, K, st.h)
+        st.synchronize()
+        dC.fill_bytes(0xFF)
+        g.launch()
+        st.synchronize()
+        assert np.array_equal(dC.to_host().view(np.uint32), dD.to_host().view(np.uint32)), rep
+        ref = A.astype(np.float64) @ B.astype(np.float64)
+        assert np.abs(dC.to_host() - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    g.close()
+    st.close()
+
+
+def test_kwave_edge_rejects_other_shapes(gpu):
+    """M or N below 64, K = 0, negative sizes, null or non-float-aligned operands are refused
+    before any launch; M or N = 0 is a no-op."""
+    dA, dB, dC = gpu.DeviceArray(64 * 4096 + 4), gpu.DeviceArray(4096 * 128 + 4), gpu.DeviceArray(64 * 128 + 4)
+    L = gpu.lib()
+    for M, N, K in ((63, 64, 64), (64, 63, 64), (64, 64, 0), (-64, 64, 64), (64, 64, -1)):
+        assert L.sgpu_sgemm_kwave_edge(dA.ptr, dB.ptr, dC.ptr, M, N, K, None) == gpu.SGPU_ERR_INVALID_ARG, (M, N, K)
+    assert L.sgpu_sgemm_kwave_edge(dA.ptr + 2, dB.ptr, dC.ptr, 64, 64, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave_edge(dA.ptr, dB.ptr + 1, dC.ptr, 64, 64, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave_edge(dA.ptr, dB.ptr, dC.ptr + 3, 64, 64, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave_edge(None, dB.ptr, dC.ptr, 64, 64, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave_edge(dA.ptr, dB.ptr, dC.ptr, 0, 64, 64, None) == 0
+    assert L.sgpu_sgemm_kwave_edge(dA.ptr, dB.ptr, dC.ptr, 64, 0, 64, None) == 0
 
 
 NAN_PAD_CASES = [(7, 300, 13), (100, 70, 3000), (33, 17, 96), (64, 48, 2), (257, 511, 1030)]
@@ -431,16 +550,17 @@ def test_operands_followed_by_nan_integer_exact(gpu, M, N, K, launcher, a_off):
 NONFINITE_CASES = [(7, 300, 13), (100, 70, 3000), (130, 190, 65), (256, 256, 256), (1023, 1025, 997)]
 
 
-def nonfinite_operands(M, N, K, seed):
-    """Small integers plus: NaN at A[ia, ka]; +Inf at B[kb, jb] and -Inf at B[0, jb]; a zero
-    at A[iz, kb].  Returns A, B and the IEEE product the reference's serial fp32 loop
+def nonfinite_operands(M, N, K, seed, jb=None):
+    """Small integers plus: NaN at A[ia, ka]; +Inf at B[kb, jb] and -Inf at B[0, jb] (jb
+    N // 2 unless given); a zero at A[iz, kb].  Returns A, B and the IEEE product the reference's serial fp32 loop
     (gpu_workload.c:97-98) yields: row ia all NaN (NaN times anything); in column jb,
     A[i,kb]*Inf + A[i,0]*(-Inf) is NaN when either multiplier is 0 (Inf * 0) or the two
     infinities have opposite signs, else that infinity; everything else the exact integer sum."""
     rng = np.random.default_rng(seed)
     A = rng.integers(-2, 3, (M, K)).astype(np.float32)
     B = rng.integers(-2, 3, (K, N)).astype(np.float32)
-    ia, ka, kb, jb, iz = M // 2, K // 3, K - 1, N // 2, (M // 2 + 1) % M
+    ia, ka, kb, iz = M // 2, K // 3, K - 1, (M // 2 + 1) % M
+    jb = N // 2 if jb is None else jb
     A[iz, kb] = 0.0
     Af, Bf = A.copy(), B.copy()
     A[ia, ka] = np.nan

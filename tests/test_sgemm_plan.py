@@ -33,9 +33,17 @@ PINNED_256 = [
     (768, 768, 2048, "sgemm_splitk", 5),
     (512, 1024, 1024, "sgemm_splitk", 2),
     (1088, 1024, 1024, "sgemm_splitk", 4),
+    # edge tiles (M or N off 64, K off 32) filling 3/4 of the CUs or more in one round: the
+    # K-over-waves edge member from K 384, or from K 128 when the 64x64 member needs a second
+    # round (N % 64 == 1 rides on the last column of whole tiles)
+    (1023, 1025, 997, "sgemm_kwave_edge", 1),
+    (1000, 1000, 1000, "sgemm_kwave_edge", 1),
+    (1024, 1024, 1000, "sgemm_kwave_edge", 1),
+    (8192, 128, 1000, "sgemm_kwave_edge", 1),
+    (1000, 1000, 384, "sgemm_kwave_edge", 1),
+    (1023, 1025, 128, "sgemm_kwave_edge", 1),
+    (1023, 1025, 64, "sgemm_tiled", 1),
     # K tails
-    (1023, 1025, 997, "sgemm_splitk", 4),
-    (1000, 1000, 1000, "sgemm_splitk", 2),
     (640, 640, 1000, "sgemm_splitk", 5),
     (1087, 1085, 2000, "sgemm_splitk", 7),
     (1408, 1408, 997, "sgemm_tiled", 1),
@@ -72,10 +80,10 @@ def cdiv(a, b):
 
 @pytest.mark.parametrize("cus", [1, 80, 104, 256, 304])
 def test_plan_invariants(cus):
-    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled", "sgemm_kwave"}
-    for M in (1, 17, 64, 300, 1023, 2048):
-        for N in (1, 64, 511, 1025, 4096):
-            for K in (0, 1, 31, 64, 997, 2048, 8192):
+    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled", "sgemm_kwave", "sgemm_kwave_edge"}
+    for M in (1, 17, 64, 300, 1000, 1023, 2048):
+        for N in (1, 64, 511, 1000, 1025, 4096):
+            for K in (0, 1, 31, 64, 128, 320, 997, 2048, 8192):
                 name, S = plan(M, N, K, cus)
                 tiles = cdiv(M, 64) * cdiv(N, 64)
                 nk = cdiv(K, 32)
@@ -96,6 +104,12 @@ def test_plan_invariants(cus):
                     elif name == "sgemm_kwave":
                         assert M % 64 == 0 and N % 64 == 0 and K % 32 == 0 and K >= 1024
                         assert tiles <= cus and 4 * tiles >= 3 * cus
+                    elif name == "sgemm_kwave_edge":
+                        assert M >= 64 and N >= 64 and K >= 128
+                        assert M % 64 or N % 64 or K % 32
+                        edge_tiles = cdiv(M, 64) * (N // 64 if N % 64 == 1 else cdiv(N, 64))
+                        assert edge_tiles <= cus and 4 * edge_tiles >= 3 * cus
+                        assert K >= 384 or tiles > cus
                     else:
                         assert name in members
 
