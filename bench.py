@@ -255,8 +255,12 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1, cpu=False):
         g.close()
         st.close()
         tf = 2.0 * M * N * K / (us_g * 1e-6) / 1e12
+        # the reference's own timing form (events around a host loop of launches,
+        # gpu_workload.c:133-139) beside the graph replay's
+        tf_loop = 2.0 * M * N * K / (us * 1e-6) / 1e12
         out.append({"M": M, "N": N, "K": K, "launch": launch, "us_in_graph": round(us_g, 2), "us_host_loop": round(us, 2),
-                    "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MATRIX_TFLOPS, 4), "normwise_err": err,
+                    "tflops": round(tf, 2), "frac": round(tf / PEAK_FP32_MATRIX_TFLOPS, 4),
+                    "frac_host_loop": round(tf_loop / PEAK_FP32_MATRIX_TFLOPS, 4), "normwise_err": err,
                     **cpu_row})
         for d in (dA, dB, dC):
             d.close()
