@@ -168,9 +168,13 @@ def test_opt_launches_its_plan(gpu, M, N, K):
 # Shapes whose edge tiles take the clamped-address path: an A tile (BM rows of K floats) or a
 # B slice (BK rows of N floats) of 2^31 bytes or more.  Entries in {-1, 0, 1}: every partial
 # sum is an exact fp32 integer (|sum| <= K < 2^24).
+# The edge member's loads use 64-bit addresses throughout: A and B of 2^31 bytes or more through
+# a K tail, and the extra column (N % 64 == 1) at 2^23 + 1 columns.
 @pytest.mark.parametrize("fn,M,N,K", [("sgpu_sgemm_tiled", 3, 5, (1 << 23) + 7),
                                       ("sgpu_sgemm_opt256", 3, 5, (1 << 21) + 3),
-                                      ("sgpu_sgemm_tiled", 2, (1 << 24) + 5, 3)])
+                                      ("sgpu_sgemm_tiled", 2, (1 << 24) + 5, 3),
+                                      ("sgpu_sgemm_kwave_edge", 64, 64, (1 << 23) + 7),
+                                      ("sgpu_sgemm_kwave_edge", 64, (1 << 23) + 1, 65)])
 def test_large_operand_windows_integer_exact(gpu, fn, M, N, K):
     say(f"sgemm {fn} large window {M}x{N}x{K}")
     rng = np.random.default_rng(K + N)
