@@ -805,10 +805,9 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
      * clamped edge tiles and a zero-padded last k-slice, from K 384, or from K 128 when the
      * 64x64 member would need a second round (N % 64 == 1 past the CUs).  Recorded graphs,
      * srand inputs, us, against the best of the 64x64 member and S = 2..6 splits:
-     * 1023x1025x997 23.5 vs 31.1 (S = 4); 1023x1025x128 7.2 vs 8.3; 1023x1025x64 6.9 vs 5.9;
-     * 1000x1000x1000 22.6 vs 26.9 (S = 3); 1000x1000x384 11.5 vs 12.5; 1000x1000x320 11.3 vs
-     * 10.9; 1000x1000x192 9.1 vs 8.0; 900x900x900 23.6 vs 24.5 (S = 3); 8192x128x1000 23.3
-     * vs 26.9 (S = 3). */
+     * 1023x1025x997 22.0 vs 31.1 (S = 4); 1024x1024x1000 21.0 vs 26.6; 1023x1025x128 7.1 vs
+     * 8.2; 1023x1025x96 7.0 vs 7.0; 1023x1025x64 6.9 vs 5.8; 1000x1000x384 11.5 vs 12.2;
+     * 1000x1000x320 11.2 vs 10.8; 1000x1000x256 9.3 vs 9.3; 1000x1000x192 9.1 vs 7.8. */
     if (kwave_edge_shape(M, N, K) && !kwave_shape(M, N, K) && K >= 128) {
         const long long tiles = kwave_edge_tiles(M, N), tiles64 = (long long)cdiv(M, 64) * cdiv(N, 64);
         if (tiles <= cus && 4 * tiles >= 3LL * cus && (K >= 384 || tiles64 > cus)) return PLAN_KWAVE_EDGE;

@@ -649,9 +649,11 @@ __device__ __forceinline__ void kw_wave_sync() {
 //   the next slice's first group.  Memory instructions are dealt out one per MFMA.
 // EDGE (sgemm_kwave_edge): any M, N >= 64, any K >= 1, rows of any float alignment.  A partial
 //   last row of tiles is computed as the 64 rows ending at row M-1 and stored from row m0 on;
-//   a partial last column of tiles likewise.  A partial last k-slice reads zeros past K (A's
-//   elements element-wise past the last whole quad, B's rows past K not at all); it can only
-//   be the last slice of wave 3, loaded by that wave's third-last slice or by its prologue.
+//   a partial last column of tiles likewise.  With K % 32 != 0 the partial k-slice is slice 0
+//   (k < K % 32; the later slices shifted to end at K): it reads zeros past K % 32 (A's
+//   elements element-wise past the last whole quad, B's rows past it not at all), and only the
+//   prologue of the wave holding slice 0 loads it, so every slice of the pipelined loop is
+//   whole, as in the exact member.
 // TH (with EDGE, N % 64 == 1, the last column of whole tiles): the tile also computes column
 //   N-1 of its rows.  Lane l stages that column's element of k-row s*32 + l%32 in Bt; each
 //   group's A operands already in registers (rows l32 and 32+l32, k = 8g+4h+t) meet it in 8
@@ -674,7 +676,10 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
     const int wave = EDGE ? __builtin_amdgcn_readfirstlane(sgpu_tid() >> 6) : sgpu_tid() >> 6;
     const int l32 = lane & 31, h = lane >> 5;
     const int nk = EDGE ? (K + KW_BK - 1) / KW_BK : K / KW_BK;
-    const int tail_s = K % KW_BK ? nk - 1 : nk;                  // the partial last slice, if any
+    // EDGE, K % 32 != 0: slice 0 is the partial one, k in [0, K % 32), and slice s >= 1 covers
+    // k from 32 s - kshift; only the prologue of the wave holding slice 0 loads a partial slice
+    const int kpart = EDGE ? K % KW_BK : 0;
+    const int kshift = kpart ? KW_BK - kpart : 0;
     const int s0 = wave * nk / 4, s1 = (wave + 1) * nk / 4;      // this wave's slices
     const int mt = EDGE ? min(m0, M - 64) : m0;                  // the tile's first computed row
     const int nt = EDGE ? min(n0, N - 64) : n0;                  // and column
@@ -682,43 +687,39 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
     const float* pb = B + (size_t)(lane >> 4) * N + nt + 4 * (lane & 15);
     const size_t astep = (size_t)8 * K, bstep = (size_t)4 * N;
     sgpu_f32x4 ra[8], rb[8];
-    float tb = 0.0f;                                             // TH: B[s*32 + l%32][N-1]
+    float tb = 0.0f;                                             // TH: B[k of slice row l%32][N-1]
     const float* pt = B + (size_t)l32 * N + (N - 1);
     auto load_whole = [&](int s) __attribute__((always_inline)) {
-        const float* a = pa + (size_t)s * KW_BK;
-        const float* b = pb + (size_t)s * KW_BK * N;
+        const size_t k0 = (size_t)s * KW_BK - kshift;
+        const float* a = pa + k0;
+        const float* b = pb + k0 * N;
 #pragma unroll
         for (int q = 0; q < 8; q++) ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a + q * astep);
 #pragma unroll
         for (int q = 0; q < 8; q++) rb[q] = *reinterpret_cast<const sgpu_f32x4*>(b + q * bstep);
-        if constexpr (TH) tb = pt[(size_t)s * KW_BK * N];
+        if constexpr (TH) tb = pt[k0 * N];
     };
-    // the partial last slice: elements past K read as zero, nothing past A or B is touched
-    auto load_tail = [&](int s) __attribute__((always_inline)) {
-        const int kq = s * KW_BK + 4 * (lane & 7);
+    // the partial slice 0: k >= K % 32 reads as zero, nothing past A or B is touched
+    auto load_part = [&]() __attribute__((always_inline)) {
+        const int kq = 4 * (lane & 7);
 #pragma unroll
         for (int q = 0; q < 8; q++) {
-            const float* a = pa + q * astep + (size_t)s * KW_BK;
-            if (kq + 3 < K) {
+            const float* a = pa + q * astep;
+            if (kq + 3 < kpart) {
                 ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a);
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; e++) ra[q][e] = kq + e < K ? a[e] : 0.0f;
+                for (int e = 0; e < 4; e++) ra[q][e] = kq + e < kpart ? a[e] : 0.0f;
             }
         }
-        const int kr = s * KW_BK + (lane >> 4);
 #pragma unroll
         for (int q = 0; q < 8; q++)
-            rb[q] = kr + 4 * q < K ? *reinterpret_cast<const sgpu_f32x4*>(pb + (size_t)(s * KW_BK + 4 * q) * N)
-                                   : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (TH) {
-            const int k = s * KW_BK + l32;
-            const float v = B[(size_t)min(k, K - 1) * N + (N - 1)];
-            tb = k < K ? v : 0.0f;
-        }
+            rb[q] = (lane >> 4) + 4 * q < kpart ? *reinterpret_cast<const sgpu_f32x4*>(pb + (size_t)(4 * q) * N)
+                                                : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (TH) tb = l32 < kpart ? pt[0] : 0.0f;
     };
     auto load = [&](int s) __attribute__((always_inline)) {
-        if (EDGE && s == tail_s) load_tail(s);
+        if (EDGE && kpart && s == 0) load_part();
         else load_whole(s);
     };
     auto store = [&](int buf) __attribute__((always_inline)) {
@@ -753,14 +754,10 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
     };
     using Z = std::integral_constant<int, 0>;
     using O = std::integral_constant<int, 1>;
-    using L0 = std::integral_constant<int, 0>;
-    using L1 = std::integral_constant<int, 1>;
-    using L2 = std::integral_constant<int, 2>;
     // ST: this slice stores the next one (and reads its first group); LD: it loads slice s+2
-    // (0 no, 1 a whole slice, 2 the wave's last slice, which may be the partial one).
+    // (always a whole slice: s+2 >= 2).
     auto slice = [&](int s, auto st_c, auto ld_c) __attribute__((always_inline)) {
-        constexpr bool ST = decltype(st_c)::value;
-        constexpr int LD = decltype(ld_c)::value;
+        constexpr bool ST = decltype(st_c)::value, LD = decltype(ld_c)::value;
         const int buf = (s - s0) & 1;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -773,8 +770,7 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
                 read_group(buf ^ 1, 0, Z{});
             }
             if (g == 1 && ST) store(buf ^ 1);
-            if (g == 2 && LD == 1) load_whole(s + 2);
-            if (g == 2 && LD == 2) load(s + 2);
+            if (g == 2 && LD) load_whole(s + 2);
 #pragma unroll
             for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -801,8 +797,8 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
                 if ((g + 1 < 4 || ST) && q < (TH ? 7 : 6)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // operand read
                 if (g == 1 && ST) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                // LDS store
                 if (g == 1 && ST && TH && q == 15) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-                if (g == 2 && LD == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);           // global load
-                if (g == 2 && LD == 1 && TH && q == 15) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                if (g == 2 && LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // global load
+                if (g == 2 && LD && TH && q == 15) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -814,20 +810,12 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
         kw_wave_sync();
         read_group(0, 0, Z{});
         int s = s0;
-        if constexpr (EDGE) {
-            for (; s + 3 < s1; s++) slice(s, std::true_type{}, L1{});  // loads s+2 < s1-1: whole slices
-            if (s + 2 < s1) {                                             // loads s1-1, possibly the partial one
-                slice(s, std::true_type{}, L2{});
-                s++;
-            }
-        } else {
-            for (; s + 2 < s1; s++) slice(s, std::true_type{}, L1{});
-        }
+        for (; s + 2 < s1; s++) slice(s, std::true_type{}, std::true_type{});
         if (s + 1 < s1) {
-            slice(s, std::true_type{}, L0{});
+            slice(s, std::true_type{}, std::false_type{});
             s++;
         }
-        slice(s, std::false_type{}, L0{});
+        slice(s, std::false_type{}, std::false_type{});
     }
     // Partial tiles: lane l's accumulator registers 4rq..4rq+3 of block (i, j) at
     // red[((w*4 + 2i+j)*4 + rq)*64 + l]; wave w then finishes block (w/2, w%2), summing the
