@@ -857,13 +857,28 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const float v = ((p[0][rq][e] + p[1][rq][e]) + p[2][rq][e]) + p[3][rq][e];
-            if constexpr (EDGE) {
-                const int gm = mt + bi * 32 + 8 * rq + 4 * h + e, gn = nt + bj * 32 + l32;
-                if (gm >= m0 && gn >= n0) C[(size_t)gm * N + gn] = v;
-            } else {
-                C[(size_t)(m0 + bi * 32 + 8 * rq + 4 * h + e) * N + n0 + bj * 32 + l32] = v;
-            }
+            if constexpr (EDGE) p[0][rq][e] = v;
+            else C[(size_t)(m0 + bi * 32 + 8 * rq + 4 * h + e) * N + n0 + bj * 32 + l32] = v;
         }
+    // EDGE: a clamped edge tile stores only its new rows and columns, every other tile all of
+    // them (the per-element test costs ~0.7 us a launch when every tile takes it)
+    if constexpr (EDGE) {
+        if (mt == m0 && nt == n0) {
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    C[(size_t)(m0 + bi * 32 + 8 * rq + 4 * h + e) * N + n0 + bj * 32 + l32] = p[0][rq][e];
+        } else {
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int gm = mt + bi * 32 + 8 * rq + 4 * h + e, gn = nt + bj * 32 + l32;
+                    if (gm >= m0 && gn >= n0) C[(size_t)gm * N + gn] = p[0][rq][e];
+                }
+        }
+    }
     __syncthreads();                                              // the staging is reused by the next tile
 }
 
