@@ -157,7 +157,8 @@ int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int
 /* The sgemm_kwave_edge member: sgemm_kwave's structure for any M >= 64, N >= 64, K >= 1 and
  * float-aligned A, B, C (SGPU_ERR_INVALID_ARG otherwise; M or N == 0 is a no-op).  A partial
  * last row or column of tiles is computed as the 64 rows or columns ending at the last one
- * and stored from its first new row or column on; a partial last k-slice reads zeros past K.
+ * and stored from its first new row or column on; with K % 32 != 0 the first 32-deep k-slice
+ * is the partial one (k < K % 32), read with zeros past it.
  * With N % 64 == 1 the last column is computed by the last column of whole tiles alongside
  * their MFMAs, so ceil(M/64) * (N/64) blocks; otherwise ceil(M/64) * ceil(N/64).  No
  * counterpart in the reference: an added member of the family with the (A, B, C, M, N, K)

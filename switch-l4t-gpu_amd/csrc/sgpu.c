@@ -802,7 +802,7 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
     }
     /* Any other problem whose edge-member tiles (M and N rounded up to 64, or N rounded down
      * when N % 64 == 1) fill 3/4 to all of the CUs in one round: the same structure with
-     * clamped edge tiles and a zero-padded last k-slice, from K 384, or from K 128 when the
+     * clamped edge tiles and a zero-padded first k-slice, from K 384, or from K 128 when the
      * 64x64 member would need a second round (N % 64 == 1 past the CUs).  Recorded graphs,
      * srand inputs, us, against the best of the 64x64 member and S = 2..6 splits:
      * 1023x1025x997 22.0 vs 31.1 (S = 4); 1024x1024x1000 21.0 vs 26.6; 1023x1025x128 7.1 vs

@@ -655,7 +655,7 @@ __device__ __forceinline__ void kw_wave_sync() {
 //   prologue of the wave holding slice 0 loads it, so every slice of the pipelined loop is
 //   whole, as in the exact member.
 // TH (with EDGE, N % 64 == 1, the last column of whole tiles): the tile also computes column
-//   N-1 of its rows.  Lane l stages that column's element of k-row s*32 + l%32 in Bt; each
+//   N-1 of its rows.  Lane l stages that column's element of the slice's k-row l%32 in Bt; each
 //   group's A operands already in registers (rows l32 and 32+l32, k = 8g+4h+t) meet it in 8
 //   VALU FMAs, and the four waves' partials are summed at the end.  One column costs a few
 //   VALU FMAs per MFMA group instead of a 64-column tile of MFMAs.
@@ -689,6 +689,7 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
     sgpu_f32x4 ra[8], rb[8];
     float tb = 0.0f;                                             // TH: B[k of slice row l%32][N-1]
     const float* pt = B + (size_t)l32 * N + (N - 1);
+    // a whole slice s (s >= 1 when K % 32 != 0: slice 0 is then the partial one)
     auto load_whole = [&](int s) __attribute__((always_inline)) {
         const size_t k0 = (size_t)s * KW_BK - kshift;
         const float* a = pa + k0;
@@ -965,8 +966,8 @@ sgemm_kwave(const float* __restrict__ A, const float* __restrict__ B, float* __r
 
 // sgemm_kwave_edge: sgemm_kwave for any M >= 64, N >= 64 and K >= 1, rows of any float
 // alignment.  A partial last row or column of tiles is computed as the 64 rows (columns)
-// ending at the last one and stored from its first new row (column) on; a partial last
-// k-slice reads zeros past K.  N % 64 == 1 (one column past the last whole tile) is computed
+// ending at the last one and stored from its first new row (column) on; with K % 32 != 0 the
+// first k-slice is the partial one (k < K % 32, zeros past it).  N % 64 == 1 (one column past the last whole tile) is computed
 // by the last column of whole tiles alongside their MFMAs (TH) rather than by a column of
 // 64-wide tiles; every other N rounds the tile columns up.  Tiles: ceil(M/64) times N/64
 // (N % 64 == 1) or ceil(N/64); grid-stride as sgemm_kwave; 145 KB of LDS, one block per CU.
