@@ -141,7 +141,10 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
  * units ("sgemm_small16", "sgemm_splitk", "sgemm_opt256", ...), with the split count in
  * *splits (1 unless "sgemm_splitk"); a pure function, no device needed.  NULL when nothing
  * is launched (M or N < 1) or an argument is invalid.  sgpu_sgemm_opt launches the unsplit
- * member instead of "sgemm_splitk" on a stream being recorded that has no workspace yet.
+ * member instead of "sgemm_splitk" on a stream being recorded that has no workspace yet;
+ * the plan assumes 16-byte aligned A and B: with A or B off 16 bytes, "sgemm_kwave" becomes
+ * "sgemm_kwave_edge", and with an operand off 4 bytes "sgemm_kwave" or "sgemm_kwave_edge"
+ * becomes the 64x64-or-larger member the size rule picks.
  * No counterpart in the reference (its sgemm_opt is one kernel). */
 const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits);
 /* The sgemm_opt256 member alone (any shape; masked loads on edge tiles).  No
