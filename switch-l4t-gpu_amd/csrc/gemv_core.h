@@ -251,7 +251,7 @@ struct XHalf {
 // barrier for teams of up to one wave.
 struct XRms {
     const float* x;
-    const uint16_t* w;
+    const uint16_t* w;                   // 16-byte aligned (segments of 8 codes are loaded whole)
     float eps;
     float inv;
     __device__ __forceinline__ sgpu_f32x4 load4(int k) const { return *reinterpret_cast<const sgpu_f32x4*>(x + k); }
@@ -273,8 +273,17 @@ struct XRms {
         for (int j = 0; j < S; j++) {
             if (!has[j]) continue;
             const int k0 = (sub + LPR * j) * VEC;
+            if constexpr (VEC == 8) {            // the segment's 8 gain codes in one 16-byte load
+                const sgpu_u32x4 g = *reinterpret_cast<const sgpu_u32x4*>(w + k0);
 #pragma unroll
-            for (int e = 0; e < VEC; e++) xr[j][e] = xr[j][e] * inv * sgpu_h2f(w[k0 + e]);
+                for (int e = 0; e < 4; e++) {
+                    xr[j][2 * e] = xr[j][2 * e] * inv * sgpu_h2f_lo(g[e]);
+                    xr[j][2 * e + 1] = xr[j][2 * e + 1] * inv * sgpu_h2f_hi(g[e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; e++) xr[j][e] = xr[j][e] * inv * sgpu_h2f(w[k0 + e]);
+            }
         }
     }
 };

@@ -1323,6 +1323,7 @@ int sgpu_internal_dec_qkv(const uint16_t *W, int K, int nrows, const float *x, c
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    if ((uintptr_t)lnw & 15) return SGPU_ERR_INVALID_ARG;     /* gains loaded 8 codes at a time */
     if (HD <= 0 || HD % 2 || nrows != (NH + 2 * NKV) * HD) return SGPU_ERR_INVALID_ARG;
     int nteams = nrows / 2;
     void *args[] = {(void *)&W, &K, &nteams, (void *)&x, (void *)&lnw, &eps, (void *)&bias, (void *)&q,
@@ -1335,6 +1336,7 @@ int sgpu_internal_dec_gateup(const uint16_t *W, int K, int FC, const float *x, c
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    if ((uintptr_t)lnw & 15) return SGPU_ERR_INVALID_ARG;     /* gains loaded 8 codes at a time */
     void *args[] = {(void *)&W, &K, &FC, (void *)&x, (void *)&lnw, &eps, (void *)&y};
     return dec_launch_team(d, DEC_GATEUP, K, FC, args, stream);
 }
@@ -1353,6 +1355,7 @@ int sgpu_internal_dec_lmhead(const uint16_t *W, int K, int N, const float *x, co
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
+    if ((uintptr_t)lnw & 15) return SGPU_ERR_INVALID_ARG;     /* gains loaded 8 codes at a time */
     void *args[] = {(void *)&W, &K, &N, (void *)&x, (void *)&lnw, &eps, (void *)&y};
     return dec_launch_team(d, DEC_LMHEAD, K, N, args, stream);
 }
