@@ -203,3 +203,25 @@ def test_gemv_test_harness(gpu, co, args):
     assert all(k["verdict"] == "CORRECT" and k["gbps"] > 0 for k in d["kernels"])
     if co == "gemv":
         assert [k["kernel"] for k in d["kernels"]] == ["gemv", "gemv4", "gemv_warp"]
+
+
+# The K-over-waves SGEMM members by name at grids smaller than their tile count: each block
+# strides over several tiles (the staging reused tile after tile; with sgemm_kwave_edge, the
+# clamped edge tiles and, N % 64 == 1, the tiles that also compute column N-1).
+BYNAME_KWAVE = [("sgemm_kwave", 256, 320, 544, 5), ("sgemm_kwave", 128, 192, 1024, 1),
+                ("sgemm_kwave_edge", 1023, 1025, 997, 7), ("sgemm_kwave_edge", 200, 191, 33, 3),
+                ("sgemm_kwave_edge", 130, 65, 40, 1), ("sgemm_kwave_edge", 1000, 1000, 1000, 64)]
+
+
+@pytest.mark.parametrize("sym,M,N,K,grid", BYNAME_KWAVE)
+def test_kwave_members_by_name_any_grid(gpu, hip, sym, M, N, K, grid):
+    say(f"by name {sym} {M}x{N}x{K} grid {grid}")
+    rng = np.random.default_rng(M + 3 * N + 7 * K + grid)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = upload(gpu, A), upload(gpu, B), gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    hip.launch(hip.function("switch_gpu", sym), (grid, 1), [Ptr(dA.ptr), Ptr(dB.ptr), Ptr(dC.ptr), M, N, K])
+    gpu.synchronize()
+    assert np.array_equal(dC.to_host(), want)
