@@ -507,8 +507,9 @@ def cpu_baseline(n, target_s=1.5):
 def pmc_probe():
     """One launch each of: add2 over 64 Mi floats (a plain elementwise kernel whose HBM
     traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), the lm_head
-    gemv_h and gemv_hh, and ten back-to-back launches of sgpu_sgemm_opt 4096^3 (sgemm_opt256; per-dispatch
-    counters are averaged).  Run under `rocprofv3 --pmc FETCH_SIZE`, again with WRITE_SIZE,
+    gemv_h and gemv_hh, and ten back-to-back launches each of sgpu_sgemm_opt at 4096^3
+    (sgemm_opt256), 1024^3 (sgemm_kwave) and 1023x1025x997 (sgemm_kwave_edge); per-dispatch
+    counters are averaged.  Run under `rocprofv3 --pmc FETCH_SIZE`, again with WRITE_SIZE,
     and with the MFMA-busy counters; prints the algorithmic bytes of each launch as one JSON
     line."""
     n = 64 << 20
@@ -529,6 +530,16 @@ def pmc_probe():
         sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, N4, N4, N4, None)
     sgpu.synchronize()
     del dA, dB, dC
+    mids = ((1024, 1024, 1024), (1023, 1025, 997))
+    for M, Nm, Km in mids:
+        A, B = sgpu.gen_sgemm_inputs(max(M * Km, Km * Nm), 42)
+        dA, dB = sgpu.DeviceArray.from_host(A[:M * Km]), sgpu.DeviceArray.from_host(B[:Km * Nm])
+        dC = sgpu.DeviceArray((M, Nm))
+        sgpu.synchronize()
+        for _ in range(10):
+            sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, Nm, Km, None)
+        sgpu.synchronize()
+        del dA, dB, dC
     N, K = 151936, 896
     W = sgpu.f32_to_f16(sgpu.gen_normal(N * K, 42, 0.0, 0.02)[0])
     dW, dx, dy = sgpu.DeviceArray.from_host(W), sgpu.DeviceArray(K), sgpu.DeviceArray(N)
@@ -548,6 +559,8 @@ def pmc_probe():
         sgpu.synchronize()
     print(json.dumps({"add2_read": 2 * 4 * n, "add2_write": 4 * n,
                       "sgemm_read_min": 2 * 4 * N4 * N4, "sgemm_write": 4 * N4 * N4,
+                      **{f"sgemm_{M}x{Nm}x{Km}_read_min": 4 * (M * Km + Km * Nm) for M, Nm, Km in mids},
+                      **{f"sgemm_{M}x{Nm}x{Km}_write": 4 * M * Nm for M, Nm, Km in mids},
                       "gemv_h_read": 2 * N * K + 4 * K, "gemv_h_write": 4 * N,
                       "gemv_hh_read": 2 * N * K + 2 * K, "gemv_hh_write": 4 * N}), flush=True)
 
