@@ -204,12 +204,17 @@ __device__ __forceinline__ float team_sum_bcast(float v, float* red) {
     }
 }
 
+// preload(g, has, sub): operands the prologue needs besides x that do not depend on it (the
+// RMSNorm gains), loaded before the weights so that they arrive with them.
 struct XPlain {
     const float* x;
     __device__ __forceinline__ sgpu_f32x4 load4(int k) const { return *reinterpret_cast<const sgpu_f32x4*>(x + k); }
     __device__ __forceinline__ float at(int k) const { return x[k]; }
     template <int LPR, int S, int VEC>
-    __device__ __forceinline__ void prepare(float (&)[S][VEC], const bool (&)[S], int, int, float*) {}
+    __device__ __forceinline__ void preload(sgpu_u32x4 (&)[S], const bool (&)[S], int) const {}
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&)[S][VEC], const sgpu_u32x4 (&)[S], const bool (&)[S], int, int,
+                                            float*) {}
 };
 
 // x given as fp16 bit patterns (the fp16-x GEMV): each lane converts its slice once into its
@@ -231,7 +236,10 @@ struct XHalf {
     }
     __device__ __forceinline__ float at(int k) const { return sgpu_h2f(x[k]); }
     template <int LPR, int S, int VEC>
-    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const bool (&)[S], int, int, float*) {
+    __device__ __forceinline__ void preload(sgpu_u32x4 (&)[S], const bool (&)[S], int) const {}
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const sgpu_u32x4 (&)[S], const bool (&)[S], int, int,
+                                            float*) {
 #pragma unroll
         for (int j = 0; j < S; j++)
 #pragma unroll
@@ -260,7 +268,16 @@ struct XRms {
         return x[k] * inv * sgpu_h2f(w[k]);
     }
     template <int LPR, int S, int VEC>
-    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const bool (&has)[S], int sub, int K, float* red) {
+    __device__ __forceinline__ void preload(sgpu_u32x4 (&g)[S], const bool (&has)[S], int sub) const {
+        if constexpr (VEC == 8) {
+#pragma unroll
+            for (int j = 0; j < S; j++)          // a lane without the segment reads segment 0, unused
+                g[j] = *reinterpret_cast<const sgpu_u32x4*>(w + (has[j] ? (sub + LPR * j) * VEC : 0));
+        }
+    }
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const sgpu_u32x4 (&gp)[S], const bool (&has)[S], int sub,
+                                            int K, float* red) {
 #pragma clang fp contract(off)
         float ss = 0.0f;
 #pragma unroll
@@ -273,8 +290,8 @@ struct XRms {
         for (int j = 0; j < S; j++) {
             if (!has[j]) continue;
             const int k0 = (sub + LPR * j) * VEC;
-            if constexpr (VEC == 8) {            // the segment's 8 gain codes in one 16-byte load
-                const sgpu_u32x4 g = *reinterpret_cast<const sgpu_u32x4*>(w + k0);
+            if constexpr (VEC == 8) {            // the segment's 8 gain codes, preloaded
+                const sgpu_u32x4 g = gp[j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     xr[j][2 * e] = xr[j][2 * e] * inv * sgpu_h2f_lo(g[e]);
@@ -304,7 +321,10 @@ struct XLn {
         return (x[k] - mean) * inv * w[k] + b[k];
     }
     template <int LPR, int S, int VEC>
-    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const bool (&has)[S], int sub, int K, float* red) {
+    __device__ __forceinline__ void preload(sgpu_u32x4 (&)[S], const bool (&)[S], int) const {}
+    template <int LPR, int S, int VEC>
+    __device__ __forceinline__ void prepare(float (&xr)[S][VEC], const sgpu_u32x4 (&)[S], const bool (&has)[S], int sub,
+                                            int K, float* red) {
 #pragma clang fp contract(off)
         float s = 0.0f;
 #pragma unroll
@@ -419,6 +439,8 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
     const int nb = nblk > 0 ? nblk : (int)gridDim.x;
     if ((int)blockIdx.x >= nb) return;                // block-uniform
     int rb = blockIdx.x;
+    sgpu_u32x4 gpre[S];
+    pro.template preload<LPR, S, VEC>(gpre, has, sub);
     if (rb * TEAMS < nteams) fetch(rb);
 
     // This lane's x slice: segments sub, sub+LPR, ..., kept for every row.
@@ -433,7 +455,7 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
             for (int e = 0; e < 4; e++) xr[j][4 * q + e] = a[e];
         }
     }
-    pro.template prepare<LPR, S, VEC>(xr, has, sub, K, red);
+    pro.template prepare<LPR, S, VEC>(xr, gpre, has, sub, K, red);
 
     for (; rb * TEAMS < nteams; rb += nb) {           // block-uniform loop
         const int t = rb * TEAMS + team;
