@@ -290,12 +290,16 @@ struct XRms {
         for (int j = 0; j < S; j++) {
             if (!has[j]) continue;
             const int k0 = (sub + LPR * j) * VEC;
-            if constexpr (VEC == 8) {            // the segment's 8 gain codes, preloaded
+            if constexpr (VEC == 8) {
+                // the segment's 8 gain codes, preloaded, by the hardware conversion as the
+                // weights are: a code of exponent 31 converts to inf/NaN instead of the
+                // reference's finite value, every row sum then comes out non-finite and is
+                // recomputed with the exact decode (at()); subnormal codes flush to 0 as there
                 const sgpu_u32x4 g = gp[j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    xr[j][2 * e] = xr[j][2 * e] * inv * sgpu_h2f_lo(g[e]);
-                    xr[j][2 * e + 1] = xr[j][2 * e + 1] * inv * sgpu_h2f_hi(g[e]);
+                    xr[j][2 * e] = xr[j][2 * e] * inv * WF16::cvt(g[e] & 0xffffu);
+                    xr[j][2 * e + 1] = xr[j][2 * e + 1] * inv * WF16::cvt(g[e] >> 16);
                 }
             } else {
 #pragma unroll

@@ -159,6 +159,34 @@ def test_engine_exponent31_weights(gpu, og, path):
     eng.close()
 
 
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_engine_exponent31_norm_gains(gpu, og, path):
+    """fp16 codes with exponent 31 and subnormal codes in layer 0's RMSNorm gains (in_ln ahead
+    of the qkv projection, post_ln ahead of gate|up).  The fused prologues convert gains in
+    hardware; an exponent-31 gain makes every row sum non-finite there, and those rows are
+    recomputed with the reference's exact decode (finite +-2^16(1+m/1024); subnormals read as
+    0).  Every launch structure matches the CPU golden, teacher-forced."""
+    cfg = SMALL
+    blob = gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=29, std=0.15)
+    h = blob.view(np.uint16)
+    C = cfg["C"]
+    qkv = C + 2 * cfg["NKV"] * cfg["HD"]
+    in_ln = (cfg["V"] * C * 2 + 2 * cfg["CTX"] * (cfg["HD"] // 2) * 4) // 2
+    post_ln = in_ln + C + qkv * C + qkv + C * C
+    for off, k, code in ((in_ln, 3, 0x7C00), (in_ln, C - 1, 0x0001), (post_ln, 5, 0xFC02), (post_ln, 7, 0x83FF)):
+        h[off + k] = code
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob, PATHS[path])
+    gold = og.QwenGolden(og.qwen_cfg(**cfg), blob, NT)
+    ids = [int(v) for v in np.random.default_rng(9).integers(0, cfg["V"], 12)]
+    for p, t in enumerate(ids):
+        got = eng.forward(t, p).copy()
+        want = gold.forward(t, p)
+        assert np.all(np.isfinite(want)) and np.all(np.isfinite(got)), p
+        scale = np.abs(want).max()
+        assert np.abs(got - want).max() <= 1e-4 * scale, (p, np.abs(got - want).max(), scale)
+    eng.close()
+
+
 # Long teacher-forced runs on the fused path, head dims 32 and 128: the attention kernel's
 # score and mix loops take several passes past 64 (32) positions per pass, past 256 positions
 # a head's cache is cut into chunks whose partials are combined, and past 7936 the chunk count
