@@ -630,7 +630,7 @@ __global__ void __launch_bounds__(256) sgpu_dec_attn128(const float* __restrict_
     }
 
 #define SGPU_DEC_PAIRS(F) F(16, 1) F(16, 2) F(16, 4) F(16, 7) F(16, 8) F(64, 1) F(64, 2) F(64, 4) F(64, 8)
-#define SGPU_DEC_SINGLE(F) SGPU_DEC_PAIRS(F) F(256, 1) F(256, 2) F(256, 3) F(256, 4) F(256, 8)
+#define SGPU_DEC_SINGLE(F) SGPU_DEC_PAIRS(F) F(256, 1) F(256, 2) F(256, 3) F(256, 4) F(256, 8) F(64, 10)
 
 SGPU_DEC_PAIRS(SGPU_DEC_QKV)
 SGPU_DEC_PAIRS(SGPU_DEC_GATEUP)
