@@ -255,8 +255,9 @@ struct XHalf {
 
 // x'[k] = x[k] * inv * h2f(w[k]), inv = 1 / sqrt(mean(x^2) + eps): cpu_rms (qwen_engine.c:285-290)
 // with the same product order.  A team's lanes together hold all K values of x, so the sum of
-// squares is a team reduction over the registers already loaded: no extra loads, and no
-// barrier for teams of up to one wave.
+// squares is a team reduction over the registers already loaded (no barrier for teams of up
+// to one wave).  The lane's gain segments are loaded by preload(), ahead of the weights, so
+// they arrive with them instead of costing a round trip after the reduction.
 struct XRms {
     const float* x;
     const uint16_t* w;                   // 16-byte aligned (segments of 8 codes are loaded whole)
