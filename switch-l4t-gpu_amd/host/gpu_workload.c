@@ -10,11 +10,14 @@
  *
  * Usage: gpu_workload [--json] [--ref-geometry] [--extra 2048,4096] [--ragged]
  *                     [--membw-mb MB] [--membw-iters N] [code_object]
+ *        gpu_workload --diagnostics-selftest
  *   --ref-geometry  launch with the reference's own grid/block numbers ((n/32)^2 or (n/64)^2
  *                   blocks of 16x16) instead of the kernels' intended geometry
  *   --extra         more square sizes, timed and checked on a sample of rows
  *   --ragged        add M=1023, N=1025, K=997 to the extra shapes
  *   --membw-mb      bandwidth buffer size (default 1024 MB: larger than the 256 MB MALL)
+ *   --diagnostics-selftest  print the golden check's mismatch report on planted errors, on the
+ *                   host only, and exit
  */
 #define __HIP_PLATFORM_AMD__ 1
 #include <hip/hip_runtime_api.h>
@@ -50,9 +53,25 @@ static char *read_file(const char *path, size_t *len) {
     return buf;
 }
 
-/* The reference golden and verdict (gpu_workload.c:95-112): serial fp32 k-ascending dot
- * products, |got-ref| > 5%|ref| + 1e-3 is bad, at most one bad cell counted per row,
- * stop after 5 bad rows.  rows == NULL checks every row. */
+/* The serial fp32 k-ascending dot product of the reference golden (gpu_workload.c:97-98),
+ * over k < kend. */
+static float golden_dot(const float *A, const float *B, int N, int K, int i, int j, int kend) {
+    float ref = 0;
+    for (int k = 0; k < kend && k < K; k++) ref += A[(size_t)i * K + k] * B[(size_t)k * N + j];
+    return ref;
+}
+
+/* The reference verdict predicate (gpu_workload.c:101): |got - ref| > 5%|ref| + 1e-3. */
+static int cell_bad(float got, float ref) {
+    float d = got - ref;
+    if (d < 0) d = -d;
+    return d > 0.05f * (ref < 0 ? -ref : ref) + 1e-3f;
+}
+
+/* The reference check (gpu_workload.c:95-112): at most one bad cell counted per row, stop after
+ * 5 bad rows.  The first mismatch also prints the golden's partial sums over k < 32, 64 and 96
+ * (which k-slice of a tiled kernel went wrong), the next two the short form; tag NULL prints
+ * the reference's own line, a kernel name prefixes it.  rows == NULL checks every row. */
 static int verify(const float *A, const float *B, const float *C, int M, int N, int K, const int *rows, int nrows,
                   const char *tag) {
     int bad = 0;
@@ -60,18 +79,48 @@ static int verify(const float *A, const float *B, const float *C, int M, int N, 
     for (int r = 0; r < count && bad < 5; r++) {
         const int i = rows ? rows[r] : r;
         for (int j = 0; j < N; j++) {
-            float ref = 0;
-            for (int k = 0; k < K; k++) ref += A[(size_t)i * K + k] * B[(size_t)k * N + j];
-            float d = C[(size_t)i * N + j] - ref;
-            if (d < 0) d = -d;
-            if (d > 0.05f * (ref < 0 ? -ref : ref) + 1e-3f) {
-                if (bad < 3) OUT("  %s mismatch [%d][%d]: got %.4f want %.4f\n", tag, i, j, C[(size_t)i * N + j], ref);
-                bad++;
-                break;
-            }
+            const float got = C[(size_t)i * N + j], ref = golden_dot(A, B, N, K, i, j, K);
+            if (!cell_bad(got, ref)) continue;
+            if (bad == 0)
+                OUT("  %s%smismatch [%d][%d]: got %.4f want %.4f (k<32:%.4f k<64:%.4f k<96:%.4f)\n", tag ? tag : "",
+                    tag ? " " : "", i, j, got, ref, golden_dot(A, B, N, K, i, j, 32), golden_dot(A, B, N, K, i, j, 64),
+                    golden_dot(A, B, N, K, i, j, 96));
+            else if (bad < 3)
+                OUT("  %s%smismatch [%d][%d]: got %.4f want %.4f\n", tag ? tag : "", tag ? " " : "", i, j, got, ref);
+            bad++;
+            break;
         }
     }
     return bad;
+}
+
+/* The naive bisect's count (gpu_workload.c:116-131): every bad cell of the whole matrix. */
+static int count_bad(const float *A, const float *B, const float *C, int M, int N, int K) {
+    int nbad = 0;
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) nbad += cell_bad(C[(size_t)i * N + j], golden_dot(A, B, N, K, i, j, K));
+    return nbad;
+}
+
+/* --diagnostics-selftest: the check's output on planted mismatches, on the host only (no
+ * device call): C is the golden product of the n = 256 inputs with cells [3][7], [3][9],
+ * [10][0], [11][5], [12][1] and [200][255] offset by +1, checked as the sgemm kernel and as
+ * the naive bisect. */
+static int diagnostics_selftest(void) {
+    const int n = 256;
+    float *A = malloc((size_t)n * n * 4), *B = malloc((size_t)n * n * 4), *C = malloc((size_t)n * n * 4);
+    if (!A || !B || !C) return 1;
+    sgpu_gen_sgemm_inputs(A, B, (size_t)n * n, 42);
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < n; j++) C[(size_t)i * n + j] = golden_dot(A, B, n, n, i, j, n);
+    const int planted[6][2] = {{3, 7}, {3, 9}, {10, 0}, {11, 5}, {12, 1}, {200, 255}};
+    for (int p = 0; p < 6; p++) C[(size_t)planted[p][0] * n + planted[p][1]] += 1.0f;
+    const int bad = verify(A, B, C, n, n, n, NULL, 0, NULL);
+    OUT("sgemm %d: %s\n", n, bad ? "WRONG" : "CORRECT");
+    const int nbad = count_bad(A, B, C, n, n, n);
+    OUT("sgemm_naive %d: %s (%d bad cells)\n", n, nbad ? "WRONG" : "CORRECT", nbad);
+    free(A); free(B); free(C);
+    return 0;
 }
 
 /* A JSON string body: '"' and '\\' escaped, as the reference escapes the path (gpu_workload.c:224-227). */
@@ -118,6 +167,7 @@ int main(int argc, char **argv) {
         else if (!strcmp(argv[i], "--extra") && i + 1 < argc) parse_list(argv[++i], extra, &n_extra, 8);
         else if (!strcmp(argv[i], "--membw-mb") && i + 1 < argc) membw_mb = atol(argv[++i]);
         else if (!strcmp(argv[i], "--membw-iters") && i + 1 < argc) membw_iters = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--diagnostics-selftest")) return diagnostics_selftest();
         else co_path = argv[i];
     }
     if (membw_mb < 1 || membw_iters < 1) { fprintf(stderr, "bad --membw-mb / --membw-iters\n"); return 2; }
@@ -126,6 +176,13 @@ int main(int argc, char **argv) {
     double ms[3][3] = {{0}}, gf[3][3] = {{0}};
 
     CHK(sgpu_init(0));
+    sgpu_device_props props;
+    CHK(sgpu_get_device_props(0, &props));
+    char arch[64];
+    snprintf(arch, sizeof arch, "%s", props.arch);
+    arch[strcspn(arch, ":")] = 0;
+    /* added line: the device, which selects a consumer's sanity bounds for a text report */
+    OUT("device: %s, %d CUs (%s)\n", props.name, props.compute_units, arch);
     size_t colen = 0;
     const void *image = NULL;
     char *file_image = NULL;
@@ -157,7 +214,7 @@ int main(int argc, char **argv) {
             CHK(sgpu_synchronize());
             if (n == 256) {
                 CHK(sgpu_memcpy_dtoh(C, dC, bytes));
-                const char *verdict = verify(A, B, C, n, n, n, NULL, 0, k->name) ? "WRONG" : "CORRECT";
+                const char *verdict = verify(A, B, C, n, n, n, NULL, 0, v == 0 ? NULL : k->name) ? "WRONG" : "CORRECT";
                 OUT("%s %d: %s\n", v == 0 ? "sgemm" : k->name, n, verdict);
                 if (v == 0) v_sgemm = verdict; else if (v == 1) v_tiled4 = verdict; else v_opt = verdict;
                 if (v == 0 && ks[3].f) {                    /* bisect control (:116-131) */
@@ -165,8 +222,9 @@ int main(int argc, char **argv) {
                     launch(&ks[3], dA, dB, dC, n, n, n, ref_geom);
                     CHK(sgpu_synchronize());
                     CHK(sgpu_memcpy_dtoh(C, dC, bytes));
-                    v_naive = verify(A, B, C, n, n, n, NULL, 0, "sgemm_naive") ? "WRONG" : "CORRECT";
-                    OUT("sgemm_naive %d: %s\n", n, v_naive);
+                    const int nbad = count_bad(A, B, C, n, n, n);
+                    v_naive = nbad ? "WRONG" : "CORRECT";
+                    OUT("sgemm_naive %d: %s (%d bad cells)\n", n, v_naive, nbad);
                 }
             }
             double t0 = now_s();
@@ -257,11 +315,6 @@ int main(int argc, char **argv) {
     }
 
     if (json_mode) {                                       /* schema of gpu_workload.c:222-251 */
-        sgpu_device_props props;
-        CHK(sgpu_get_device_props(0, &props));
-        char arch[64];
-        snprintf(arch, sizeof arch, "%s", props.arch);
-        arch[strcspn(arch, ":")] = 0;
         const char *path = co_path ? co_path : "(embedded switch_gpu)";
         printf("{\"ptx\":\"");
         put_json_str(path);

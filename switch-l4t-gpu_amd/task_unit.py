@@ -1,149 +1,324 @@
-"""Task-queue unit around the gpu_workload harness: run it, check its report, re-check a
-reported result -- the consumer contract of deploy/cluster/gpu_task_example.py:21-128, with
-sanity bounds sized per device instead of the Tegra X1's fixed (1, 1000).
+"""Task-queue unit for the gpu_workload harness on MI355X.
 
-A unit runs `gpu_workload --json <code_object>` (a harness built before --json is re-run
-without it and its text lines are read), and accepts the run only if
-  - the report is complete: the JSON `done` flag is true (text: the WORKLOAD_DONE sentinel);
-  - every kernel verdict of the harness's on-device CPU golden check is CORRECT (the sgemm
-    verdict must be present), and so is every added `sgemm_extra` verdict;
-  - SGEMM timings exist for 256, 512 and 1024, and they and the read bandwidth lie inside the
-    device's sanity bounds (BOUNDS) -- garbage gates, not a second correctness check.
-The device comes from the report's `arch` key (gpu_workload --json on gfx950 adds it); a
-report without one is a Tegra X1 report and gets the reference's bounds.  verify_unit()
-re-checks a reported result dict on the coordinator side with the same bounds.
+A queue worker claims a unit, runs the harness once and hands back a small result dict; the
+coordinator re-checks that dict before it trusts it.  Only the contract is shared with the
+reference consumer (deploy/cluster/gpu_task_example.py:21-24,57-102; deploy/cluster/README.md):
+  * invocation `gpu_workload --json <code object>`; a harness that predates --json reads the
+    flag as its code-object path, fails without printing a JSON object, and is then run
+    without it and read from its text lines;
+  * JSON keys `kernels`, `sgemm` [{n, ms, gflops}], `membw_gbps`, `done`; text lines
+    `<kernel> <n>: CORRECT|WRONG`, `sgemm <n>x<n>x<n>: <t> ms/iter, <g> GFLOPS`,
+    `membw read ...: <g> GB/s`, and the `WORKLOAD_DONE` sentinel;
+  * acceptance: the report is complete, every golden-check verdict is CORRECT (the sgemm one
+    present), SGEMM is timed at n = 256, 512 and 1024, and the numbers pass sanity bounds
+    that catch garbage, not fraud; one unit may take 50 s;
+  * the worker's home lookup: $CLUSTER_GPU_HOME, then ~/switch-l4t-gpu, then ~/gpu.
+
+How this module is organised:
+  Report   one normalised record.  The JSON form, the text form and a coordinator's result
+           dict are each read into it, so everything after reading has one code path.
+  LIMITS   sanity limits per device, picked by the report's `arch` (a gfx950 harness writes
+           it; a report without one comes from a Tegra X1 and keeps the reference's limits).
+  RULES    the acceptance rules as a table of named checks.  audit() applies all of them and
+           returns every finding, so a rejected unit names all of its problems at once.
+  Harness  where a harness lives and how it is invoked: a tuple of invocation forms tried
+           newest first.
 """
 from __future__ import annotations
 
 import json
+import os
 import re
 import subprocess
+from dataclasses import dataclass, field
 
-SIZES = (256, 512, 1024)
-TIMEOUT_S = 50
+REQUIRED_SIZES = (256, 512, 1024)
+UNIT_SECONDS = 50
+MALL_MB = 512            # a read-probe buffer at least this large streams HBM, not the 256 MB MALL
 
-# Sanity bounds (lower, upper) per device.  Upper bounds sit 5% above the device's peak, so
-# only numbers no run can produce are rejected:
-#   tegra-x1  the reference's gates (gpu_task_example.py:23-24; FMA peak ~472 GFLOPS, LPDDR4
-#             25.6 GB/s)
-#   gfx950    MI355X: SGEMM runs on the fp32 matrix cores, 157.3 TFLOP/s dense peak -> 165,165
-#             GFLOPS; the read probe is bounded by HBM3E (8 TB/s -> 8,400 GB/s) when its buffer
-#             is larger than the 256 MB MALL (membw_mb >= 512; the harness default is 1024),
-#             and by the MALL's peak (about 17.2 TB/s -> 18,060 GB/s) when it may sit in it.
-BOUNDS = {
-    "tegra-x1": {"gflops": (1.0, 1000.0), "gbps": (1.0, 1000.0), "gbps_mall": (1.0, 1000.0)},
-    "gfx950": {"gflops": (1.0, 157300.0 * 1.05), "gbps": (1.0, 8000.0 * 1.05), "gbps_mall": (1.0, 17200.0 * 1.05)},
+
+class Rejected(ValueError):
+    """A harness run or a reported result that must not be accepted; `findings` lists why."""
+
+    def __init__(self, findings):
+        self.findings = list(findings)
+        super().__init__("; ".join(self.findings))
+
+
+# ---------------------------------------------------------------------------------------------
+# Device limits.  The upper limits sit 5% above the device's peak, so only a number no run can
+# produce is refused:
+#   tegra-x1  the reference's fixed gates, (1, 1000) for both GFLOPS and GB/s (FMA peak about
+#             472 GFLOPS, LPDDR4 25.6 GB/s)
+#   gfx950    MI355X: SGEMM on the fp32 matrix cores, 157.3 TFLOP/s dense; the read probe is
+#             bounded by HBM3E (8 TB/s) for a buffer past the MALL and by the MALL (about
+#             17.2 TB/s) for one that may sit in it.
+@dataclass(frozen=True)
+class Limits:
+    gflops: tuple
+    gbps_hbm: tuple
+    gbps_mall: tuple
+
+    @classmethod
+    def from_peaks(cls, gflops, hbm_gbps, mall_gbps, slack=1.05):
+        return cls((1.0, gflops * slack), (1.0, hbm_gbps * slack), (1.0, mall_gbps * slack))
+
+
+LIMITS = {
+    "tegra-x1": Limits((1.0, 1000.0), (1.0, 1000.0), (1.0, 1000.0)),
+    "gfx950": Limits.from_peaks(157300.0, 8000.0, 17200.0),
 }
-MALL_MB = 512            # a probe buffer at least this large streams HBM, not the 256 MB MALL
-
-_VERDICT_LINE = re.compile(r"^(sgemm(?:_\w+)?) (\d+): (CORRECT|WRONG)\b", re.M)
-_PERF_LINE = re.compile(r"^sgemm (\d+)x\1x\1: [\d.]+ ms/iter, ([\d.]+) GFLOPS", re.M)
-_MEMBW_LINE = re.compile(r"^membw read \((\d+)MB[^)]*\).* ([\d.]+) GB/s|^membw read .* ([\d.]+) GB/s", re.M)
+UNNAMED_DEVICE = "tegra-x1"
 
 
-class UnitError(ValueError):
-    """The unit's report is incomplete, wrong, or outside the device's sanity bounds."""
+def _number(v):
+    return isinstance(v, (int, float)) and not isinstance(v, bool)
 
 
-def bounds_for(arch: str | None) -> dict:
-    if not arch:
-        return BOUNDS["tegra-x1"]
-    key = arch.split(":")[0]
-    if key not in BOUNDS:
-        raise UnitError(f"no sanity bounds for device {arch!r}")
-    return BOUNDS[key]
+def _inside(v, span):
+    return _number(v) and span[0] <= v <= span[1]
 
 
-def check_numbers(gflops: dict, gbps, arch: str | None = None, membw_mb: int | None = None) -> None:
-    """Every required SGEMM size present with GFLOPS inside the device's bounds, and the read
-    bandwidth inside the HBM bounds (or the MALL bounds for a buffer that may sit in the MALL)."""
-    b = bounds_for(arch)
-    lo, hi = b["gflops"]
-    for size in map(str, SIZES):
-        v = gflops.get(size)
-        if not isinstance(v, (int, float)) or isinstance(v, bool) or not lo <= v <= hi:
-            raise UnitError(f"gflops[{size}] = {v!r} missing or outside the sanity bounds ({lo}, {hi})")
-    glo, ghi = b["gbps"] if (membw_mb is None or membw_mb >= MALL_MB) else b["gbps_mall"]
-    if not isinstance(gbps, (int, float)) or isinstance(gbps, bool) or not glo <= gbps <= ghi:
-        raise UnitError(f"membw {gbps!r} GB/s missing or outside the sanity bounds ({glo}, {ghi})")
+# ---------------------------------------------------------------------------------------------
+# The normalised report.
+_END_MARK = {"json": "the done flag is not true", "text": "no WORKLOAD_DONE sentinel",
+             "result": "the result does not claim correct = true"}
+
+# Text lines, matched from the start of each line (indented diagnostics never match).
+_LINE_KINDS = (
+    ("verdict", re.compile(r"(?P<kernel>sgemm\w*) (?P<n>\d+): (?P<verdict>CORRECT|WRONG)\b")),
+    ("extra", re.compile(r"(?P<kernel>sgemm\w*) (?P<m>\d+)x(?P<n>\d+)x(?P<k>\d+): (?P<verdict>CORRECT|WRONG),")),
+    ("timing", re.compile(r"sgemm (?P<m>\d+)x(?P<n>\d+)x(?P<k>\d+): [\d.]+ ms/iter, (?P<gflops>[\d.]+) GFLOPS")),
+    ("membw", re.compile(r"membw read\b(?: \((?P<mb>\d+)MB)?.*?(?P<gbps>[\d.]+) GB/s")),
+    ("device", re.compile(r"device: .*\((?P<arch>[\w-]+)\)\s*$")),
+    ("end", re.compile(r"WORKLOAD_DONE\b")),
+)
 
 
-def parse_json(out: str) -> dict:
-    """A `gpu_workload --json` report -> result dict (UnitError on any problem)."""
-    try:
-        data = json.loads(out)
-    except json.JSONDecodeError as exc:
-        raise UnitError(f"harness JSON unreadable (truncated?): {exc}") from exc
-    if not isinstance(data, dict) or data.get("done") is not True:
-        raise UnitError("harness JSON incomplete: the done flag is not true")
-    kernels = data.get("kernels")
-    if not isinstance(kernels, dict) or "sgemm" not in kernels:
-        raise UnitError("harness JSON has no sgemm verdict")
-    failed = sorted(k for k, v in kernels.items() if v != "CORRECT")
-    failed += sorted(f"sgemm_extra:{r.get('kernel')}:{r.get('m')}x{r.get('n')}x{r.get('k')}"
-                     for r in data.get("sgemm_extra") or [] if not isinstance(r, dict) or r.get("verdict") != "CORRECT")
-    if failed:
-        raise UnitError(f"kernels failed the harness's CPU golden check: {failed}")
-    gflops = {}
-    for row in data.get("sgemm") or []:
-        if isinstance(row, dict) and isinstance(row.get("n"), int) and isinstance(row.get("gflops"), (int, float)):
-            gflops[str(row["n"])] = float(row["gflops"])
-    missing = [s for s in map(str, SIZES) if s not in gflops]
-    if missing:
-        raise UnitError(f"no SGEMM timing for size(s) {missing}")
-    arch, mb = data.get("arch"), data.get("membw_mb")
-    check_numbers(gflops, data.get("membw_gbps"), arch, mb)
-    return {"correct": True, "kernels_verified": sorted(kernels), "arch": arch, "membw_mb": mb,
-            "gflops": {k: round(v, 1) for k, v in gflops.items()}, "gbps": round(float(data["membw_gbps"]), 1)}
+def _extra_name(kernel, m, n, k):
+    return f"sgemm_extra:{kernel}:{m}x{n}x{k}"
 
 
-def parse_text(out: str, arch: str | None = None) -> dict:
-    """The harness's human-readable lines (a harness without --json) -> result dict."""
-    if "WORKLOAD_DONE" not in out:
-        raise UnitError("harness output incomplete: no WORKLOAD_DONE sentinel")
-    verdicts = {m.group(1): m.group(3) for m in _VERDICT_LINE.finditer(out)}
-    if "sgemm" not in verdicts:
-        raise UnitError("harness printed no sgemm verdict")
-    failed = sorted(k for k, v in verdicts.items() if v != "CORRECT")
-    if failed:
-        raise UnitError(f"kernels failed the harness's CPU golden check: {failed}")
-    gflops = {m.group(1): float(m.group(2)) for m in _PERF_LINE.finditer(out)}
-    missing = [s for s in map(str, SIZES) if s not in gflops]
-    if missing:
-        raise UnitError(f"no SGEMM timing for size(s) {missing}")
-    m = _MEMBW_LINE.search(out)
-    if m is None:
-        raise UnitError("harness printed no membw line")
-    mb = int(m.group(1)) if m.group(1) else None
-    gbps = float(m.group(2) or m.group(3))
-    check_numbers(gflops, gbps, arch, mb)
-    return {"correct": True, "kernels_verified": sorted(verdicts), "arch": arch, "membw_mb": mb,
-            "gflops": {k: round(v, 1) for k, v in gflops.items()}, "gbps": round(gbps, 1)}
+@dataclass
+class Report:
+    form: str                                       # "json", "text" or "result"
+    end_mark: bool = False                          # done: true / WORKLOAD_DONE / correct: true
+    verdicts: dict = field(default_factory=dict)    # golden-check name -> verdict string
+    gflops: dict = field(default_factory=dict)      # square size n -> GFLOPS of the sgemm kernel
+    gbps: object = None                             # the read probe's GB/s, as reported
+    membw_mb: int | None = None                     # the read probe's buffer size, when stated
+    arch: str | None = None
 
+    @classmethod
+    def read(cls, stdout: str, arch: str | None = None) -> "Report":
+        """Harness stdout in either form; `arch` names the device when the text does not."""
+        if stdout.lstrip().startswith("{"):
+            return cls.from_json(stdout)
+        rep = cls.from_text(stdout)
+        rep.arch = rep.arch or arch
+        return rep
 
-def run_unit(binary: str, code_object: str, timeout: float = TIMEOUT_S, arch: str | None = None,
-             extra_args: tuple = ()) -> dict:
-    """One task unit: run the harness on a code object and return its checked result.
-    `arch` names the device for a harness whose text report does not (JSON reports carry it)."""
-    def run(args):
+    @classmethod
+    def from_json(cls, text: str) -> "Report":
         try:
-            return subprocess.run([binary, *args], capture_output=True, text=True, timeout=timeout)
+            data = json.loads(text)
+        except json.JSONDecodeError as exc:
+            raise Rejected([f"JSON report unreadable (truncated?): {exc}"]) from exc
+        if not isinstance(data, dict):
+            raise Rejected(["JSON report incomplete: not an object"])
+        rep = cls("json", end_mark=data.get("done") is True, gbps=data.get("membw_gbps"),
+                  arch=data.get("arch") or None)
+        mb = data.get("membw_mb")
+        rep.membw_mb = mb if _number(mb) else None
+        kernels = data.get("kernels")
+        if isinstance(kernels, dict):
+            rep.verdicts.update(kernels)
+        for row in data.get("sgemm_extra") or ():
+            row = row if isinstance(row, dict) else {}
+            rep.verdicts[_extra_name(row.get("kernel"), row.get("m"), row.get("n"), row.get("k"))] = row.get("verdict")
+        for row in data.get("sgemm") or ():
+            if isinstance(row, dict) and isinstance(row.get("n"), int) and _number(row.get("gflops")):
+                rep.gflops[row["n"]] = float(row["gflops"])
+        return rep
+
+    @classmethod
+    def from_text(cls, text: str) -> "Report":
+        rep = cls("text")
+        for line in text.splitlines():
+            for kind, pat in _LINE_KINDS:
+                m = pat.match(line)
+                if m is None:
+                    continue
+                g = m.groupdict()
+                if kind == "verdict":
+                    rep.verdicts[g["kernel"]] = g["verdict"]
+                elif kind == "extra":
+                    rep.verdicts[_extra_name(g["kernel"], g["m"], g["n"], g["k"])] = g["verdict"]
+                elif kind == "timing" and g["m"] == g["n"] == g["k"]:
+                    rep.gflops[int(g["n"])] = float(g["gflops"])
+                elif kind == "membw" and rep.gbps is None:
+                    rep.gbps = float(g["gbps"])
+                    rep.membw_mb = int(g["mb"]) if g["mb"] else None
+                elif kind == "device":
+                    rep.arch = g["arch"].split(":")[0]
+                elif kind == "end":
+                    rep.end_mark = True
+                break
+        return rep
+
+    @classmethod
+    def from_result(cls, result) -> "Report":
+        """A result dict as summary() makes it, e.g. after a JSON round trip to the coordinator."""
+        d = result if isinstance(result, dict) else {}
+        rep = cls("result", end_mark=d.get("correct") is True, gbps=d.get("gbps"),
+                  membw_mb=d.get("membw_mb"), arch=d.get("arch"))
+        rep.verdicts = {k: "CORRECT" for k in d.get("kernels_verified") or ()}
+        for k, v in (d.get("gflops") or {}).items():
+            if str(k).isdigit():
+                rep.gflops[int(k)] = v
+        return rep
+
+    def summary(self) -> dict:
+        """The result dict a worker reports: JSON-ready, string size keys."""
+        return {"correct": True, "kernels_verified": sorted(k for k in self.verdicts if ":" not in k),
+                "arch": self.arch, "membw_mb": self.membw_mb,
+                "gflops": {str(n): round(float(self.gflops[n]), 1) for n in sorted(self.gflops)},
+                "gbps": round(float(self.gbps), 1)}
+
+
+# ---------------------------------------------------------------------------------------------
+# Acceptance rules.  Each takes the report and its device's limits (None when the device has
+# none) and yields findings.
+def _rule_device(rep, lim):
+    if lim is None:
+        yield f"no sanity bounds for device {rep.arch!r}"
+
+
+def _rule_complete(rep, lim):
+    if not rep.end_mark:
+        yield f"report incomplete: {_END_MARK[rep.form]}"
+
+
+def _rule_golden(rep, lim):
+    if "sgemm" not in rep.verdicts:
+        yield "no sgemm verdict: the harness's golden check did not run"
+    wrong = sorted(str(k) for k, v in rep.verdicts.items() if v != "CORRECT")
+    if wrong:
+        yield f"failed the harness's CPU golden check: {', '.join(wrong)}"
+
+
+def _rule_timed(rep, lim):
+    for n in REQUIRED_SIZES:
+        v = rep.gflops.get(n)
+        if v is None:
+            yield f"no SGEMM timing at n = {n}"
+        elif lim is not None and not _inside(v, lim.gflops):
+            yield f"SGEMM n = {n}: {v!r} GFLOPS outside the sanity bounds {lim.gflops}"
+
+
+def _rule_membw(rep, lim):
+    if lim is None:
+        return
+    span = lim.gbps_hbm if rep.membw_mb is None or rep.membw_mb >= MALL_MB else lim.gbps_mall
+    if not _inside(rep.gbps, span):
+        yield f"membw {rep.gbps!r} GB/s missing or outside the sanity bounds {span}"
+
+
+RULES = (("device", _rule_device), ("complete", _rule_complete), ("golden", _rule_golden),
+         ("timed", _rule_timed), ("membw", _rule_membw))
+
+
+def limits_for(arch: str | None) -> Limits | None:
+    return LIMITS.get((arch or UNNAMED_DEVICE).split(":")[0])
+
+
+def audit(rep: Report) -> list:
+    """Every finding against the report (empty: acceptable)."""
+    lim = limits_for(rep.arch)
+    return [f for _, rule in RULES for f in rule(rep, lim)]
+
+
+def accept(rep: Report) -> dict:
+    """The report's result dict, or Rejected naming every finding."""
+    findings = audit(rep)
+    if findings:
+        raise Rejected(findings)
+    return rep.summary()
+
+
+def recheck(result) -> None:
+    """Coordinator side: re-apply the same rules to a worker's reported result dict."""
+    findings = audit(Report.from_result(result))
+    if findings:
+        raise Rejected(findings)
+
+
+# ---------------------------------------------------------------------------------------------
+# The harness.
+_LAYOUTS = ((("switch-l4t-gpu_amd", "bin", "gpu_workload"), ("switch-l4t-gpu_amd", "build", "switch_gpu.co")),
+            (("gpu_workload",), ("switch_gpu.co",)))
+
+
+@dataclass
+class Harness:
+    binary: str
+    code_object: str
+    timeout: float = UNIT_SECONDS
+    arch: str | None = None          # the device, for a text report that does not name one
+    extra_args: tuple = ()
+
+    # (form, flags placed before the code object), newest first
+    FORMS = (("json", ("--json",)), ("text", ()))
+
+    @classmethod
+    def discover(cls, environ=None, **kw) -> "Harness | None":
+        """The first home holding an executable harness and its code object, in the lookup
+        order $CLUSTER_GPU_HOME, ~/switch-l4t-gpu, ~/gpu; None when this machine has none."""
+        env = os.environ if environ is None else environ
+        homes = [env["CLUSTER_GPU_HOME"]] if env.get("CLUSTER_GPU_HOME") else []
+        user = env.get("HOME") or os.path.expanduser("~")
+        homes += [os.path.join(user, d) for d in ("switch-l4t-gpu", "gpu")]
+        for home in homes:
+            for bin_parts, co_parts in _LAYOUTS:
+                binary, co = os.path.join(home, *bin_parts), os.path.join(home, *co_parts)
+                if os.path.isfile(binary) and os.access(binary, os.X_OK) and os.path.isfile(co):
+                    return cls(binary, co, **kw)
+        return None
+
+    def _spawn(self, flags):
+        argv = [self.binary, *flags, *self.extra_args, self.code_object]
+        try:
+            return subprocess.run(argv, capture_output=True, text=True, timeout=self.timeout)
         except subprocess.TimeoutExpired as exc:
-            raise UnitError(f"harness timed out after {timeout} s") from exc
+            raise Rejected([f"harness timed out after {self.timeout} s"]) from exc
         except OSError as exc:
-            raise UnitError(f"cannot run the harness {binary!r}: {exc}") from exc
+            raise Rejected([f"cannot run the harness {self.binary!r}: {exc}"]) from exc
 
-    proc = run(["--json", *extra_args, code_object])
-    if proc.returncode != 0 and not proc.stdout.lstrip().startswith("{"):
-        proc = run([*extra_args, code_object])        # a harness that reads --json as a path
-    if proc.returncode != 0:
-        raise UnitError(f"harness exited {proc.returncode}: {proc.stderr.strip()[:300]}")
-    out = proc.stdout
-    return parse_json(out) if out.lstrip().startswith("{") else parse_text(out, arch)
+    def report(self) -> Report:
+        """Run the harness in the newest form it understands and read its report."""
+        for i, (form, flags) in enumerate(self.FORMS):
+            proc = self._spawn(flags)
+            if proc.returncode == 0:
+                return Report.read(proc.stdout, self.arch)
+            # A JSON-capable harness that failed still starts its stdout with an object; an
+            # older one took the flag for its code-object path, so the next form is tried.
+            understood = form != "json" or proc.stdout.lstrip().startswith("{")
+            if understood or i + 1 == len(self.FORMS):
+                raise Rejected([f"harness exited {proc.returncode}: {proc.stderr.strip()[:300]}"])
+        raise AssertionError("unreachable")
+
+    def unit(self) -> dict:
+        """One task unit: the checked result dict, or Rejected."""
+        return accept(self.report())
 
 
-def verify_unit(result: dict) -> None:
-    """Coordinator-side re-check of a reported result dict."""
-    if not isinstance(result, dict) or result.get("correct") is not True:
-        raise UnitError("result does not report correct = true (no golden check)")
-    check_numbers(result.get("gflops") or {}, result.get("gbps"), result.get("arch"), result.get("membw_mb"))
+if __name__ == "__main__":
+    import sys
+
+    h = Harness.discover()
+    if h is None:
+        sys.exit("no GPU home ($CLUSTER_GPU_HOME, ~/switch-l4t-gpu, ~/gpu) holds a built harness")
+    try:
+        print(json.dumps(h.unit(), indent=2))
+    except Rejected as exc:
+        sys.exit(f"unit rejected: {exc}")

@@ -63,3 +63,34 @@ def test_round_trip_through_weights_and_bad_sizes(tmp_path):
     for name in ("gpt2_engine", "qwen_engine"):
         r = run([os.path.join(BIN, name), "--weights", str(short)])
         assert r.returncode == 2 and "expected" in r.stderr, (name, r.stderr)
+
+
+def _serial_dot(a, b):
+    """The reference golden's serial fp32 sum of fp32 products (gpu_workload.c:97-98)."""
+    acc = np.float32(0)
+    for p in (a.astype(np.float32) * b.astype(np.float32)):
+        acc = np.float32(acc + p)
+    return acc
+
+
+def test_gpu_workload_mismatch_report(sg):
+    """The harness's golden-check diagnostics (gpu_workload.c:103-131) on planted errors, host
+    only: the first mismatch carries the partial sums over k < 32, 64 and 96, two more follow
+    in the short form, one cell per row, and the naive bisect counts every bad cell."""
+    r = run([os.path.join(BIN, "gpu_workload"), "--diagnostics-selftest"])
+    assert r.returncode == 0, r.stderr
+    lines = r.stdout.splitlines()
+    n = 256
+    A, B = sg.gen_sgemm_inputs(n * n, 42)
+    A, B = A.reshape(n, n), B.reshape(n, n)
+
+    def cell(i, j, kend=n):
+        return _serial_dot(A[i, :kend], B[:kend, j])
+
+    want = [f"  mismatch [3][7]: got {cell(3, 7) + np.float32(1):.4f} want {cell(3, 7):.4f} "
+            f"(k<32:{cell(3, 7, 32):.4f} k<64:{cell(3, 7, 64):.4f} k<96:{cell(3, 7, 96):.4f})",
+            f"  mismatch [10][0]: got {cell(10, 0) + np.float32(1):.4f} want {cell(10, 0):.4f}",
+            f"  mismatch [11][5]: got {cell(11, 5) + np.float32(1):.4f} want {cell(11, 5):.4f}",
+            "sgemm 256: WRONG",
+            "sgemm_naive 256: WRONG (6 bad cells)"]
+    assert lines == want
