@@ -31,6 +31,7 @@ import ctypes as ct
 import itertools
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -428,6 +429,32 @@ def bench_gpt2_decode(prompt_len=8, gen=128):
                 prefill_ms=t_prefill * 1e3)
 
 
+def decode_floor(quick=False):
+    """The decode structure's cost model, measured: bin/decode_floor's dependent-launch,
+    per-phase weight-streaming floor and AQL dispatch legs, and the engine's own in-graph time
+    per launch of each decode phase (sgpu_qwen_phase_times) at three cache lengths, on the
+    random-init Qwen2.5-0.5B-architecture model."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "decode_floor")
+    log(f"decode floor: {exe}")
+    r = subprocess.run([exe] + (["--quick"] if quick else []), capture_output=True, text=True, timeout=600)
+    sys.stderr.write(r.stderr)
+    if r.returncode != 0:
+        raise SystemExit(f"decode_floor exited {r.returncode}")
+    floor = json.loads(r.stdout)
+    cfg = sgpu.qwen_default_cfg()
+    eng = sgpu.QwenEngine(cfg, sgpu.qwen_random_blob(cfg, seed=2024, std=0.02), sgpu.QWEN_PATH_FUSED)
+    phases = {}
+    for pos in (32, 96, 160):
+        ph = eng.phase_times(pos, reps=10 if quick else 30)
+        layer = sum(ph[k] for k in ("qkv", "attention", "o", "gate_up", "down"))
+        ph["layer"] = layer
+        ph["token_sum"] = layer * cfg.NL + ph["lm_head"] + ph["argmax_embed"]
+        phases[str(pos)] = {k: round(v, 3) for k, v in ph.items()}
+        log(f"decode phases at position {pos}: " + ", ".join(f"{k} {v:.2f}" for k, v in ph.items()) + " us")
+    eng.close()
+    return {"decode_floor": floor, "decode_phase_us": phases}
+
+
 def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -581,7 +608,15 @@ def main():
     ap.add_argument("--decode-path", choices=["reference", "fused", "graph"], default="graph")
     ap.add_argument("--decode-model", choices=["qwen", "gpt2"], default="qwen",
                     help="model of the --decode-only leg (gpt2: the graph path)")
+    ap.add_argument("--decode-floor", action="store_true",
+                    help="measure the decode structure's launch and streaming floors and the per-phase "
+                         "in-graph times (one JSON line)")
+    ap.add_argument("--quick", action="store_true", help="fewer repetitions in --decode-floor")
     args = ap.parse_args()
+    if args.decode_floor:
+        sgpu.init(0)
+        print(json.dumps(decode_floor(args.quick)), flush=True)
+        return
     if args.decode_only:
         sgpu.init(0)
         if args.decode_model == "gpt2":

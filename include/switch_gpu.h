@@ -103,8 +103,9 @@ int sgpu_event_elapsed_ms(float *ms, void *start, void *stop);
 
 /* ---- code objects (the PTX modules' role: switch_gpu.ptx, gemv.ptx, gpt2.ptx, qwen.ptx) ----
  * Returns the embedded gfx950 ELF code object named "switch_gpu", "gemv", "gpt2_kernels",
- * "qwen_kernels" or "sgpu_tuned" (and its size), ready for hipModuleLoadData; NULL if the
- * name is unknown.  The first four export the reference's kernel names and arguments. */
+ * "qwen_kernels", "sgpu_tuned", "sgpu_decode" or "sgpu_probe" (and its size), ready for
+ * hipModuleLoadData; NULL if the name is unknown.  The first four export the reference's
+ * kernel names and arguments; "sgpu_probe" holds the measurement kernels of bin/decode_floor. */
 const void *sgpu_code_object(const char *name, size_t *size);
 
 /* Launch geometry the launchers use for a reference-named kernel at a given shape
@@ -370,6 +371,16 @@ int sgpu_qwen_forward_trace(sgpu_qwen *engine, int token, int pos, float *logits
 #define SGPU_QWEN_PATH_FUSED 1
 #define SGPU_QWEN_PATH_GRAPH 2
 int sgpu_qwen_set_path(sgpu_qwen *engine, int path);
+/* In-graph cost of each decode phase on the FUSED kernels at position `pos` (0 <= pos < CTX):
+ * for each phase, its launches for all NL layers recorded in one graph (the argmax and the
+ * lm_head NL times over the same buffers), replayed reps times after a warm-up; us[i] gets the
+ * best replay's time per launch, in the order qkv (RMSNorm + qkv + RoPE + KV write),
+ * attention, o + residual, gate|up (RMSNorm + gate|up + SwiGLU), down + residual, lm_head
+ * (final RMSNorm + lm_head), argmax + next embedding (SGPU_QWEN_NPHASES values).  The replays
+ * overwrite the KV cache at `pos` and the activations; the engine is left at `pos` with token
+ * 0's embedding.  No counterpart in the reference (a measurement of the decode structure). */
+#define SGPU_QWEN_NPHASES 7
+int sgpu_qwen_phase_times(sgpu_qwen *engine, int pos, int reps, float *us);
 /* Greedy decode (the reference generation loop, qwen_engine.c:534-548, without its EOT
  * stop): prime with prompt[0..T-1], then n_gen more positions.  out_tokens receives n_gen + 1
  * ids -- the argmax after the prompt and after each generated position, first max winning.

@@ -17,5 +17,6 @@ EMBED(sgpu_co_gpt2_kernels, "gpt2_kernels.co")
 EMBED(sgpu_co_qwen_kernels, "qwen_kernels.co")
 EMBED(sgpu_co_sgpu_tuned, "sgpu_tuned.co")
 EMBED(sgpu_co_sgpu_decode, "sgpu_decode.co")
+EMBED(sgpu_co_sgpu_probe, "sgpu_probe.co")
 
 .section .note.GNU-stack, "", @progbits

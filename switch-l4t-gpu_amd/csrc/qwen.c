@@ -407,6 +407,70 @@ int sgpu_qwen_forward_trace(sgpu_qwen *e, int token, int pos, float *logits_host
     return forward_reference(e, token, pos, logits_host != NULL, logits_host, trace_host);
 }
 
+/* ---- per-phase timing: each decode phase's 24 layer launches recorded in one graph ---- */
+static int phase_layer(sgpu_qwen *e, int phase, int l) {
+    const sgpu_qwen_cfg *c = &e->cfg;
+    const int C = c->C, FC = c->FC;
+    void *s = (void *)e->stream;
+    switch (phase) {
+    case 0:
+        return sgpu_internal_dec_qkv(e->d_qkvw[l], C, e->L.qkvd, e->d_x, e->d_ln1w[l], c->eps, e->d_qkvb[l], e->d_q,
+                                     e->d_kc[l], e->d_vc[l], e->d_cos, e->d_sin, e->d_step, c->NH, c->NKV, c->HD, s);
+    case 1:
+        return sgpu_internal_dec_attn(e->d_q, e->d_kc[l], e->d_vc[l], e->d_att, e->d_step, c->NH, c->NKV, c->HD,
+                                      (float)(1.0 / sqrt((double)c->HD)), e->d_attn_ws, e->d_attn_cnt, s);
+    case 2: return sgpu_internal_dec_res(e->d_ow[l], C, C, e->d_att, NULL, e->d_x, s);
+    case 3: return sgpu_internal_dec_gateup(e->d_gateupw[l], C, FC, e->d_x, e->d_ln2w[l], c->eps, e->d_down, s);
+    case 4: return sgpu_internal_dec_res(e->d_downw[l], FC, C, e->d_down, NULL, e->d_x, s);
+    case 5: return lm_head(e);
+    default:   /* the argmax and the next token's embedding, without the token list */
+        return sgpu_internal_dec_argmax_next(e->d_logits, c->V, e->d_amax_v, e->d_amax_i, e->d_step, NULL, e->d_emb,
+                                             NULL, NULL, e->d_x, C, c->CTX, s);
+    }
+}
+
+int sgpu_qwen_phase_times(sgpu_qwen *e, int pos, int reps, float *us) {
+    if (!e || !us || reps < 1 || !fused_ok(&e->cfg) || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
+    const int NL = e->cfg.NL;
+    hipEvent_t e0 = NULL, e1 = NULL;
+    int rc = (int)hipEventCreate(&e0);
+    if (!rc) rc = (int)hipEventCreate(&e1);
+    /* phases in order; the argmax (which advances the device position) last */
+    for (int phase = 0; phase < SGPU_QWEN_NPHASES && !rc; phase++) {
+        rc = sgpu_internal_dec_embed(e->d_emb, 0, pos, e->d_x, e->cfg.C, e->d_step, (void *)e->stream);
+        if (rc) break;
+        hipGraph_t g = NULL;
+        hipGraphExec_t ge = NULL;
+        hipError_t he = hipStreamBeginCapture(e->stream, hipStreamCaptureModeRelaxed);
+        if (he != hipSuccess) { rc = (int)he; break; }
+        for (int l = 0; l < NL && !rc; l++) rc = phase_layer(e, phase, l);
+        he = hipStreamEndCapture(e->stream, &g);
+        if (!rc && he != hipSuccess) rc = (int)he;
+        if (!rc) rc = (int)hipGraphInstantiate(&ge, g, NULL, NULL, 0);
+        float best = 1e30f;
+        for (int r = 0; r <= reps && !rc; r++) {           /* r = 0: warm-up */
+            if (phase == SGPU_QWEN_NPHASES - 1)
+                rc = sgpu_internal_dec_embed(e->d_emb, 0, pos, e->d_x, e->cfg.C, e->d_step, (void *)e->stream);
+            if (!rc) rc = (int)hipEventRecord(e0, e->stream);
+            if (!rc) rc = (int)hipGraphLaunch(ge, e->stream);
+            if (!rc) rc = (int)hipEventRecord(e1, e->stream);
+            if (!rc) rc = (int)hipEventSynchronize(e1);
+            float ms = 0;
+            if (!rc) rc = (int)hipEventElapsedTime(&ms, e0, e1);
+            if (!rc && r > 0 && ms < best) best = ms;
+        }
+        if (ge) hipGraphExecDestroy(ge);
+        if (g) hipGraphDestroy(g);
+        if (!rc) us[phase] = best * 1e3f / (float)NL;
+    }
+    /* leave the engine at `pos` with token 0's embedding, as sgpu_qwen_forward would start */
+    if (!rc) rc = sgpu_internal_dec_embed(e->d_emb, 0, pos, e->d_x, e->cfg.C, e->d_step, (void *)e->stream);
+    if (!rc) rc = sgpu_stream_synchronize((void *)e->stream);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    return rc;
+}
+
 /* ---- batched prompt prefill: the prompt's rows go through each layer together, so each
  * layer's weights stream once per chunk of up to PF_ROWS rows instead of once per position ---- */
 #define PF_ROWS 512

@@ -28,8 +28,9 @@ extern const unsigned char sgpu_co_gpt2_kernels[], sgpu_co_gpt2_kernels_end[];
 extern const unsigned char sgpu_co_qwen_kernels[], sgpu_co_qwen_kernels_end[];
 extern const unsigned char sgpu_co_sgpu_tuned[], sgpu_co_sgpu_tuned_end[];
 extern const unsigned char sgpu_co_sgpu_decode[], sgpu_co_sgpu_decode_end[];
+extern const unsigned char sgpu_co_sgpu_probe[], sgpu_co_sgpu_probe_end[];
 
-enum { MOD_SWITCH, MOD_GEMV, MOD_GPT2, MOD_QWEN, MOD_TUNED, MOD_DECODE, NMOD };
+enum { MOD_SWITCH, MOD_GEMV, MOD_GPT2, MOD_QWEN, MOD_TUNED, MOD_DECODE, MOD_PROBE, NMOD };
 static const struct {
     const char *name;
     const unsigned char *start, *end;
@@ -40,6 +41,7 @@ static const struct {
     {"qwen_kernels", sgpu_co_qwen_kernels, sgpu_co_qwen_kernels_end},
     {"sgpu_tuned", sgpu_co_sgpu_tuned, sgpu_co_sgpu_tuned_end},
     {"sgpu_decode", sgpu_co_sgpu_decode, sgpu_co_sgpu_decode_end},
+    {"sgpu_probe", sgpu_co_sgpu_probe, sgpu_co_sgpu_probe_end},
 };
 
 /* Every kernel the launchers use: (module, symbol). */

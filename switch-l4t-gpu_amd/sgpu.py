@@ -128,6 +128,7 @@ _SIGS = {
     "sgpu_qwen_device_logits": (_P, [_P]),
     "sgpu_qwen_set_path": (_I, [_P, _I]),
     "sgpu_qwen_generate": (_I, [_P, _P, _I, _I, _P]),
+    "sgpu_qwen_phase_times": (_I, [_P, _I, _I, _P]),
     "sgpu_qwen_prefill": (_I, [_P, _P, _I, _P]),
     "sgpu_gen_sgemm_inputs": (None, [_P, _P, _S, ct.c_uint]),
     "sgpu_frand": (_F, [ct.POINTER(ct.c_uint64)]),
@@ -380,6 +381,7 @@ def qwen_random_blob(cfg: QwenCfg, seed: int, std: float = 0.02) -> np.ndarray:
 
 
 QWEN_PATH_REFERENCE, QWEN_PATH_FUSED, QWEN_PATH_GRAPH = 0, 1, 2
+QWEN_PHASES = ("qkv", "attention", "o", "gate_up", "down", "lm_head", "argmax_embed")
 
 
 class QwenEngine:
@@ -413,6 +415,12 @@ class QwenEngine:
         trace = np.empty((self.cfg.NL, self.cfg.C), np.float32)
         call("sgpu_qwen_forward_trace", self.h, token, pos, self.logits.ctypes.data, trace.ctypes.data)
         return self.logits, trace
+
+    def phase_times(self, pos: int, reps: int = 20) -> dict:
+        """In-graph us per launch of each decode phase at position pos (sgpu_qwen_phase_times)."""
+        us = np.zeros(len(QWEN_PHASES), np.float32)
+        call("sgpu_qwen_phase_times", self.h, pos, reps, us.ctypes.data)
+        return {k: float(v) for k, v in zip(QWEN_PHASES, us)}
 
     def prefill(self, ids) -> np.ndarray:
         """Positions 0..len(ids)-1 in one batched pass; logits of the last row."""

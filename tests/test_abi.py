@@ -54,7 +54,7 @@ def test_library_exports_every_header_function(sg):
     assert set(declared) <= set(sg._SIGS), set(declared) - set(sg._SIGS)
 
 
-@pytest.mark.parametrize("module", sorted(REFERENCE_KERNELS) + ["sgpu_tuned"])
+@pytest.mark.parametrize("module", sorted(REFERENCE_KERNELS) + ["sgpu_tuned", "sgpu_probe"])
 def test_code_objects_embedded(sg, module):
     size = ct.c_size_t()
     p = sg.lib().sgpu_code_object(module.encode(), ct.byref(size))
@@ -66,6 +66,8 @@ def test_code_objects_embedded(sg, module):
     assert flags & 0x300 != 0x300                # not an xnack+ code object
     if module in REFERENCE_KERNELS:
         assert REFERENCE_KERNELS[module] <= names, REFERENCE_KERNELS[module] - names
+    elif module == "sgpu_probe":
+        assert {"sgpu_probe_stream", "sgpu_probe_link"} <= names
     else:
         assert {f"sgpu_gemv_h_l16_s7", "sgpu_gemv_f32_l64_s3", "sgpu_embed_h"} <= names
 

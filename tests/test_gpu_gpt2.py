@@ -238,16 +238,22 @@ FULL = dict(V=50257, C=768, NL=12, NH=12, HD=64, FC=3072, CTX=1024)
 
 
 def check_position(p, got, ref, gaps, stats):
-    """Logits within 1e-4 of the logit scale (fp32 weights); the argmax equal unless the
-    reference's top two are within 4x this position's largest difference (a near-tie)."""
-    err = np.abs(got - ref)
+    """Logits within 1e-4 (fp32 weights) of the logit scale; the argmax equal unless the reference's margin of
+    its top token over the GPU's pick is within 4x this position's RMS logit error (a near-tie,
+    counted and printed).  The RMS, not the largest error, sets the bar: a flip is always
+    within twice the largest error of the two logits involved, so only an outlier error on
+    exactly those two logits can flip a wider margin, and that fails the test."""
+    err = np.abs(got.astype(np.float64) - ref)
     stats["worst"] = max(stats["worst"], float(err.max() / np.abs(ref).max()))
     assert err.max() <= 1e-4 * np.abs(ref).max(), (p, float(err.max()), float(np.abs(ref).max()))
     top2 = np.sort(ref)[-2:]
     gaps.append(float(top2[1] - top2[0]))
     g_tok, c_tok = int(np.argmax(got)), int(np.argmax(ref))
     if g_tok != c_tok:
-        assert ref[c_tok] - ref[g_tok] <= 4 * float(err.max()), (p, g_tok, c_tok, gaps[-1])
+        rms = float(np.sqrt(np.mean(err * err)))
+        margin = float(ref[c_tok] - ref[g_tok])
+        stats.setdefault("flips", []).append((p, c_tok, g_tok, margin, rms))
+        assert margin <= 4 * rms, (p, g_tok, c_tok, margin, rms)
         stats["ties"] += 1
     return g_tok
 
@@ -272,7 +278,7 @@ def test_engine_full_teacher_forced(gpu, full_spec, path):
         check_position(p, eng.forward(t, p, True).copy(), logits[p], gaps, stats)
     eng.close()
     say(f"{path}: 64 teacher-forced positions, worst logit error {stats['worst']:.2e} of scale, "
-        f"min top-1/top-2 gap {min(gaps):.3e}, median {np.median(gaps):.3e}, near-ties {stats['ties']}")
+        f"min top-1/top-2 gap {min(gaps):.3e}, median {np.median(gaps):.3e}, near-ties {stats['ties']} {stats.get('flips', [])}")
     assert stats["ties"] <= 2
 
 

@@ -278,6 +278,28 @@ def test_engine_small_generate(gpu, og, path):
     eng.close()
 
 
+def test_phase_times_leave_the_engine_usable(gpu):
+    """sgpu_qwen_phase_times replays every decode phase (the argmax advancing the device position
+    on each launch) and restores the position: afterwards greedy decoding still equals a fresh
+    engine's, every phase time is positive, and a position outside the cache is refused."""
+    cfg = gpu.qwen_cfg(**SMALL)
+    blob = gpu.qwen_random_blob(cfg, seed=33, std=0.15)
+    prompt = [int(v) for v in np.random.default_rng(5).integers(0, SMALL["V"], 9)]
+    fresh = gpu.QwenEngine(cfg, blob, PATHS["graph"])
+    want = fresh.generate(prompt, 20).tolist()
+    fresh.close()
+    eng = gpu.QwenEngine(cfg, blob, PATHS["graph"])
+    for pos in (0, 7, SMALL["CTX"] - 1):
+        t = eng.phase_times(pos, reps=3)
+        say(f"phase times at {pos}: {t}")
+        assert all(v > 0 and np.isfinite(v) for v in t.values()), t
+    assert eng.generate(prompt, 20).tolist() == want
+    us = np.zeros(len(gpu.QWEN_PHASES), np.float32)
+    for bad in (-1, SMALL["CTX"]):
+        assert gpu.lib().sgpu_qwen_phase_times(eng.h, bad, 3, us.ctypes.data) != 0
+    eng.close()
+
+
 def test_engine_full_generate_graph_token_identical(gpu, og):
     """Full Qwen2.5-0.5B architecture, graph path, on-device greedy loop: 32-token prompt,
     64 generated positions; the CPU golden, fed the same ids, picks the same argmax at every
@@ -384,16 +406,22 @@ def rich_variant(blob, c, seed=7, proj_scale=2.0):
 
 
 def check_position(p, got, ref, gaps, stats):
-    """Logits within 1e-3 of the logit scale; the argmax equal unless the reference's top two
-    are within 4x this position's largest difference (a near-tie; counted and printed)."""
-    err = np.abs(got - ref)
+    """Logits within 1e-3 of the logit scale; the argmax equal unless the reference's margin of
+    its top token over the GPU's pick is within 4x this position's RMS logit error (a near-tie,
+    counted and printed).  The RMS, not the largest error, sets the bar: a flip is always
+    within twice the largest error of the two logits involved, so only an outlier error on
+    exactly those two logits can flip a wider margin, and that fails the test."""
+    err = np.abs(got.astype(np.float64) - ref)
     stats["worst"] = max(stats["worst"], float(err.max() / np.abs(ref).max()))
     assert err.max() <= 1e-3 * np.abs(ref).max(), (p, float(err.max()), float(np.abs(ref).max()))
     top2 = np.sort(ref)[-2:]
     gaps.append(float(top2[1] - top2[0]))
     g_tok, c_tok = int(np.argmax(got)), int(np.argmax(ref))
     if g_tok != c_tok:
-        assert ref[c_tok] - ref[g_tok] <= 4 * float(err.max()), (p, g_tok, c_tok, gaps[-1])
+        rms = float(np.sqrt(np.mean(err * err)))
+        margin = float(ref[c_tok] - ref[g_tok])
+        stats.setdefault("flips", []).append((p, c_tok, g_tok, margin, rms))
+        assert margin <= 4 * rms, (p, g_tok, c_tok, margin, rms)
         stats["ties"] += 1
     return g_tok
 
@@ -423,7 +451,7 @@ def test_engine_full_teacher_forced(gpu, full_spec, path):
         check_position(p, eng.forward(t, p, True).copy(), logits[p], gaps, stats)
     eng.close()
     say(f"{path}: 64 teacher-forced positions, worst logit error {stats['worst']:.2e} of scale, "
-        f"min top-1/top-2 gap {min(gaps):.3e}, median {np.median(gaps):.3e}, near-ties {stats['ties']}")
+        f"min top-1/top-2 gap {min(gaps):.3e}, median {np.median(gaps):.3e}, near-ties {stats['ties']} {stats.get('flips', [])}")
     assert stats["ties"] <= 2
 
 

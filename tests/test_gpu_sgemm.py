@@ -684,10 +684,12 @@ def test_full_size_integer_exact(gpu, fn, n):
     assert np.array_equal(C, want.astype(np.float32))
 
 
-@pytest.mark.parametrize("fn", ["sgpu_sgemm_tiled", "sgpu_sgemm_opt"])
-def test_4096_reference_generator_sampled_rows(gpu, og, fn):
-    n = 4096
-    say(f"sgemm {fn} 4096 reference inputs, sampled rows")
+@pytest.mark.parametrize("n", [2048, 4096])
+@pytest.mark.parametrize("fn", ["sgpu_sgemm_tiled", "sgpu_sgemm_tiled4", "sgpu_sgemm_opt"])
+def test_full_size_reference_generator_sampled_rows(gpu, og, fn, n):
+    """The sweep's 2048^3 and 4096^3 on the reference generator's inputs: 24 rows spread over
+    C against the oracle's serial golden, normwise <= 1e-4 and the 5% verdict clean."""
+    say(f"sgemm {fn} {n}^3 reference inputs, sampled rows")
     A, B = ref_inputs(n, n, n)
     C = run_sgemm(gpu, fn, A, B, n, n, n)
     rows = np.linspace(0, n - 1, 24).astype(int)
