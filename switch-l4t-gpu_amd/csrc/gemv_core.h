@@ -525,37 +525,164 @@ __device__ __forceinline__ void gemv_xreg_hh(const uint16_t* __restrict__ W, con
 __device__ __forceinline__ XPlain x_source(const float* x) { return XPlain{x}; }
 __device__ __forceinline__ XHalf x_source(const uint16_t* x) { return XHalf{x}; }
 
+// The team GEMV of the reference-named symbols: a team of LPR lanes per row (16, 32 or 64; a
+// block iteration covers 256/LPR rows), each lane owning up to S fixed 16-byte segments of
+// every row (as gemv_team<WT, LPR, S>), but with x staged once per block in LDS as fp32 (fp16-bit
+// x converted there as XHalf converts it) and read back for each row, so a lane's registers hold
+// only its weight segments.  Blocks 0..nb-1 walk the row blocks with stride nb, the next one's
+// weights fetched one block ahead of use.  Preconditions (gemv_byname): blockDim 256,
+// K % VEC == 0, K <= LPR*S*VEC, W and x 16-byte aligned, xs holds K floats.
+template <class WT, int LPR, int S, int NR, class XT>
+__device__ __forceinline__ void gemv_team_xlds(const typename WT::elem* __restrict__ W, const XT* __restrict__ x,
+                                               const float* __restrict__ bias, float* __restrict__ y, int K, int N,
+                                               int nb, float* __restrict__ xs) {
+    static_assert(LPR == 16 || LPR == 32 || LPR == 64, "teams within one wave");
+    typedef typename WT::vec vec;
+    constexpr int VEC = WT::VEC, TEAMS = 256 / LPR, RPB = TEAMS * NR;   // rows per block iteration
+    const int tid = threadIdx.x, team = tid / LPR, sub = tid % LPR;
+    const int nseg = K / VEC;
+    bool has[S];
+#pragma unroll
+    for (int j = 0; j < S; j++) has[j] = sub + LPR * j < nseg;
+    if ((int)blockIdx.x >= nb) return;                // block-uniform
+    vec w[NR][S];
+    int row[NR];
+    bool valid[NR];
+    float b[NR];
+    auto fetch = [&](int rb) {
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const int t = (rb * TEAMS + team) * NR + r;
+            valid[r] = t < N;
+            row[r] = valid[r] ? t : 0;
+            b[r] = 0.0f;
+            if (valid[r]) {
+                const vec* rv = reinterpret_cast<const vec*>(W + (size_t)row[r] * K) + sub;
+#pragma unroll
+                for (int j = 0; j < S; j++)
+                    if (has[j]) w[r][j] = sgpu_ldnt(rv + LPR * j);
+                b[r] = bias ? bias[row[r]] : 0.0f;
+            }
+        }
+    };
+    int rb = blockIdx.x;
+    if (rb * RPB < N) fetch(rb);
+    const auto src = x_source(x);
+    for (int k = 4 * tid; k < K; k += 4 * 256) {
+        sgpu_f32x4 v = src.load4(k);
+        if constexpr (std::is_same<XT, uint16_t>::value) {
+            const uint32_t u0 = __float_as_uint(v[0]), u1 = __float_as_uint(v[1]);
+            v = sgpu_f32x4{WF16::cvt(u0 & 0xffffu), WF16::cvt(u0 >> 16), WF16::cvt(u1 & 0xffffu), WF16::cvt(u1 >> 16)};
+        }
+        *reinterpret_cast<sgpu_f32x4*>(xs + k) = v;
+    }
+    __syncthreads();
+    for (; rb * RPB < N; rb += nb) {                  // block-uniform loop
+        bool cur_valid[NR];
+        int cur_row[NR];
+        float cur_b[NR], acc[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            cur_valid[r] = valid[r];
+            cur_row[r] = row[r];
+            cur_b[r] = b[r];
+            acc[r] = 0.0f;
+        }
+        // x in rounds of U segments (16 floats): all of a round's LDS reads are issued before its
+        // FMAs (the scheduler is kept from merging rounds, which would hold every segment's x in
+        // registers at once), and one read of a segment's x serves the NR rows
+        constexpr int U = 16 / VEC;
+#pragma unroll
+        for (int j0 = 0; j0 < S; j0 += U) {
+            float xa[U][VEC];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int j = j0 + u;
+                const sgpu_f32x4* xp = reinterpret_cast<const sgpu_f32x4*>(xs + (sub + LPR * j) * VEC);
+#pragma unroll
+                for (int q = 0; q < VEC / 4; q++) {
+                    const sgpu_f32x4 a = (j < S && has[j]) ? xp[q] : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) xa[u][4 * q + e] = a[e];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int j = j0 + u;
+                if (j >= S || !has[j]) continue;
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    if (cur_valid[r]) acc[r] = WT::dot(w[r][j], xa[u], acc[r]);
+            }
+            __asm__ volatile("" ::: "memory");       // rounds stay in order: U segments of x live at a time
+        }
+        // the next row block's weights load into the registers this one's just left: the dot
+        // products are pinned before the fetch (each sum is an operand of an empty asm), so the
+        // two sets of weights are never live together
+#pragma unroll
+        for (int r = 0; r < NR; r++) __asm__ volatile("" : "+v"(acc[r]));
+        __asm__ volatile("" ::: "memory");
+        if ((rb + nb) * RPB < N) fetch(rb + nb);
+#pragma unroll
+        for (int r = 0; r < NR; r++) acc[r] = sgpu_group_sum<LPR>(acc[r]);
+        if (sub == LPR - 1) {
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                if (!cur_valid[r]) continue;
+                float a = acc[r];
+                if (WT::NEEDS_RECHECK && !__builtin_isfinite(a)) a = recompute_row_x<WT>(W + (size_t)cur_row[r] * K, src, K);
+                y[cur_row[r]] = a + cur_b[r];
+            }
+        }
+    }
+}
+
 // Body of the reference-named GEMV symbols (gemv, gemv4, gemv_warp, gemv_warp_b, gemv_h,
 // gemv_hh), which hosts launch by name with their own geometry -- (N+7)/8 or (N+255)/256
 // blocks of 256 in the reference callers.  When the launch has 1-D blocks of 256 threads and
-// 16-byte aligned rows, with at least one block per 8 rows, it runs the team GEMV on at most
-// kByNameBlocks blocks (a persistent
-// grid: those blocks walk the row blocks with the next one's weights in flight, surplus blocks
-// exit), with a team shape sized to the decoder rows: fp32 16 lanes x 12 segments (K <= 768),
-// 64 x 16 (K <= 4096); fp16 16 x 7 (K <= 896), 64 x 10 (K <= 5120); 256 x 8 beyond, up to 2048
-// segments.  Other launches (unaligned rows, other block shapes, longer rows) take the
-// wave-per-row kernel.  The choice is block-uniform.
-constexpr int kByNameBlocks = 2048;      // 8 per CU on MI355X's 256 CUs
+// 16-byte aligned rows, with at least one block per 8 rows, it runs a team GEMV on a capped
+// number of blocks (a persistent grid: those blocks walk the row blocks with the next one's
+// weights in flight; surplus blocks exit):
+//  * fp16 weights (gemv_h, gemv_hh): x staged in LDS (gemv_team_xlds), 16 lanes x 7 segments
+//    (K <= 896), then 64 lanes x 10 segments with two rows per team (K <= 5120); at most
+//    4608 blocks (18 per CU).  With x in LDS a lane's registers hold only its weights, so the
+//    symbols take 4 waves per SIMD where x in registers (the wide member's 80 floats of it)
+//    allowed 3;
+//  * fp32 weights: x in registers (gemv_team), 16 x 12 (K <= 768), 64 x 16 (K <= 4096), 256 x 8
+//    beyond, up to 2048 segments; at most 2048 blocks (8 per CU).  For fp32 the LDS form gains
+//    on the GPT-2 lm_head but loses more on its 3072-wide rows.
+// Other launches (unaligned rows, other block shapes, longer rows) take the wave-per-row
+// kernel.  The choice is block-uniform.
 template <class WT, class XT>
 __device__ __forceinline__ void gemv_byname(const typename WT::elem* __restrict__ W, const XT* __restrict__ x,
                                             const float* __restrict__ bias, float* __restrict__ y, int K, int N) {
     constexpr int VEC = WT::VEC;
-    constexpr bool H = VEC == 8;
     // a grid of one thread per row or fewer ((N+255)/256 blocks, gemv_test.c:108) keeps a wave
     // per row: with so few waves the team kernel's one row block in flight per block is slower
     const bool team = blockDim.x == 256 && blockDim.y == 1 && blockDim.z == 1 && gridDim.y == 1 &&
                       gridDim.z == 1 && K > 0 && K % VEC == 0 && ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0 &&
                       (long long)gridDim.x * 8 >= N;
-    const int nseg = K / VEC, nb = min((int)gridDim.x, kByNameBlocks);
-    constexpr int S16 = H ? 7 : 12, S64 = H ? 10 : 16;
-    if (team && nseg <= 16 * S16)
-        gemv_team<WT, 16, S16, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
-    else if (team && nseg <= 64 * S64)
-        gemv_team<WT, 64, S64, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
-    else if (team && nseg <= 256 * 8)
-        gemv_team<WT, 256, 8, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
-    else
-        gemv_generic<WT, XT>(W, x, bias, y, K, N);
+    const int nseg = K / VEC;
+    if constexpr (VEC == 8) {
+        const int nb = min((int)gridDim.x, 4608);
+        __shared__ __attribute__((aligned(16))) float xs[64 * 10 * VEC];
+        if (team && nseg <= 16 * 7)
+            gemv_team_xlds<WT, 16, 7, 1, XT>(W, x, bias, y, K, N, nb, xs);
+        else if (team && nseg <= 64 * 10)
+            gemv_team_xlds<WT, 64, 10, 2, XT>(W, x, bias, y, K, N, nb, xs);
+        else
+            gemv_generic<WT, XT>(W, x, bias, y, K, N);
+    } else {
+        const int nb = min((int)gridDim.x, 2048);
+        if (team && nseg <= 16 * 12)
+            gemv_team<WT, 16, 12, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
+        else if (team && nseg <= 64 * 16)
+            gemv_team<WT, 64, 16, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
+        else if (team && nseg <= 256 * 8)
+            gemv_team<WT, 256, 8, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
+        else
+            gemv_generic<WT, XT>(W, x, bias, y, K, N);
+    }
 }
 
 // ---------------------------------------------------------------------------------------

@@ -187,6 +187,41 @@ def test_integer_exact_reference_geometry(gpu, hip, module, sym, N, K):
     assert np.array_equal(y, (Wi @ xi + (bi if bias is not None else 0)).astype(np.float32))
 
 
+@pytest.mark.parametrize("N,K", [(41, 896), (37, 4864)])
+@pytest.mark.parametrize("sym", ["gemv_h", "gemv_hh"])
+def test_special_codes_reference_geometry(gpu, hip, og, sym, N, K):
+    """The fp16 by-name symbols at (N+7)/8 blocks, narrow (16-lane teams) and wide (64-lane
+    teams, two rows each; N odd leaves the last team one row) rows, x staged in LDS: subnormal
+    and -0 codes read +0, exponent-31 codes 2^16 (1 + m/1024) in W and, for gemv_hh, in x
+    (rows whose fast sum is not finite are recomputed with the exact decode).  Integer-valued
+    operands keep every partial sum exact, so the results are compared bit for bit with the
+    oracle's serial decode."""
+    say(f"by name {sym} special codes {N}x{K}")
+    rng = np.random.default_rng(N * K)
+    big = np.concatenate([np.arange(0x7c00, 0x8000), np.arange(0xfc00, 0x10000)]).astype(np.uint16)
+    small = np.concatenate([np.arange(0, 1024), np.arange(0x8000, 0x8400),
+                            np.array([0x3c00, 0x4000, 0x4200, 0xbc00, 0xc000] * 60)]).astype(np.uint16)
+    W = rng.choice(small, (N, K)).astype(np.uint16)
+    xbig = rng.choice(K, 4, replace=False)         # exponent-31 x positions (gemv_hh)
+    cols = np.setdiff1d(np.arange(K), xbig)        # exponent-31 weights elsewhere: no big x big product
+    for r in range(0, N, 3):                       # exponent-31 weights in every third row
+        W[r, rng.choice(cols, 8, replace=False)] = rng.choice(big, 8)
+    xi = rng.integers(-2, 3, K)
+    bias = rng.integers(-5, 6, N).astype(np.float32)
+    grid = ((N + 7) // 8, 1)
+    if sym == "gemv_h":
+        x = xi.astype(np.float32)
+        y = run_gemv(gpu, hip, "qwen_kernels", sym, grid, W, x, bias, K, N)
+        ref = og.gemv_h_fbias(W, x, bias, K, N, NT)
+    else:
+        x16 = xi.astype(np.float16).view(np.uint16)
+        x16[rng.choice(cols, 16, replace=False)] = rng.choice(small[:2048], 16)   # subnormal, -0
+        x16[xbig] = rng.choice(big, 4)                                            # exponent 31
+        y = run_gemv(gpu, hip, "qwen_kernels", sym, grid, W, x16, bias, K, N)
+        ref = og.gemv_hh(W, x16, bias, K, N, NT)
+    assert np.array_equal(y, ref)
+
+
 @pytest.mark.parametrize("co,args", [("gemv", ["4096", "4096"]), ("gpt2_kernels", ["2304", "768", "--bias"]),
                                      ("qwen_kernels", ["151936", "896", "--h", "--normal"]),
                                      ("qwen_kernels", ["9728", "896", "--hh", "--normal"]),
