@@ -177,14 +177,16 @@ int sgpu_sgemm_kwave_edge(const float *A, const float *B, float *C, int M, int N
  * Split-K workspaces (also used by sgpu_sgemm_opt and sgpu_gemv_multi when they split K): one
  * per stream, so launches on different streams or from different host threads may overlap;
  * launches on one stream run in order.  The null stream's is made by sgpu_init; another
- * stream's on its first split launch (32 MB + 64 KB, at most 32 streams per device), kept
- * until sgpu_stream_destroy releases it (streams not made by sgpu_stream_create keep theirs
- * until the process ends).  A stream being recorded (sgpu_graph_begin) cannot get one: make
- * its first split launch before recording, else sgpu_sgemm_splitk returns
- * SGPU_ERR_NO_WORKSPACE and sgpu_sgemm_opt / sgpu_gemv_multi launch their unsplit kernels
- * instead.  A recorded graph uses the workspace of the stream it was recorded on: do not
- * replay it concurrently with itself or with other split launches on that stream, nor after
- * that stream is destroyed. */
+ * stream's on its first launch that splits (32 MB + 64 KB, at most 32 streams per device),
+ * kept until sgpu_stream_destroy releases it (streams not made by sgpu_stream_create keep
+ * theirs until the process ends).  hipStreamPerThread names a different stream in every host
+ * thread and gets none: sgpu_sgemm_splitk returns SGPU_ERR_NO_WORKSPACE on it.  A stream
+ * being recorded (sgpu_graph_begin) cannot get one: make its first split launch before
+ * recording, else sgpu_sgemm_splitk returns SGPU_ERR_NO_WORKSPACE; on either kind of stream
+ * sgpu_sgemm_opt / sgpu_gemv_multi launch their unsplit kernels instead.  A recorded graph
+ * uses the workspace of the stream it was recorded on, which stays allocated while the graph
+ * exists, also after that stream is destroyed; do not replay the graph concurrently with
+ * itself or with other split launches on that stream. */
 int sgpu_sgemm_splitk(const float *A, const float *B, float *C, int M, int N, int K, int S, void *stream);
 /* sgpu_sgemm_splitk that allocates nothing, for callers that cannot allocate device memory
  * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc).  No

@@ -111,6 +111,8 @@ typedef struct {
         void *stream;
         float *ws;
         unsigned *cnt;
+        int graphs;           /* recorded graphs (sgpu_graph_end) that reference this workspace */
+        int orphan;           /* its stream was destroyed while graphs still referenced it */
     } sk[SK_STREAMS];
     int nsk;
 } devstate;
@@ -250,9 +252,12 @@ out:
  * streams already hold one). */
 static int sk_workspace(devstate *d, void *stream, float **ws, unsigned **cnt) {
     int rc = SGPU_ERR_NO_WORKSPACE;
+    /* hipStreamPerThread is one handle value naming a different stream in every host thread:
+     * a workspace keyed by it would be shared by streams that run concurrently */
+    if (stream == (void *)hipStreamPerThread) return rc;
     pthread_mutex_lock(&g_lock);
     for (int i = 0; i < d->nsk; i++)
-        if (d->sk[i].stream == stream) {
+        if (!d->sk[i].orphan && d->sk[i].stream == stream) {
             *ws = d->sk[i].ws;
             *cnt = d->sk[i].cnt;
             rc = SGPU_OK;
@@ -274,6 +279,7 @@ static int sk_workspace(devstate *d, void *stream, float **ws, unsigned **cnt) {
     d->sk[d->nsk].stream = stream;
     d->sk[d->nsk].ws = *ws = w;
     d->sk[d->nsk].cnt = *cnt = c;
+    d->sk[d->nsk].graphs = d->sk[d->nsk].orphan = 0;
     d->nsk++;
     rc = SGPU_OK;
 out:
@@ -401,19 +407,87 @@ int sgpu_stream_create(void **stream) {
     *stream = (void *)st;
     return SGPU_OK;
 }
-/* Free the split-K workspaces of `stream` (its work finished) and drop them from the tables. */
+/* Recorded graphs that reference a split-K workspace (the one of the stream they were recorded
+ * on), so that the workspace outlives its stream until the last such graph is destroyed. */
+typedef struct {
+    void *graph;
+    int dev;
+    float *ws;
+} graph_ref;
+static graph_ref *g_graph_refs;
+static int g_ngraph_refs, g_cap_graph_refs;
+
+/* Drop slot i of device dev's workspace table (g_lock held). */
+static void sk_drop(devstate *d, int i) {
+    hipFree(d->sk[i].ws);
+    hipFree(d->sk[i].cnt);
+    d->sk[i] = d->sk[--d->nsk];
+}
+
+/* Release the split-K workspaces of `stream` (its work finished): freed now, or, while recorded
+ * graphs still reference them, kept (no longer found by the stream) until the last of those
+ * graphs is destroyed. */
 static void sk_release(void *stream) {
     pthread_mutex_lock(&g_lock);
     for (int dev = 0; dev < SGPU_MAX_DEVICES; dev++) {
         devstate *d = &g_dev[dev];
         if (!__atomic_load_n(&d->ready, __ATOMIC_RELAXED)) continue;
         for (int i = 1; i < d->nsk; i++)
-            if (d->sk[i].stream == stream) {
-                hipFree(d->sk[i].ws);
-                hipFree(d->sk[i].cnt);
-                d->sk[i] = d->sk[--d->nsk];
+            if (!d->sk[i].orphan && d->sk[i].stream == stream) {
+                if (d->sk[i].graphs > 0) d->sk[i].orphan = 1;
+                else sk_drop(d, i);
                 break;
             }
+    }
+    pthread_mutex_unlock(&g_lock);
+}
+
+/* graph was recorded on stream: if the stream has a workspace, count the graph against it. */
+static int sk_graph_recorded(void *graph, void *stream) {
+    int rc = SGPU_OK;
+    pthread_mutex_lock(&g_lock);
+    for (int dev = 0; dev < SGPU_MAX_DEVICES && !rc; dev++) {
+        devstate *d = &g_dev[dev];
+        if (!__atomic_load_n(&d->ready, __ATOMIC_RELAXED)) continue;
+        for (int i = 1; i < d->nsk; i++)
+            if (!d->sk[i].orphan && d->sk[i].stream == stream) {
+                if (g_ngraph_refs == g_cap_graph_refs) {
+                    const int cap = g_cap_graph_refs ? 2 * g_cap_graph_refs : 16;
+                    graph_ref *p = realloc(g_graph_refs, (size_t)cap * sizeof *p);
+                    if (!p) { rc = SGPU_ERR_HOST_ALLOC; break; }
+                    g_graph_refs = p;
+                    g_cap_graph_refs = cap;
+                }
+                g_graph_refs[g_ngraph_refs++] = (graph_ref){graph, dev, d->sk[i].ws};
+                d->sk[i].graphs++;
+                break;
+            }
+    }
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+/* graph is being destroyed: uncount it, and free an orphaned workspace it held last (after the
+ * device's work, which may include its replays, has finished). */
+static void sk_graph_destroyed(void *graph) {
+    pthread_mutex_lock(&g_lock);
+    for (int r = 0; r < g_ngraph_refs; r++) {
+        if (g_graph_refs[r].graph != graph) continue;
+        devstate *d = &g_dev[g_graph_refs[r].dev];
+        for (int i = 1; i < d->nsk; i++)
+            if (d->sk[i].ws == g_graph_refs[r].ws) {
+                if (--d->sk[i].graphs == 0 && d->sk[i].orphan) {
+                    int cur = 0;
+                    if (hipGetDevice(&cur) == hipSuccess && hipSetDevice(g_graph_refs[r].dev) == hipSuccess) {
+                        hipDeviceSynchronize();
+                        sk_drop(d, i);
+                        hipSetDevice(cur);
+                    }
+                }
+                break;
+            }
+        g_graph_refs[r] = g_graph_refs[--g_ngraph_refs];
+        break;
     }
     pthread_mutex_unlock(&g_lock);
 }
@@ -441,6 +515,11 @@ int sgpu_graph_end(void *stream, void **graph) {
     hipError_t e = hipGraphInstantiate(&ge, g, NULL, NULL, 0);
     hipGraphDestroy(g);
     if (e != hipSuccess) return (int)e;
+    int rc = sk_graph_recorded((void *)ge, stream);
+    if (rc) {
+        hipGraphExecDestroy(ge);
+        return rc;
+    }
     *graph = (void *)ge;
     return SGPU_OK;
 }
@@ -451,8 +530,9 @@ int sgpu_graph_launch(void *graph, void *stream) {
 }
 int sgpu_graph_destroy(void *graph) {
     if (!graph) return SGPU_OK;
-    HIPCHK(hipGraphExecDestroy((hipGraphExec_t)graph));
-    return SGPU_OK;
+    hipError_t e = hipGraphExecDestroy((hipGraphExec_t)graph);
+    sk_graph_destroyed(graph);
+    return e == hipSuccess ? SGPU_OK : (int)e;
 }
 
 int sgpu_event_create(void **event) {
@@ -963,6 +1043,20 @@ static int nt_splits(int T, int N, int K, int cus) {
     return S < 1 ? 1 : (int)S;
 }
 
+/* The batched GEMV's kernel choice: up to 8 tokens on aligned rows of at most 4096 take the
+ * register-resident team GEMV; otherwise the matrix-core tile, with K split over S blocks when
+ * there are too few 32x32 tiles to fill the CUs (whole aligned quads and at least 4 tokens).
+ * *S is the split the tile path would take given a workspace (1: none). */
+static int gemv_multi_x8(const float *W, const float *X, int K, int T) {
+    const int aligned = K > 0 && K % 4 == 0 && !(((uintptr_t)W | (uintptr_t)X) & 15);
+    return aligned && T <= 8 && K <= 4096;
+}
+static int gemv_multi_splits(const devstate *d, const float *W, const float *X, int K, int N, int T) {
+    const int aligned = K > 0 && K % 4 == 0 && !(((uintptr_t)W | (uintptr_t)X) & 15);
+    if (gemv_multi_x8(W, X, K, T) || !aligned || T < 4) return 1;
+    return nt_splits(T, N, K, d->cus);
+}
+
 int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, float *Y, int K, int N, int T,
                              float *ws, unsigned *cnt, void *stream) {
     if (K < 0 || N < 0 || T < 0) return SGPU_ERR_INVALID_ARG;
@@ -971,11 +1065,10 @@ int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, 
     int rc;
     devstate *d = cur(&rc);
     if (!d) return rc;
-    const int aligned = K > 0 && K % 4 == 0 && !(((uintptr_t)W | (uintptr_t)X) & 15);
     /* Up to 8 tokens on aligned rows of at most 4096: the register-resident team GEMV with
      * eight input vectors (a wave per row up to K = 1024, a block per row beyond; one block
      * per 4 or 1 rows, capped at the 2 or 3 blocks per CU their registers allow). */
-    if (aligned && T <= 8 && K <= 4096) {
+    if (gemv_multi_x8(W, X, K, T)) {
         const int wide = K > 1024;
         const unsigned teams = wide ? 1u : 4u, cap = (unsigned)d->cus * (wide ? 3u : 2u);
         unsigned g[3] = {umin(cdiv(N, (int)teams), cap), 1, 1}, b[3] = {256, 1, 1};
@@ -984,8 +1077,7 @@ int sgpu_internal_gemv_multi(const float *W, const float *X, const float *bias, 
     }
     /* Too few 32x32 tiles to fill the CUs: split each tile's K over blocks (matrix-core path
      * conditions: whole aligned quads and at least 4 tokens). */
-    const int mfma_ok = aligned && T >= 4;
-    const int S = (mfma_ok && ws && cnt) ? nt_splits(T, N, K, d->cus) : 1;
+    const int S = (ws && cnt) ? gemv_multi_splits(d, W, X, K, N, T) : 1;
     if (S > 1) {
         const long long tiles = (long long)cdiv(T, 32) * cdiv(N, 32);
         unsigned g[3] = {(unsigned)(tiles * S), 1, 1}, b[3] = {256, 1, 1};
@@ -1004,7 +1096,10 @@ int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y,
     devstate *d = (N > 0 && T > 0 && K >= 0) ? cur(&rc) : NULL;
     float *ws = NULL;
     unsigned *cnt = NULL;
-    if (d && sk_workspace(d, stream, &ws, &cnt) != SGPU_OK) ws = NULL, cnt = NULL;   /* unsplit kernels */
+    /* a workspace only for a launch that splits (unsplit kernels without one) */
+    if (d && (!Y || K == 0 || (W && X)) && gemv_multi_splits(d, W, X, K, N, T) > 1 &&
+        sk_workspace(d, stream, &ws, &cnt) != SGPU_OK)
+        ws = NULL, cnt = NULL;
     return sgpu_internal_gemv_multi(W, X, bias, Y, K, N, T, ws, cnt, stream);
 }
 

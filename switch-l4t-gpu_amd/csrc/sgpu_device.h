@@ -10,6 +10,16 @@
 
 typedef float sgpu_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sgpu_u32x4 __attribute__((ext_vector_type(4)));
+// The same four floats at any float alignment (4 bytes): a load through this type tells the
+// compiler no more than the address guarantees; gfx950 still loads it with one dwordx4.
+typedef float sgpu_f32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// Four consecutive floats from p: 16-byte aligned (ALIGNED) or any float alignment.
+template <bool ALIGNED>
+__device__ __forceinline__ sgpu_f32x4 sgpu_ld4(const float* p) {
+    if constexpr (ALIGNED) return *reinterpret_cast<const sgpu_f32x4*>(p);
+    else return *reinterpret_cast<const sgpu_f32x4_a4*>(p);
+}
 
 // 128-bit streaming loads (global_load_dwordx4 with the nontemporal hint): data read once.
 __device__ __forceinline__ sgpu_f32x4 sgpu_ldnt(const sgpu_f32x4* p) { return __builtin_nontemporal_load(p); }

@@ -695,9 +695,9 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
         const float* a = pa + k0;
         const float* b = pb + k0 * N;
 #pragma unroll
-        for (int q = 0; q < 8; q++) ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a + q * astep);
+        for (int q = 0; q < 8; q++) ra[q] = sgpu_ld4<!EDGE>(a + q * astep);
 #pragma unroll
-        for (int q = 0; q < 8; q++) rb[q] = *reinterpret_cast<const sgpu_f32x4*>(b + q * bstep);
+        for (int q = 0; q < 8; q++) rb[q] = sgpu_ld4<!EDGE>(b + q * bstep);
         if constexpr (TH) tb = pt[k0 * N];
     };
     // the partial slice 0: k >= K % 32 reads as zero, nothing past A or B is touched
@@ -707,7 +707,7 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
         for (int q = 0; q < 8; q++) {
             const float* a = pa + q * astep;
             if (kq + 3 < kpart) {
-                ra[q] = *reinterpret_cast<const sgpu_f32x4*>(a);
+                ra[q] = sgpu_ld4<!EDGE>(a);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++) ra[q][e] = kq + e < kpart ? a[e] : 0.0f;
@@ -715,7 +715,7 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
         }
 #pragma unroll
         for (int q = 0; q < 8; q++)
-            rb[q] = (lane >> 4) + 4 * q < kpart ? *reinterpret_cast<const sgpu_f32x4*>(pb + (size_t)(4 * q) * N)
+            rb[q] = (lane >> 4) + 4 * q < kpart ? sgpu_ld4<!EDGE>(pb + (size_t)(4 * q) * N)
                                                 : sgpu_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (TH) tb = l32 < kpart ? pt[0] : 0.0f;
     };

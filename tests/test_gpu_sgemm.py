@@ -5,6 +5,7 @@ Bars: reference-generator inputs (srand(42), gpu_workload.c:81-82) at every size
 max|C - C_ref| / max|C_ref| <= 1e-4 and the reference verdict (5% + 1e-3) clean; small-integer
 inputs (|a|, |b| <= 2, every partial sum an exact fp32 integer) bit-exact against float64
 BLAS at every shape, including ragged edges and the full 4096^3."""
+import ctypes as ct
 import functools
 import json
 import os
@@ -292,6 +293,92 @@ def test_splitk_recording_needs_a_workspace(gpu):
         st.synchronize()
         assert np.array_equal(dC.to_host(), want) and np.array_equal(dD.to_host(), want)
     g2.close()
+    st.close()
+
+
+def test_splitk_graph_outlives_its_stream(gpu):
+    """A graph recorded on a stream holds that stream's split-K workspace: after the stream is
+    destroyed the graph still replays exactly (here on another stream, between that stream's
+    own split launches); destroying the graph then frees it, and streams made afterwards
+    (whose handles may repeat the destroyed one's) get workspaces of their own."""
+    M, N, K = 768, 768, 2048                                # sgpu_sgemm_opt splits this one 5 ways
+    rng = np.random.default_rng(29)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC, dD = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N)), \
+        gpu.DeviceArray((M, N))
+    st = gpu.Stream()
+    gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, st.h)   # the stream's workspace
+    st.synchronize()
+    with gpu.Graph(st) as g:
+        gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, st.h)
+    st.close()                                              # the graph keeps its workspace
+    st2 = gpu.Stream()
+    for _ in range(3):
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_graph_launch", g.h, st2.h)
+        st2.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+        dD.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dD.ptr, M, N, K, st2.h)   # st2's own workspace
+        st2.synchronize()
+        assert np.array_equal(dD.to_host(), want)
+    g.close()
+    for _ in range(2):
+        st3 = gpu.Stream()
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_splitk", dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, st3.h)
+        st3.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+        st3.close()
+    st2.close()
+
+
+def test_per_thread_stream_has_no_workspace(gpu):
+    """hipStreamPerThread names a different stream in every host thread, so it gets no split-K
+    workspace: sgpu_sgemm_splitk refuses it, sgpu_sgemm_opt runs its unsplit member there."""
+    per_thread = ct.c_void_p(2)                             # hipStreamPerThread
+    M, N, K = 768, 768, 2048
+    rng = np.random.default_rng(31)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    assert gpu.lib().sgpu_sgemm_splitk(dA.ptr, dB.ptr, dC.ptr, M, N, K, 4, per_thread) == gpu.SGPU_ERR_NO_WORKSPACE
+    dC.fill_bytes(0xFF)
+    gpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, per_thread)
+    gpu.call("sgpu_stream_synchronize", per_thread)
+    assert np.array_equal(dC.to_host(), want)
+
+
+def test_gemv_multi_workspace_only_when_split(gpu, og):
+    """sgpu_gemv_multi makes a stream's split-K workspace (32 MB) only for a launch that splits:
+    the few-token register GEMV allocates nothing on a new stream; a matrix-core launch with
+    too few 32x32 tiles to fill the CUs makes it, once."""
+    hip = ct.CDLL("libamdhip64.so")
+
+    def free_bytes():
+        f, t = ct.c_size_t(), ct.c_size_t()
+        gpu.synchronize()
+        assert hip.hipMemGetInfo(ct.byref(f), ct.byref(t)) == 0
+        return f.value
+
+    K, N = 768, 64
+    W, s = gpu.gen_normal(N * K, 41, 0.0, 0.02)
+    X, _ = gpu.gen_normal(32 * K, s, 0.0, 1.0)
+    dW, dX, dY = gpu.DeviceArray.from_host(W), gpu.DeviceArray.from_host(X), gpu.DeviceArray((32, N))
+    st = gpu.Stream()
+    for T, grows in ((2, False), (8, False), (32, True), (32, False)):
+        before = free_bytes()
+        dY.fill_bytes(0xFF)
+        gpu.call("sgpu_gemv_multi", dW.ptr, dX.ptr, None, dY.ptr, K, N, T, st.h)
+        st.synchronize()
+        used = before - free_bytes()
+        say(f"gemv_multi T={T}: {used} bytes of device memory")
+        assert (used >= 32 << 20) if grows else (used < 8 << 20), (T, used)
+        ref = og.gemv_multi(W, X[:T * K], None, K, N, T).reshape(T, N)
+        assert np.all(np.abs(dY.to_host()[:T] - ref) <= 1e-4 * np.abs(ref) + 1e-4)
     st.close()
 
 
