@@ -309,6 +309,18 @@ int sgpu_gpt2_forward(sgpu_gpt2 *engine, int token, int pos, int want_logits, fl
  * trace of the reference's self-test (gpt2_engine.c:478-494).  Logits to logits_host when it
  * is not NULL.  Synchronous; the KV cache gains `pos` as with sgpu_gpt2_forward. */
 int sgpu_gpt2_forward_trace(sgpu_gpt2 *engine, int token, int pos, float *logits_host, float *trace_host, int fused);
+/* Receives one stage vector of a traced forward (sgpu_gpt2_forward_stages,
+ * sgpu_qwen_forward_stages): the stage's name and a host copy of its n floats, valid during the
+ * call. */
+typedef void (*sgpu_stage_fn)(void *ctx, const char *stage, const float *v, int n);
+/* The GPU stage tracer of the reference's --debug (gprvec, gpt2_engine.c:173-251,356-362):
+ * sgpu_gpt2_forward on the REFERENCE launch sequence (fused: the bias epilogue GEMVs), whatever
+ * the engine's path, which at layer 0 waits for each stage and hands its vector to fn: "ln1",
+ * "qkv" (3C), "scores" and "probs" ((pos+1) x NH), "attnout", "ao", "res1", "ln2", "fc" (FC),
+ * "gelu" (FC), "proj", "res2" (C unless noted).  Logits to logits_host when it is not NULL.
+ * Synchronous; the KV cache gains `pos`. */
+int sgpu_gpt2_forward_stages(sgpu_gpt2 *engine, int token, int pos, float *logits_host, int fused, sgpu_stage_fn fn,
+                             void *ctx);
 /* gpu_prefill (gpt2_engine.c:269-326): all T prompt positions through the layers with the
  * weight-stationary gemv_multi; fills cache positions 0..T-1; logits of the last row. */
 int sgpu_gpt2_prefill(sgpu_gpt2 *engine, const int *ids, int T, float *logits_host);
@@ -362,6 +374,13 @@ int sgpu_qwen_forward(sgpu_qwen *engine, int token, int pos, int want_logits, fl
  * qwen_engine.c:355; gpt2_engine.c:478-494).  Logits to logits_host when it is not NULL.
  * Synchronous.  The KV cache gains `pos` as with sgpu_qwen_forward. */
 int sgpu_qwen_forward_trace(sgpu_qwen *engine, int token, int pos, float *logits_host, float *trace_host);
+/* The GPU stage tracer of the reference's --debug (gprvec, qwen_engine.c:196-202,216-260):
+ * sgpu_qwen_forward on the REFERENCE launch sequence, whatever the engine's path, which at
+ * layer 0 waits for each stage and hands its vector to fn, as a host copy valid during the
+ * call: "ln1" (C), "qkv" (after RoPE, QKVD), "scores" and "probs" ((pos+1) x NH), "attnout"
+ * (C), "res1" (C), "gate" (the gate half, FC), "swiglu" (FC), "res2" (C).  Logits to
+ * logits_host when it is not NULL.  Synchronous; the KV cache gains `pos`. */
+int sgpu_qwen_forward_stages(sgpu_qwen *engine, int token, int pos, float *logits_host, sgpu_stage_fn fn, void *ctx);
 /* Execution paths of sgpu_qwen_forward / sgpu_qwen_generate.  All compute the same
  * function (checked against the CPU golden); they differ in launch structure:
  *  REFERENCE -- the reference's per-layer sequence above, 14 launches + 2 copies per layer

@@ -290,7 +290,7 @@ static int forward_fused(sgpu_gpt2 *e, int token, int pos, int want_logits, floa
 /* gpu_forward (gpt2_engine.c:174-264), `fused` = its --fused variant.  With trace_host, the
  * residual after each layer is copied there (NL x C floats, gpu_forward's trace argument). */
 static int forward_reference(sgpu_gpt2 *e, int token, int pos, int want_logits, float *logits_host, int fused,
-                             float *trace_host) {
+                             float *trace_host, sgpu_stage_sink *sink) {
     const sgpu_gpt2_cfg *c = &e->cfg;
     const int C = c->C, FC = c->FC, T = pos + 1;
     const float eps = c->eps, scale = 0.125f;   /* 1/sqrt(64), gpt2_engine.c:75 */
@@ -298,24 +298,38 @@ static int forward_reference(sgpu_gpt2 *e, int token, int pos, int want_logits, 
     const float *W = e->w;
     int rc;
 #define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+#define STAGE(tag, dev, n) do { if (sink && l == 0) TRY(sgpu_internal_stage_out(s, sink, tag, dev, n)); } while (0)
+    const int NH = c->NH;
     /* x = wte[token] + wpe[pos] (the reference adds on the host, gpt2_engine.c:176-179) */
     TRY(sgpu_add2(W + e->L.wte + (size_t)token * C, W + e->L.wpe + (size_t)pos * C, e->x, C, s));
     for (int l = 0; l < c->NL; l++) {
         const float *b = W + e->L.l_base + (size_t)l * e->L.lstride;
         TRY(sgpu_layernorm(e->x, b + e->L.ln1w, b + e->L.ln1b, e->ln1, C, eps, 1, s));
+        STAGE("ln1", e->ln1, C);
         TRY(proj(b + e->L.qkvw, e->ln1, b + e->L.qkvb, e->qkv, C, 3 * C, fused, s));
+        STAGE("qkv", e->qkv, 3 * C);
         TRY(sgpu_memcpy_dtod_async(e->kc[l] + (size_t)pos * C, e->qkv + C, (size_t)C * 4, s));
         TRY(sgpu_memcpy_dtod_async(e->vc[l] + (size_t)pos * C, e->qkv + 2 * C, (size_t)C * 4, s));
         TRY(sgpu_gpt2_attn_scores(e->qkv, e->kc[l], e->scores, T, scale, s));
         TRY(sgpu_gpt2_attn_softmax(e->scores, e->probs, T, s));
         TRY(sgpu_gpt2_attn_mix(e->probs, e->vc[l], e->att, T, s));
+        STAGE("scores", e->scores, T * NH);
+        STAGE("probs", e->probs, T * NH);
+        STAGE("attnout", e->att, C);
         TRY(proj(b + e->L.aow, e->att, b + e->L.aob, e->y, C, C, fused, s));
+        STAGE("ao", e->y, C);
         TRY(sgpu_add2(e->x, e->y, e->x, C, s));
+        STAGE("res1", e->x, C);
         TRY(sgpu_layernorm(e->x, b + e->L.ln2w, b + e->L.ln2b, e->ln2, C, eps, 1, s));
+        STAGE("ln2", e->ln2, C);
         TRY(proj(b + e->L.fcw, e->ln2, b + e->L.fcb, e->fc, C, FC, fused, s));
+        STAGE("fc", e->fc, FC);
         TRY(sgpu_gelu(e->fc, e->fc, FC, s));
+        STAGE("gelu", e->fc, FC);
         TRY(proj(b + e->L.projw, e->fc, b + e->L.projb, e->y, FC, C, fused, s));
+        STAGE("proj", e->y, C);
         TRY(sgpu_add2(e->x, e->y, e->x, C, s));
+        STAGE("res2", e->x, C);
         if (trace_host) {
             hipError_t he = hipMemcpyAsync(trace_host + (size_t)l * C, e->x, (size_t)C * 4, hipMemcpyDeviceToHost,
                                            e->stream);
@@ -323,6 +337,7 @@ static int forward_reference(sgpu_gpt2 *e, int token, int pos, int want_logits, 
         }
     }
     if (trace_host) TRY(sgpu_stream_synchronize(s));
+#undef STAGE
 #undef TRY
     return want_logits ? logits_out(e, e->x, logits_host) : SGPU_OK;
 }
@@ -331,13 +346,27 @@ int sgpu_gpt2_forward(sgpu_gpt2 *e, int token, int pos, int want_logits, float *
     if (!e) return SGPU_ERR_INVALID_ARG;
     if (token < 0 || token >= e->cfg.V || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
     if (e->path != SGPU_GPT2_PATH_REFERENCE) return forward_fused(e, token, pos, want_logits, logits_host);
-    return forward_reference(e, token, pos, want_logits, logits_host, fused, NULL);
+    return forward_reference(e, token, pos, want_logits, logits_host, fused, NULL, NULL);
 }
 
 int sgpu_gpt2_forward_trace(sgpu_gpt2 *e, int token, int pos, float *logits_host, float *trace_host, int fused) {
     if (!e || !trace_host) return SGPU_ERR_INVALID_ARG;
     if (token < 0 || token >= e->cfg.V || pos < 0 || pos >= e->cfg.CTX) return SGPU_ERR_INVALID_ARG;
-    return forward_reference(e, token, pos, logits_host != NULL, logits_host, fused, trace_host);
+    return forward_reference(e, token, pos, logits_host != NULL, logits_host, fused, trace_host, NULL);
+}
+
+int sgpu_gpt2_forward_stages(sgpu_gpt2 *e, int token, int pos, float *logits_host, int fused, sgpu_stage_fn fn,
+                             void *ctx) {
+    if (!e || !fn) return SGPU_ERR_INVALID_ARG;
+    const sgpu_gpt2_cfg *c = &e->cfg;
+    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
+    int cap = 3 * c->C > c->FC ? 3 * c->C : c->FC;
+    if ((pos + 1) * c->NH > cap) cap = (pos + 1) * c->NH;
+    sgpu_stage_sink sink = {fn, ctx, malloc(sizeof(float) * (size_t)cap), cap};
+    if (!sink.host) return SGPU_ERR_HOST_ALLOC;
+    int rc = forward_reference(e, token, pos, logits_host != NULL, logits_host, fused, NULL, &sink);
+    free(sink.host);
+    return rc;
 }
 
 /* gpu_prefill's layer loop: all T prompt rows through each layer, cache positions 0..T-1

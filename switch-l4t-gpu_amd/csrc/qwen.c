@@ -253,7 +253,7 @@ const float *sgpu_qwen_device_logits(const sgpu_qwen *e) { return e ? e->d_logit
  * trace_host, the residual after each layer is copied there (NL x C floats, the layer
  * trace of cpu_forward, qwen_engine.c:355). */
 static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, float *logits_host,
-                             float *trace_host) {
+                             float *trace_host, sgpu_stage_sink *sink) {
     const sgpu_qwen_cfg *c = &e->cfg;
     const int C = c->C, NH = c->NH, NKV = c->NKV, HD = c->HD, FC = c->FC;
     const int KVD = e->L.kvd, QKVD = e->L.qkvd, Tp = pos + 1;
@@ -261,25 +261,35 @@ static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, 
     void *s = (void *)e->stream;
     int rc;
 #define TRY(x) do { if ((rc = (x))) return rc; } while (0)
+#define STAGE(tag, dev, n) do { if (sink && l == 0) TRY(sgpu_internal_stage_out(s, sink, tag, dev, n)); } while (0)
     TRY(sgpu_internal_embed_h(e->d_emb, token, e->d_x, C, s));
     for (int l = 0; l < c->NL; l++) {
         TRY(sgpu_rmsnorm(e->d_x, e->d_ln1w[l], e->d_ln1, C, eps, 1, s));
+        STAGE("ln1", e->d_ln1, C);
         TRY(sgpu_gemv_h(e->d_qkvw[l], e->d_ln1, e->d_qkvb[l], e->d_qkv, C, QKVD, s));
         TRY(sgpu_rope(e->d_qkv, e->d_cos, e->d_sin, 1, NH, HD, pos, s));
         TRY(sgpu_rope(e->d_qkv + (size_t)NH * HD, e->d_cos, e->d_sin, 1, NKV, HD, pos, s));
+        STAGE("qkv", e->d_qkv, QKVD);
         TRY(sgpu_memcpy_dtod_async(e->d_kc[l] + (size_t)pos * KVD, e->d_qkv + (size_t)NH * HD, (size_t)KVD * 4, s));
         TRY(sgpu_memcpy_dtod_async(e->d_vc[l] + (size_t)pos * KVD, e->d_qkv + (size_t)NH * HD + KVD,
                                    (size_t)KVD * 4, s));
         TRY(sgpu_attn_scores_gqa(e->d_qkv, e->d_kc[l], e->d_scores, Tp, scale, NH, KVD, HD, s));
         TRY(sgpu_attn_softmax(e->d_scores, e->d_probs, Tp, NH, s));
         TRY(sgpu_attn_mix_gqa(e->d_probs, e->d_vc[l], e->d_att, Tp, NH, KVD, HD, s));
+        STAGE("scores", e->d_scores, Tp * NH);
+        STAGE("probs", e->d_probs, Tp * NH);
+        STAGE("attnout", e->d_att, C);
         TRY(sgpu_gemv_h(e->d_ow[l], e->d_att, NULL, e->d_y, C, C, s));
         TRY(sgpu_add2(e->d_x, e->d_y, e->d_x, C, s));
+        STAGE("res1", e->d_x, C);
         TRY(sgpu_rmsnorm(e->d_x, e->d_ln2w[l], e->d_ln2, C, eps, 1, s));
         TRY(sgpu_gemv_h(e->d_gateupw[l], e->d_ln2, NULL, e->d_gate, C, 2 * FC, s));
+        STAGE("gate", e->d_gate, FC);
         TRY(sgpu_swiglu(e->d_gate, e->d_gate + FC, e->d_down, FC, s));
+        STAGE("swiglu", e->d_down, FC);
         TRY(sgpu_gemv_h(e->d_downw[l], e->d_down, NULL, e->d_y, FC, C, s));
         TRY(sgpu_add2(e->d_x, e->d_y, e->d_x, C, s));
+        STAGE("res2", e->d_x, C);
         if (trace_host) {
             hipError_t he = hipMemcpyAsync(trace_host + (size_t)l * C, e->d_x, (size_t)C * 4, hipMemcpyDeviceToHost,
                                            e->stream);
@@ -295,6 +305,7 @@ static int forward_reference(sgpu_qwen *e, int token, int pos, int want_logits, 
         if (he != hipSuccess) return (int)he;
         TRY(sgpu_stream_synchronize(s));
     }
+#undef STAGE
 #undef TRY
     return SGPU_OK;
 }
@@ -392,7 +403,7 @@ int sgpu_qwen_forward(sgpu_qwen *e, int token, int pos, int want_logits, float *
     if (!e) return SGPU_ERR_INVALID_ARG;
     const sgpu_qwen_cfg *c = &e->cfg;
     if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
-    if (e->path == SGPU_QWEN_PATH_REFERENCE) return forward_reference(e, token, pos, want_logits, logits_host, NULL);
+    if (e->path == SGPU_QWEN_PATH_REFERENCE) return forward_reference(e, token, pos, want_logits, logits_host, NULL, NULL);
     int rc = sgpu_internal_dec_embed(e->d_emb, token, pos, e->d_x, c->C, e->d_step, (void *)e->stream);
     if (!rc) rc = run_layers(e);
     if (rc || !want_logits) return rc;
@@ -404,7 +415,21 @@ int sgpu_qwen_forward_trace(sgpu_qwen *e, int token, int pos, float *logits_host
     if (!e || !trace_host) return SGPU_ERR_INVALID_ARG;
     const sgpu_qwen_cfg *c = &e->cfg;
     if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
-    return forward_reference(e, token, pos, logits_host != NULL, logits_host, trace_host);
+    return forward_reference(e, token, pos, logits_host != NULL, logits_host, trace_host, NULL);
+}
+
+int sgpu_qwen_forward_stages(sgpu_qwen *e, int token, int pos, float *logits_host, sgpu_stage_fn fn, void *ctx) {
+    if (!e || !fn) return SGPU_ERR_INVALID_ARG;
+    const sgpu_qwen_cfg *c = &e->cfg;
+    if (token < 0 || token >= c->V || pos < 0 || pos >= c->CTX) return SGPU_ERR_INVALID_ARG;
+    int cap = e->L.qkvd > c->FC ? e->L.qkvd : c->FC;
+    if (c->C > cap) cap = c->C;
+    if ((pos + 1) * c->NH > cap) cap = (pos + 1) * c->NH;
+    sgpu_stage_sink sink = {fn, ctx, malloc(sizeof(float) * (size_t)cap), cap};
+    if (!sink.host) return SGPU_ERR_HOST_ALLOC;
+    int rc = forward_reference(e, token, pos, logits_host != NULL, logits_host, NULL, &sink);
+    free(sink.host);
+    return rc;
 }
 
 /* ---- per-phase timing: each decode phase's 24 layer launches recorded in one graph ---- */
@@ -558,14 +583,14 @@ int sgpu_qwen_generate(sgpu_qwen *e, const int *prompt, int T, int n_gen, int *o
     if (e->path == SGPU_QWEN_PATH_REFERENCE) {       /* host-driven loop, the reference's own */
         float *logits = malloc(sizeof(float) * (size_t)c->V);
         if (!logits) return SGPU_ERR_HOST_ALLOC;
-        for (int p = 0; p < T && !(rc = forward_reference(e, prompt[p], p, p == T - 1, logits, NULL)); p++) {
+        for (int p = 0; p < T && !(rc = forward_reference(e, prompt[p], p, p == T - 1, logits, NULL, NULL)); p++) {
         }
         for (int g = 0; !rc && g <= n_gen; g++) {
             int b = 0;
             for (int i = 1; i < c->V; i++)
                 if (logits[i] > logits[b]) b = i;
             out_tokens[g] = b;
-            if (g < n_gen) rc = forward_reference(e, b, T + g, 1, logits, NULL);
+            if (g < n_gen) rc = forward_reference(e, b, T + g, 1, logits, NULL, NULL);
         }
         free(logits);
         return rc;

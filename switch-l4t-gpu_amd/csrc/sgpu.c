@@ -1103,6 +1103,15 @@ int sgpu_gemv_multi(const float *W, const float *X, const float *bias, float *Y,
     return sgpu_internal_gemv_multi(W, X, bias, Y, K, N, T, ws, cnt, stream);
 }
 
+int sgpu_internal_stage_out(void *stream, sgpu_stage_sink *k, const char *tag, const float *dev, int n) {
+    if (n > k->cap) n = k->cap;
+    hipError_t he = hipMemcpyAsync(k->host, dev, (size_t)n * 4, hipMemcpyDeviceToHost, (hipStream_t)stream);
+    if (he == hipSuccess) he = hipStreamSynchronize((hipStream_t)stream);
+    if (he != hipSuccess) return (int)he;
+    k->fn(k->ctx, tag, k->host, n);
+    return SGPU_OK;
+}
+
 /* ---- Qwen support kernels ---- */
 static int elem_grid(int n) { return (int)umin(cdiv(n > 0 ? n : 1, 256), 65535u); }
 

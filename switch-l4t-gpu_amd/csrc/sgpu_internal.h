@@ -3,6 +3,8 @@
 #define SGPU_INTERNAL_H
 #include <stdint.h>
 
+#include "switch_gpu.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -84,6 +86,16 @@ SGPU_HIDDEN int sgpu_internal_g2_embed(const float *wte, const float *wpe, int t
 #define SGPU_SCRATCH_TILES 16384u
 SGPU_HIDDEN int sgpu_internal_scratch_setup(int dev);
 SGPU_HIDDEN int sgpu_internal_scratch(int dev, float **ws, unsigned **cnt);
+
+/* A stage vector of a traced forward: the stream's work so far waited for, the n floats at
+ * dev (at most cap) copied to host and handed to fn. */
+typedef struct {
+    sgpu_stage_fn fn;
+    void *ctx;
+    float *host;                  /* scratch of cap floats */
+    int cap;
+} sgpu_stage_sink;
+SGPU_HIDDEN int sgpu_internal_stage_out(void *stream, sgpu_stage_sink *k, const char *tag, const float *dev, int n);
 
 #ifdef __cplusplus
 }

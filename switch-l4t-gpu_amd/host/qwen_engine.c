@@ -28,9 +28,11 @@
  *                    layer at position 0, then the logits at position S-1 (max |gpu-cpu|, top-5
  *                    ids, argmax MATCH/MISMATCH, SELFTEST: PASS/FAIL; qwen_engine.c:494-521).
  *                    The cache keeps those positions; priming continues from S.
- *   --debug          with --selftest: the CPU forward's layer-0 stage vectors at position 0
- *                    (first four values and sum, qwen_engine.c:297-346) and both layer traces
- *                    written to trace_g.bin / trace_c.bin (NL x C floats each).
+ *   --debug          with --selftest: the layer-0 stage vectors at position 0 (first four
+ *                    values and sum), first the GPU's (g.* lines, the reference launch sequence
+ *                    waited for after each stage, qwen_engine.c:196-202,216-260) then the CPU
+ *                    forward's (c.* lines, qwen_engine.c:297-346), and both layer traces written
+ *                    to trace_g.bin / trace_c.bin (NL x C floats each).
  * Decoding is greedy (argmax, first max wins, qwen_engine.c:360-364) and stops at EOT or
  * <|im_end|> as the reference does (:539); --greedy is accepted for command-line
  * compatibility.
@@ -108,6 +110,14 @@ static void prvec(const char *tag, const float *v, int n) {
     float s = 0.0f;
     for (int i = 0; i < n; i++) s += v[i];
     printf("    c.%-8s first4=%.3f %.3f %.3f %.3f sum=%.3f\n", tag, v[0], v[1], v[2], v[3], s);
+}
+
+/* A GPU stage vector (sgpu_qwen_forward_stages) in the same format, tagged g. */
+static void gprvec(void *ctx, const char *tag, const float *v, int n) {
+    (void)ctx;
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += v[i];
+    printf("    g.%-8s first4=%.3f %.3f %.3f %.3f sum=%.3f\n", tag, v[0], v[1], v[2], v[3], s);
 }
 
 static int cpu_init(cpu_model *m, const sgpu_qwen_cfg *c, const void *blob, int debug) {
@@ -240,6 +250,7 @@ static int selftest(sgpu_qwen *eng, const sgpu_qwen_cfg *cfg, const void *blob, 
     cpu_model m;
     if (!cpu_init(&m, cfg, blob, debug)) { fprintf(stderr, "selftest: out of host memory\n"); exit(2); }
     float *tr_g = malloc((size_t)NL * C * 4), *tr_c = malloc((size_t)NL * C * 4);
+    if (debug) CHK(sgpu_qwen_forward_stages(eng, ids[0], 0, NULL, gprvec, NULL));
     double t0 = now_s();
     CHK(sgpu_qwen_forward_trace(eng, ids[0], 0, logits, tr_g));
     for (int p = 1; p < S; p++) CHK(sgpu_qwen_forward(eng, ids[p], p, p == S - 1, logits));

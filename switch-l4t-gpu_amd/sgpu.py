@@ -115,6 +115,7 @@ _SIGS = {
     "sgpu_gpt2_destroy": (None, [_P]),
     "sgpu_gpt2_forward": (_I, [_P, _I, _I, _I, _P, _I]),
     "sgpu_gpt2_forward_trace": (_I, [_P, _I, _I, _P, _P, _I]),
+    "sgpu_gpt2_forward_stages": (_I, [_P, _I, _I, _P, _I, _P, _P]),
     "sgpu_gpt2_prefill": (_I, [_P, _P, _I, _P]),
     "sgpu_gpt2_set_path": (_I, [_P, _I]),
     "sgpu_gpt2_generate": (_I, [_P, _P, _I, _I, _P]),
@@ -129,6 +130,7 @@ _SIGS = {
     "sgpu_qwen_set_path": (_I, [_P, _I]),
     "sgpu_qwen_generate": (_I, [_P, _P, _I, _I, _P]),
     "sgpu_qwen_phase_times": (_I, [_P, _I, _I, _P]),
+    "sgpu_qwen_forward_stages": (_I, [_P, _I, _I, _P, _P, _P]),
     "sgpu_qwen_prefill": (_I, [_P, _P, _I, _P]),
     "sgpu_gen_sgemm_inputs": (None, [_P, _P, _S, ct.c_uint]),
     "sgpu_frand": (_F, [ct.POINTER(ct.c_uint64)]),
@@ -380,6 +382,20 @@ def qwen_random_blob(cfg: QwenCfg, seed: int, std: float = 0.02) -> np.ndarray:
     return blob
 
 
+STAGE_FN = ct.CFUNCTYPE(None, ct.c_void_p, ct.c_char_p, ct.POINTER(ct.c_float), ct.c_int)
+
+
+def _stage_collector():
+    """A stage callback for the *_forward_stages entry points and the ordered list it fills
+    with (stage, copy of the vector)."""
+    got = []
+
+    def fn(ctx, tag, v, n):
+        got.append((tag.decode(), np.ctypeslib.as_array(v, (n,)).copy()))
+
+    return STAGE_FN(fn), got
+
+
 QWEN_PATH_REFERENCE, QWEN_PATH_FUSED, QWEN_PATH_GRAPH = 0, 1, 2
 QWEN_PHASES = ("qkv", "attention", "o", "gate_up", "down", "lm_head", "argmax_embed")
 
@@ -415,6 +431,13 @@ class QwenEngine:
         trace = np.empty((self.cfg.NL, self.cfg.C), np.float32)
         call("sgpu_qwen_forward_trace", self.h, token, pos, self.logits.ctypes.data, trace.ctypes.data)
         return self.logits, trace
+
+    def forward_stages(self, token: int, pos: int):
+        """The reference launch sequence with its layer-0 stage vectors (sgpu_qwen_forward_stages):
+        (logits, [(stage, vector), ...] in launch order)."""
+        cb, got = _stage_collector()
+        call("sgpu_qwen_forward_stages", self.h, token, pos, self.logits.ctypes.data, ct.cast(cb, ct.c_void_p), None)
+        return self.logits, got
 
     def phase_times(self, pos: int, reps: int = 20) -> dict:
         """In-graph us per launch of each decode phase at position pos (sgpu_qwen_phase_times)."""
@@ -491,6 +514,14 @@ class Gpt2Engine:
         trace = np.empty((self.cfg.NL, self.cfg.C), np.float32)
         call("sgpu_gpt2_forward_trace", self.h, token, pos, self.logits.ctypes.data, trace.ctypes.data, int(fused))
         return self.logits, trace
+
+    def forward_stages(self, token: int, pos: int, fused: bool = False):
+        """The reference launch sequence with its layer-0 stage vectors (sgpu_gpt2_forward_stages):
+        (logits, [(stage, vector), ...] in launch order)."""
+        cb, got = _stage_collector()
+        call("sgpu_gpt2_forward_stages", self.h, token, pos, self.logits.ctypes.data, int(fused),
+             ct.cast(cb, ct.c_void_p), None)
+        return self.logits, got
 
     def prefill(self, ids):
         a = np.ascontiguousarray(ids, np.int32)

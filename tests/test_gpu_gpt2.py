@@ -364,6 +364,29 @@ def check_selftest_output(text, NL):
     assert text.count("top-5 ids:") == 2
 
 
+STAGE_RE = r"^    ([gc])\.(\w+)\s+first4=(\S+) (\S+) (\S+) (\S+) sum=(\S+)$"
+
+
+def stage_lines(text):
+    """{("g"|"c", stage): (first4, sum)} from the --debug stage lines (format of the
+    reference's prvec / gprvec)."""
+    import re
+
+    out = {}
+    for m in re.finditer(STAGE_RE, text, re.M):
+        v = [float(x) for x in m.groups()[2:]]
+        out[(m.group(1), m.group(2))] = (v[:4], v[4])
+    return out
+
+
+def check_stages_agree(st, tags, tol):
+    """The GPU's and the CPU's printed values of each stage both print (3 decimals)."""
+    for tag in tags:
+        (g4, gs), (c4, cs) = st[("g", tag)], st[("c", tag)]
+        for a, b in zip(g4 + [gs], c4 + [cs]):
+            assert abs(a - b) <= tol * max(abs(b), 1.0) + 2e-3, (tag, g4, gs, c4, cs)
+
+
 @pytest.mark.parametrize("extra", [[], ["--fused"], ["--batch-prefill"], ["--path", "graph"]])
 def test_cli_selftest(gpu, extra, tmp_path):
     """bin/gpt2_engine --selftest 4 on the full random-init model (fp32 weights): the per-layer
@@ -379,8 +402,33 @@ def test_cli_selftest(gpu, extra, tmp_path):
     assert "ENGINE_DONE" in out.stdout
 
 
+def test_forward_stages(gpu):
+    """sgpu_gpt2_forward_stages: the reference's twelve layer-0 stages in launch order (plain
+    and fused GEMVs), the last one bit-identical to the layer trace of the same launch
+    sequence; at position 0 every head's softmax is exactly 1 and its output is its v."""
+    cfg = gpu.gpt2_cfg()
+    w = gpu.gpt2_random_weights(cfg, 21, 0.03)
+    eng = gpu.Gpt2Engine(cfg, w, 0)
+    for fused in (False, True):
+        logits_s, st = eng.forward_stages(7, 0, fused)
+        logits_s = logits_s.copy()
+        names = [t for t, _ in st]
+        assert names == ["ln1", "qkv", "scores", "probs", "attnout", "ao", "res1", "ln2", "fc", "gelu", "proj",
+                         "res2"]
+        v = dict(st)
+        C, NH, FC = cfg.C, cfg.NH, cfg.FC
+        assert [len(v[k]) for k in names] == [C, 3 * C, NH, NH, C, C, C, C, FC, FC, C, C]
+        assert np.array_equal(v["probs"], np.ones(NH, np.float32))
+        assert np.array_equal(v["attnout"], v["qkv"][2 * C:])
+        logits_t, trace = eng.forward_trace(7, 0, fused)
+        assert np.array_equal(v["res2"], trace[0]) and np.array_equal(logits_s, logits_t)
+    eng.close()
+
+
 def test_cli_selftest_debug(gpu, tmp_path):
-    """--debug adds the CPU forward's layer-0 stage lines and writes both layer traces."""
+    """--debug adds the layer-0 stage lines, the GPU's (g.*, the reference launch sequence)
+    before the CPU forward's (c.*), agreeing where both print a stage, and writes both layer
+    traces."""
     exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "gpt2_engine")
     say("gpt2_engine --selftest 2 --debug")
     out = subprocess.run([exe, "--random", "4", "--selftest", "2", "--debug", "--gen", "1"],
@@ -389,6 +437,10 @@ def test_cli_selftest_debug(gpu, tmp_path):
     check_selftest_output(out.stdout, 12)
     for tag in ("embed", "ln1", "qkv", "ao", "res1", "ln2", "fc", "gelu", "proj", "res2"):
         assert f"c.{tag}" in out.stdout
+    st = stage_lines(out.stdout)
+    assert all(("g", t) in st for t in ("ln1", "qkv", "scores", "probs", "attnout", "ao", "res1", "ln2", "fc", "gelu", "proj", "res2")), sorted(st)
+    assert out.stdout.index("g.ln1") < out.stdout.index("c.ln1")
+    check_stages_agree(st, ("ln1", "qkv", "ao", "res1", "ln2", "fc", "gelu", "proj", "res2"), 1e-4)
     g = np.fromfile(tmp_path / "trace_g.bin", np.float32)
     c = np.fromfile(tmp_path / "trace_c.bin", np.float32)
     assert g.size == c.size == 12 * 768

@@ -564,6 +564,29 @@ def check_selftest_output(text, NL):
     assert text.count("top-5 ids:") == 2
 
 
+STAGE_RE = r"^    ([gc])\.(\w+)\s+first4=(\S+) (\S+) (\S+) (\S+) sum=(\S+)$"
+
+
+def stage_lines(text):
+    """{("g"|"c", stage): (first4, sum)} from the --debug stage lines (format of the
+    reference's prvec / gprvec)."""
+    import re
+
+    out = {}
+    for m in re.finditer(STAGE_RE, text, re.M):
+        v = [float(x) for x in m.groups()[2:]]
+        out[(m.group(1), m.group(2))] = (v[:4], v[4])
+    return out
+
+
+def check_stages_agree(st, tags, tol):
+    """The GPU's and the CPU's printed values of each stage both print (3 decimals)."""
+    for tag in tags:
+        (g4, gs), (c4, cs) = st[("g", tag)], st[("c", tag)]
+        for a, b in zip(g4 + [gs], c4 + [cs]):
+            assert abs(a - b) <= tol * max(abs(b), 1.0) + 2e-3, (tag, g4, gs, c4, cs)
+
+
 @pytest.mark.parametrize("path", ["reference", "graph"])
 def test_cli_selftest(gpu, path, tmp_path):
     """bin/qwen_engine --selftest 3 on the full random-init model: the per-layer residual trace at
@@ -580,7 +603,9 @@ def test_cli_selftest(gpu, path, tmp_path):
 
 
 def test_cli_selftest_debug(gpu, tmp_path):
-    """--debug adds the CPU forward's layer-0 stage lines and writes both layer traces."""
+    """--debug adds the layer-0 stage lines, the GPU's (g.*, the reference launch sequence)
+    before the CPU forward's (c.*), agreeing where both print a stage, and writes both layer
+    traces."""
     exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "qwen_engine")
     say("qwen_engine --selftest 1 --debug")
     out = subprocess.run([exe, "--random", "7", "--selftest", "1", "--debug", "--gen", "1"],
@@ -589,10 +614,37 @@ def test_cli_selftest_debug(gpu, tmp_path):
     check_selftest_output(out.stdout, 24)
     for tag in ("embed", "ln1", "qkv", "ao", "res1"):
         assert f"c.{tag}" in out.stdout
+    st = stage_lines(out.stdout)
+    assert all(("g", t) in st for t in ("ln1", "qkv", "scores", "probs", "attnout", "res1", "gate", "swiglu", "res2")), sorted(st)
+    assert out.stdout.index("g.ln1") < out.stdout.index("c.ln1")
+    check_stages_agree(st, ("ln1", "qkv", "res1"), 1e-3)
     g = np.fromfile(tmp_path / "trace_g.bin", np.float32)
     c = np.fromfile(tmp_path / "trace_c.bin", np.float32)
     assert g.size == c.size == 24 * 896
     assert np.abs(g - c).max() <= 1e-3 * max(np.abs(g).max(), 1.0)
+
+
+def test_forward_stages(gpu):
+    """sgpu_qwen_forward_stages: the reference's nine layer-0 stages in launch order, the last
+    one bit-identical to the layer trace of the same launch sequence; at position 0 every
+    head's softmax is exactly 1 and its output is its KV group's v."""
+    c = gpu.qwen_cfg(**SMALL)
+    blob = gpu.qwen_random_blob(c, seed=11, std=0.15)
+    eng = gpu.QwenEngine(c, blob, PATHS["graph"])
+    logits_s, st = eng.forward_stages(5, 0)
+    logits_s = logits_s.copy()
+    names = [t for t, _ in st]
+    assert names == ["ln1", "qkv", "scores", "probs", "attnout", "res1", "gate", "swiglu", "res2"]
+    v = dict(st)
+    C, NH, NKV, HD, FC = SMALL["C"], SMALL["NH"], SMALL["NKV"], SMALL["HD"], SMALL["FC"]
+    assert [len(v[k]) for k in names] == [C, C + 2 * NKV * HD, NH, NH, C, C, FC, FC, C]
+    assert np.array_equal(v["probs"], np.ones(NH, np.float32))
+    vpart = v["qkv"][C + NKV * HD:]
+    want = np.concatenate([vpart[(h // (NH // NKV)) * HD:(h // (NH // NKV) + 1) * HD] for h in range(NH)])
+    assert np.array_equal(v["attnout"], want)
+    logits_t, trace = eng.forward_trace(5, 0)
+    assert np.array_equal(v["res2"], trace[0]) and np.array_equal(logits_s, logits_t)
+    eng.close()
 
 
 def test_forward_trace_is_the_reference_forward(gpu):
