@@ -659,12 +659,12 @@ __device__ __forceinline__ void gemv_byname(const typename WT::elem* __restrict_
     constexpr int VEC = WT::VEC;
     // a grid of one thread per row or fewer ((N+255)/256 blocks, gemv_test.c:108) keeps a wave
     // per row: with so few waves the team kernel's one row block in flight per block is slower
-    const bool team = blockDim.x == 256 && blockDim.y == 1 && blockDim.z == 1 && gridDim.y == 1 &&
-                      gridDim.z == 1 && K > 0 && K % VEC == 0 && ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0 &&
-                      (long long)gridDim.x * 8 >= N;
+    const bool team = sgpu_bdim_x() == 256 && sgpu_bdim_y() == 1 && sgpu_bdim_z() == 1 && sgpu_gdim(1) == 1 &&
+                      sgpu_gdim(2) == 1 && K > 0 && K % VEC == 0 && ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0 &&
+                      (long long)sgpu_gdim(0) * 8 >= N;
     const int nseg = K / VEC;
     if constexpr (VEC == 8) {
-        const int nb = min((int)gridDim.x, 4608);
+        const int nb = min(sgpu_gdim(0), 4608);
         __shared__ __attribute__((aligned(16))) float xs[64 * 10 * VEC];
         if (team && nseg <= 16 * 7)
             gemv_team_xlds<WT, 16, 7, 1, XT>(W, x, bias, y, K, N, nb, xs);
@@ -673,7 +673,7 @@ __device__ __forceinline__ void gemv_byname(const typename WT::elem* __restrict_
         else
             gemv_generic<WT, XT>(W, x, bias, y, K, N);
     } else {
-        const int nb = min((int)gridDim.x, 2048);
+        const int nb = min(sgpu_gdim(0), 2048);
         if (team && nseg <= 16 * 12)
             gemv_team<WT, 16, 12, 1>(W, K, N, x_source(x), MapRows{}, EpiStore{bias, y}, nb);
         else if (team && nseg <= 64 * 16)
@@ -1007,8 +1007,8 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
 // with so few 32x32 tiles the weight stream runs on too few CUs).  The host launcher
 // applies the same rule (sgpu.c) to size the grid.
 __device__ __forceinline__ bool gemm_nt_ok(const float* W, const float* X, int K, int T) {
-    return K > 0 && (K % 4 == 0) && ((((uintptr_t)W) | ((uintptr_t)X)) & 15) == 0 && blockDim.x == 256 &&
-           blockDim.y == 1 && blockDim.z == 1 && T >= 4 && !(T <= 8 && K > 1024);
+    return K > 0 && (K % 4 == 0) && ((((uintptr_t)W) | ((uintptr_t)X)) & 15) == 0 && sgpu_bdim_x() == 256 &&
+           sgpu_bdim_y() == 1 && sgpu_bdim_z() == 1 && T >= 4 && !(T <= 8 && K > 1024);
 }
 
 // Weight-stationary batched GEMV (gemv_multi role): Y[t*N+n] = W[n,:].X[t,:] + bias?[n].

@@ -97,10 +97,27 @@ __device__ __forceinline__ float sgpu_wave_max(float v) {
 // acknowledgment of stores that bypass the L2 write-back: the release measured +55% on split
 // SGEMM (1023x1025x997 at 4 splits 31.7 -> 48.9 us, 1024x768x1024 21.8 -> 33.1) while the
 // acquire costs ~0.5 us per launch.
-// Linear thread index / block size for kernels that accept 1-D or 2-D blocks.
-__device__ __forceinline__ int sgpu_tid() { return threadIdx.x + threadIdx.y * blockDim.x; }
-__device__ __forceinline__ int sgpu_nthreads() { return blockDim.x * blockDim.y * blockDim.z; }
-__device__ __forceinline__ int sgpu_bid() {
-    return blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+// Launch geometry from the hidden kernel arguments (code object v5), read as aligned dwords:
+// bytes 0, 4, 8 hold the grid's block counts x, y, z; bytes 12..17 the 16-bit group sizes x,
+// y, z.  HIP's blockDim also allows for a partial last block and picks, per block, between
+// the group size and the remainder field.  That can compile to 16-bit vector loads (a
+// dword-unaligned field cannot take a scalar load) that run one after another, through the
+// vector cache a streaming kernel keeps full, before the block's first useful load.  HIP
+// launches whole blocks only, so the group sizes are the block sizes.  Aligned dwords come
+// from the preloaded argument SGPRs or one scalar load.
+__device__ __forceinline__ uint32_t sgpu_hidden_u32(int dword) {
+    typedef const uint32_t __attribute__((address_space(4))) * cu32;
+    return ((cu32)__builtin_amdgcn_implicitarg_ptr())[dword];
 }
-__device__ __forceinline__ int sgpu_nblocks() { return gridDim.x * gridDim.y * gridDim.z; }
+__device__ __forceinline__ int sgpu_gdim(int d) { return (int)sgpu_hidden_u32(d); }
+__device__ __forceinline__ int sgpu_bdim_x() { return (int)(sgpu_hidden_u32(3) & 0xffffu); }
+__device__ __forceinline__ int sgpu_bdim_y() { return (int)(sgpu_hidden_u32(3) >> 16); }
+__device__ __forceinline__ int sgpu_bdim_z() { return (int)(sgpu_hidden_u32(4) & 0xffffu); }
+
+// Linear thread index / block size for kernels that accept 1-D or 2-D blocks.
+__device__ __forceinline__ int sgpu_tid() { return threadIdx.x + threadIdx.y * sgpu_bdim_x(); }
+__device__ __forceinline__ int sgpu_nthreads() { return sgpu_bdim_x() * sgpu_bdim_y() * sgpu_bdim_z(); }
+__device__ __forceinline__ int sgpu_bid() {
+    return blockIdx.x + sgpu_gdim(0) * (blockIdx.y + sgpu_gdim(1) * blockIdx.z);
+}
+__device__ __forceinline__ int sgpu_nblocks() { return sgpu_gdim(0) * sgpu_gdim(1) * sgpu_gdim(2); }
