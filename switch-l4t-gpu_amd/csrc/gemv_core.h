@@ -659,7 +659,7 @@ __device__ __forceinline__ void gemv_byname(const typename WT::elem* __restrict_
     constexpr int VEC = WT::VEC;
     // a grid of one thread per row or fewer ((N+255)/256 blocks, gemv_test.c:108) keeps a wave
     // per row: with so few waves the team kernel's one row block in flight per block is slower
-    const bool team = sgpu_bdim_x() == 256 && sgpu_bdim_y() == 1 && sgpu_bdim_z() == 1 && sgpu_gdim(1) == 1 &&
+    const bool team = sgpu_bdim_x() == 256 && sgpu_block256() && sgpu_gdim(1) == 1 &&
                       sgpu_gdim(2) == 1 && K > 0 && K % VEC == 0 && ((((uintptr_t)W) | ((uintptr_t)x)) & 15) == 0 &&
                       (long long)sgpu_gdim(0) * 8 >= N;
     const int nseg = K / VEC;
@@ -1008,7 +1008,7 @@ __device__ __forceinline__ void gemm_nt_mfma(const typename WT::elem* __restrict
 // applies the same rule (sgpu.c) to size the grid.
 __device__ __forceinline__ bool gemm_nt_ok(const float* W, const float* X, int K, int T) {
     return K > 0 && (K % 4 == 0) && ((((uintptr_t)W) | ((uintptr_t)X)) & 15) == 0 && sgpu_bdim_x() == 256 &&
-           sgpu_bdim_y() == 1 && sgpu_bdim_z() == 1 && T >= 4 && !(T <= 8 && K > 1024);
+           sgpu_block256() && T >= 4 && !(T <= 8 && K > 1024);
 }
 
 // Weight-stationary batched GEMV (gemv_multi role): Y[t*N+n] = W[n,:].X[t,:] + bias?[n].

@@ -97,26 +97,38 @@ __device__ __forceinline__ float sgpu_wave_max(float v) {
 // acknowledgment of stores that bypass the L2 write-back: the release measured +55% on split
 // SGEMM (1023x1025x997 at 4 splits 31.7 -> 48.9 us, 1024x768x1024 21.8 -> 33.1) while the
 // acquire costs ~0.5 us per launch.
-// Launch geometry from the hidden kernel arguments (code object v5), read as aligned dwords:
-// bytes 0, 4, 8 hold the grid's block counts x, y, z; bytes 12..17 the 16-bit group sizes x,
-// y, z.  HIP's blockDim also allows for a partial last block and picks, per block, between
-// the group size and the remainder field.  That can compile to 16-bit vector loads (a
-// dword-unaligned field cannot take a scalar load) that run one after another, through the
-// vector cache a streaming kernel keeps full, before the block's first useful load.  HIP
-// launches whole blocks only, so the group sizes are the block sizes.  Aligned dwords come
-// from the preloaded argument SGPRs or one scalar load.
+// Launch geometry from the hidden kernel arguments (code object v5): the grid's block counts
+// x, y, z (32-bit, bytes 0, 4, 8) and the 16-bit group sizes x, y, z (bytes 12, 14, 16).
+// HIP's blockDim also allows for a partial last block and picks, per block, between the group
+// size and the remainder field.  That pick can compile to 16-bit vector loads that run one
+// after another, through the vector cache a streaming kernel keeps full, before the block's
+// first useful load.  HIP launches whole blocks only, so the group sizes are the block sizes.
+// Read as below, the block counts and the x, y group sizes come from the argument SGPRs
+// preloaded at wave launch (for kernels whose own arguments take at most 40 bytes), and the z
+// group size from one scalar load.  Each block count passes through an empty asm so that
+// neighbouring fields are not merged into one wider load, which the preload would not serve.
 __device__ __forceinline__ uint32_t sgpu_hidden_u32(int dword) {
     typedef const uint32_t __attribute__((address_space(4))) * cu32;
     return ((cu32)__builtin_amdgcn_implicitarg_ptr())[dword];
 }
-__device__ __forceinline__ int sgpu_gdim(int d) { return (int)sgpu_hidden_u32(d); }
-__device__ __forceinline__ int sgpu_bdim_x() { return (int)(sgpu_hidden_u32(3) & 0xffffu); }
-__device__ __forceinline__ int sgpu_bdim_y() { return (int)(sgpu_hidden_u32(3) >> 16); }
+__device__ __forceinline__ int sgpu_gdim(int d) {
+    uint32_t v = sgpu_hidden_u32(d);
+    __asm__("" : "+s"(v));
+    return (int)v;
+}
+__device__ __forceinline__ int sgpu_bdim_x() { return __builtin_amdgcn_workgroup_size_x(); }
+__device__ __forceinline__ int sgpu_bdim_y() { return __builtin_amdgcn_workgroup_size_y(); }
 __device__ __forceinline__ int sgpu_bdim_z() { return (int)(sgpu_hidden_u32(4) & 0xffffu); }
 
-// Linear thread index / block size for kernels that accept 1-D or 2-D blocks.
-__device__ __forceinline__ int sgpu_tid() { return threadIdx.x + threadIdx.y * sgpu_bdim_x(); }
+// Linear thread index / block size for any block shape.
+__device__ __forceinline__ int sgpu_tid() {
+    return threadIdx.x + sgpu_bdim_x() * (threadIdx.y + sgpu_bdim_y() * threadIdx.z);
+}
 __device__ __forceinline__ int sgpu_nthreads() { return sgpu_bdim_x() * sgpu_bdim_y() * sgpu_bdim_z(); }
+// A block of exactly 256 threads, for kernels declared __launch_bounds__(256) only: HIP refuses
+// a launch whose block holds more threads than the kernel's bound, so x*y == 256 leaves z == 1
+// and the check needs no load of the z size.
+__device__ __forceinline__ bool sgpu_block256() { return sgpu_bdim_x() * sgpu_bdim_y() == 256; }
 __device__ __forceinline__ int sgpu_bid() {
     return blockIdx.x + sgpu_gdim(0) * (blockIdx.y + sgpu_gdim(1) * blockIdx.z);
 }

@@ -354,9 +354,11 @@ __device__ __forceinline__ void sgemm_mfma(const float* __restrict__ A, const fl
     static_assert(STORE_AT >= 0 && LAYOUT >= 2 && LAYOUT <= 4, "store point and layout");
     __shared__ __attribute__((aligned(16))) SgemmLdsM<BM, BN, BK, WGM, WGN> LM;
 
-    // The tile split assumes exactly NT threads per block; any other block size is rejected
-    // by every thread alike (no barrier is reached, C is left untouched).
-    if (sgpu_nthreads() != T::NT) return;
+    // The tile split assumes exactly NT = 256 threads per block (the kernels' launch bound);
+    // any other block size is rejected by every thread alike (no barrier is reached, C is
+    // left untouched).
+    static_assert(T::NT == 256, "four waves per block");
+    if (!sgpu_block256()) return;
     const SgemmThread<BM, BN, BK, WGM, WGN> th;
 
     const int ntm = (M + BM - 1) / BM, ntn = (N + BN - 1) / BN, ntiles = ntm * ntn;
@@ -618,7 +620,7 @@ template <int TS, int U>
 __device__ __forceinline__ void sgemm_small(const float* __restrict__ A, const float* __restrict__ B,
                                             float* __restrict__ C, int M, int N, int K) {
     __shared__ __attribute__((aligned(16))) float red[4][TS * TS / 64][64];
-    if (sgpu_nthreads() != 256) return;
+    if (!sgpu_block256()) return;
     if (K % 4 == 0 && ((uintptr_t)A & 15) == 0) sgemm_small_tiles<TS, U, true>(A, B, C, M, N, K, red);
     else sgemm_small_tiles<TS, U, false>(A, B, C, M, N, K, red);
 }
@@ -950,7 +952,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sgemm_kwave(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     __shared__ __attribute__((aligned(16))) KwaveLds L[4];
     static_assert(sizeof(L) >= 4 * 4 * 4 * 64 * sizeof(sgpu_f32x4), "the partial tiles fit the staging");
-    if (sgpu_nthreads() != 256 || M <= 0 || N <= 0 || K <= 0 || M % 64 || N % 64 || K % KW_BK ||
+    if (!sgpu_block256() || M <= 0 || N <= 0 || K <= 0 || M % 64 || N % 64 || K % KW_BK ||
         ((((uintptr_t)A) | ((uintptr_t)B)) & 15))
         return;
     const int ntm = M / 64, ntn = N / 64, ntiles = ntm * ntn;
@@ -976,7 +978,7 @@ sgemm_kwave_edge(const float* __restrict__ A, const float* __restrict__ B, float
     __shared__ __attribute__((aligned(16))) KwaveLdsEdge L[4];
     static_assert(sizeof(L) >= 4 * 4 * 4 * 64 * sizeof(sgpu_f32x4) + 8 * 64 * sizeof(float),
                   "the partial tiles and the extra column's partials fit the staging");
-    if (sgpu_nthreads() != 256 || M < 64 || N < 64 || K < 1) return;
+    if (!sgpu_block256() || M < 64 || N < 64 || K < 1) return;
     const bool th = N % 64 == 1;
     const int ntm = (M + 63) / 64, ntn = th ? N / 64 : (N + 63) / 64, ntiles = ntm * ntn;
     const int nb = sgpu_nblocks();

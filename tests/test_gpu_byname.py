@@ -67,6 +67,13 @@ class Hip:
         gx, gy = grid
         assert self.lib.hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, None, params, None) == 0
 
+    def launch_shape(self, f, grid, block, args):
+        """hipModuleLaunchKernel with any block shape; returns HIP's status."""
+        vals = [ct.c_void_p(a.v) if isinstance(a, Ptr) else (ct.c_void_p(None) if a is None else ct.c_int(a))
+                for a in args]
+        params = (ct.c_void_p * len(vals))(*[ct.addressof(v) for v in vals])
+        return self.lib.hipModuleLaunchKernel(f, grid, 1, 1, *block, 0, None, params, None)
+
 
 class Ptr:
     def __init__(self, v):
@@ -260,3 +267,46 @@ def test_kwave_members_by_name_any_grid(gpu, hip, sym, M, N, K, grid):
     hip.launch(hip.function("switch_gpu", sym), (grid, 1), [Ptr(dA.ptr), Ptr(dB.ptr), Ptr(dC.ptr), M, N, K])
     gpu.synchronize()
     assert np.array_equal(dC.to_host(), want)
+
+
+def test_block_beyond_launch_bound_refused(gpu, hip):
+    """The kernels' block-size checks (sgpu_block256) read no z size: a block of x*y == 256
+    threads has z == 1 because HIP refuses a launch whose block holds more threads than the
+    kernel's __launch_bounds__(256).  This pins that refusal, for a by-name GEMV symbol and an
+    SGEMM member: the launch returns an error and nothing is written."""
+    N, K = 1024, 896
+    dW, dx, dy = gpu.DeviceArray(N * K // 2), gpu.DeviceArray(K), gpu.DeviceArray(N)
+    dy.fill_bytes(0xFF)
+    f = hip.function("qwen_kernels", "gemv_h")
+    say("gemv_h launched with a 256x1x2 block")
+    assert hip.launch_shape(f, N // 8, (256, 1, 2), [Ptr(dW.ptr), Ptr(dx.ptr), None, Ptr(dy.ptr), K, N]) != 0
+    n = 256
+    dA, dB, dC = gpu.DeviceArray((n, n)), gpu.DeviceArray((n, n)), gpu.DeviceArray((n, n))
+    dC.fill_bytes(0xFF)
+    g = hip.function("switch_gpu", "sgemm_tiled")
+    say("sgemm_tiled launched with a 128x2x2 block")
+    assert hip.launch_shape(g, 16, (128, 2, 2), [Ptr(dA.ptr), Ptr(dB.ptr), Ptr(dC.ptr), n, n, n]) != 0
+    gpu.synchronize()
+    assert np.all(np.isnan(dy.to_host())) and np.all(np.isnan(dC.to_host()))
+
+
+@pytest.mark.parametrize("block", [(64, 2, 2), (32, 2, 4), (128, 1, 2)])
+def test_three_d_blocks(gpu, hip, og, block):
+    """gemv_h launched by name with 3-D blocks of 256 threads (the wave-per-row path): every
+    row against the oracle.  Each z layer of a block has its own thread indices."""
+    N, K = 1000, 896
+    say(f"by name gemv_h {N}x{K} block {block}")
+    Wf, s = gpu.gen_normal(N * K, 11, 0.0, 0.02)
+    W = gpu.f32_to_f16(Wf)
+    x, s = gpu.gen_normal(K, s, 0.0, 1.0)
+    bias = np.linspace(-1, 1, N).astype(np.float32)
+    dW, dx, db = upload(gpu, W), upload(gpu, x), upload(gpu, bias)
+    dy = gpu.DeviceArray(N)
+    dy.fill_bytes(0xFF)
+    f = hip.function("qwen_kernels", "gemv_h")
+    assert hip.launch_shape(f, (N + 3) // 4, block, [Ptr(dW.ptr), Ptr(dx.ptr), Ptr(db.ptr), Ptr(dy.ptr), K, N]) == 0
+    gpu.synchronize()
+    y = dy.to_host()
+    ref = og.gemv_h_fbias(W, x, bias, K, N, NT)
+    m = np.abs(ref).max()
+    assert np.all(np.abs(y - ref) <= 1e-4 * np.abs(ref) + 1e-4 * m), np.abs(y - ref).max()
