@@ -441,8 +441,11 @@ __device__ __forceinline__ void gemv_team(const typename WT::elem* __restrict__ 
             epi.load(t, rows, pre);
         }
     };
-    const int nb = nblk > 0 ? nblk : (int)gridDim.x;
-    if ((int)blockIdx.x >= nb) return;                // block-uniform
+    // With nblk == 0 every block takes part, and the grid size is first needed as the stride to
+    // a block's second row block: the first fetch does not wait for it (a kernel whose own
+    // arguments fill the preloaded SGPRs reads it with a scalar load).
+    if (nblk > 0 && (int)blockIdx.x >= nblk) return;  // block-uniform
+    const int nb = nblk > 0 ? nblk : sgpu_gdim(0);
     int rb = blockIdx.x;
     sgpu_u32x4 gpre[S];
     pro.template preload<LPR, S, VEC>(gpre, has, sub);
