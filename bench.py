@@ -455,6 +455,19 @@ def decode_floor(quick=False):
     return {"decode_floor": floor, "decode_phase_us": phases}
 
 
+def sgemm_floor(quick=False):
+    """The matrix-core floor of short SGEMM launches next to the library's SGEMM: bin/sgemm_floor's
+    register-only MFMA probe (one wave per SIMD, 0..512 MFMAs per wave, graphs of 50 launches)
+    and sgpu_sgemm_opt at 1024^3, 768x1024x1024 and 1023x1025x997 timed the same way."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "sgemm_floor")
+    log(f"sgemm floor: {exe}")
+    r = subprocess.run([exe] + (["--quick"] if quick else []), capture_output=True, text=True, timeout=300)
+    sys.stderr.write(r.stderr)
+    if r.returncode != 0:
+        raise SystemExit(f"sgemm_floor exited {r.returncode}")
+    return {"sgemm_floor": json.loads(r.stdout)}
+
+
 def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -611,8 +624,14 @@ def main():
     ap.add_argument("--decode-floor", action="store_true",
                     help="measure the decode structure's launch and streaming floors and the per-phase "
                          "in-graph times (one JSON line)")
-    ap.add_argument("--quick", action="store_true", help="fewer repetitions in --decode-floor")
+    ap.add_argument("--sgemm-floor", action="store_true",
+                    help="measure the matrix-core floor of short SGEMM launches beside sgpu_sgemm_opt (one JSON line)")
+    ap.add_argument("--quick", action="store_true", help="fewer repetitions in --decode-floor / --sgemm-floor")
     args = ap.parse_args()
+    if args.sgemm_floor:
+        sgpu.init(0)
+        print(json.dumps(sgemm_floor(args.quick)), flush=True)
+        return
     if args.decode_floor:
         sgpu.init(0)
         print(json.dumps(decode_floor(args.quick)), flush=True)

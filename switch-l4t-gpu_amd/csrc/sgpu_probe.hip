@@ -1,7 +1,8 @@
-// sgpu_probe.hip -- measurement kernels behind bin/decode_floor: the costs that bound a decode
-// step built from dependent kernels (a kernel boundary, a weight stream after it, a device-side
-// hand-off between kernels in flight together).  Not on the hot path; nothing here computes a
-// result of the library.
+// sgpu_probe.hip -- measurement kernels behind bin/decode_floor and bin/sgemm_floor: the costs
+// that bound a decode step built from dependent kernels (a kernel boundary, a weight stream
+// after it, a device-side hand-off between kernels in flight together), and the matrix-core
+// floor of a short SGEMM launch.  Not on the hot path; nothing here computes a result of the
+// library.
 #include "sgpu_device.h"
 
 extern "C" {
@@ -84,6 +85,36 @@ __global__ void __launch_bounds__(256) sgpu_probe_link(const sgpu_u32x4* __restr
         __builtin_amdgcn_s_waitcnt(0);          // the write-through store is acknowledged
         __syncthreads();
         if (tid == 0) __hip_atomic_fetch_add(counter + (b & 7), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+
+// The matrix-core floor of an SGEMM launch: each wave of a 256-thread block issues iters x 16
+// v_mfma_f32_32x32x2f32 on four independent accumulators, operands in registers, then writes
+// its 16 sums, out[r * nthreads + gid] for gid < nout / 16 (gid the thread's grid index,
+// nthreads the grid's): every store instruction covers consecutive floats, as an SGEMM's C
+// write does, and that is the only memory it touches.  One block per CU (one wave per SIMD,
+// as sgemm_kwave) and iters 32 give each SIMD the MFMA count of a 1024^3 SGEMM, with none of
+// its loads and a C-sized store.
+typedef float sgpu_f32x16_p __attribute__((ext_vector_type(16)));
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgpu_probe_mfma(float* __restrict__ out, long long nout, int iters, float a0, float b0) {
+    sgpu_f32x16_p acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+    const float a = a0 + threadIdx.x * 1e-7f, b = b0 - threadIdx.x * 1e-7f;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i], 0, 0, 0);
+    }
+    const long long nthreads = (long long)sgpu_gdim(0) * 256, gid = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (gid < nout / 16) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) out[r * nthreads + gid] = ((acc[0][r] + acc[1][r]) + acc[2][r]) + acc[3][r];
     }
 }
 

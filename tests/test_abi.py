@@ -67,7 +67,7 @@ def test_code_objects_embedded(sg, module):
     if module in REFERENCE_KERNELS:
         assert REFERENCE_KERNELS[module] <= names, REFERENCE_KERNELS[module] - names
     elif module == "sgpu_probe":
-        assert {"sgpu_probe_stream", "sgpu_probe_link"} <= names
+        assert {"sgpu_probe_stream", "sgpu_probe_link", "sgpu_probe_mfma"} <= names
     else:
         assert {f"sgpu_gemv_h_l16_s7", "sgpu_gemv_f32_l64_s3", "sgpu_embed_h"} <= names
 
