@@ -278,6 +278,30 @@ def test_engine_small_generate(gpu, og, path):
     eng.close()
 
 
+@pytest.mark.parametrize("path", ["fused", "graph"])
+def test_engine_generate_across_chunk_boundary(gpu, og, path):
+    """Greedy decoding across position 256, where the attention's cache of one head stops fitting
+    one chunk and the chunk partials start going through the cross-block hand-off, inside one
+    recorded step on the graph path.  The ids equal the CPU golden's, twice in a row."""
+    cfg = dict(V=300, C=128, NL=2, NH=4, NKV=2, HD=32, FC=256, CTX=320)
+    blob = gpu.qwen_random_blob(gpu.qwen_cfg(**cfg), seed=45, std=0.15)
+    eng = gpu.QwenEngine(gpu.qwen_cfg(**cfg), blob, PATHS[path])
+    prompt = [int(v) for v in np.random.default_rng(8).integers(0, cfg["V"], 248)]
+    n = 16
+    say(f"qwen generate across position 256, {path} path")
+    got = eng.generate(prompt, n)
+    gold = og.QwenGolden(og.qwen_cfg(**cfg), blob, NT)
+    for p, t in enumerate(prompt):
+        ref = gold.forward(t, p, p == len(prompt) - 1)
+    want = [og.argmax(ref)]
+    for g in range(n):
+        ref = gold.forward(want[-1], len(prompt) + g)
+        want.append(og.argmax(ref))
+    assert got.tolist() == want
+    assert eng.generate(prompt, n).tolist() == want
+    eng.close()
+
+
 def test_phase_times_leave_the_engine_usable(gpu):
     """sgpu_qwen_phase_times replays every decode phase (the argmax advancing the device position
     on each launch) and restores the position: afterwards greedy decoding still equals a fresh
