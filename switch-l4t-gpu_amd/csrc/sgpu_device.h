@@ -97,6 +97,7 @@ __device__ __forceinline__ float sgpu_wave_max(float v) {
 // acknowledgment of stores that bypass the L2 write-back: the release measured +55% on split
 // SGEMM (1023x1025x997 at 4 splits 31.7 -> 48.9 us, 1024x768x1024 21.8 -> 33.1) while the
 // acquire costs ~0.5 us per launch.
+
 // Launch geometry from the hidden kernel arguments (code object v5): the grid's block counts
 // x, y, z (32-bit, bytes 0, 4, 8) and the 16-bit group sizes x, y, z (bytes 12, 14, 16).
 // HIP's blockDim also allows for a partial last block and picks, per block, between the group
