@@ -468,6 +468,40 @@ def sgemm_floor(quick=False):
     return {"sgemm_floor": json.loads(r.stdout)}
 
 
+def sgemm_floor_summary():
+    """The register-only MFMA kernel with a 1024^3 SGEMM's MFMA count per SIMD (512 per wave)
+    next to sgpu_sgemm_opt at 1024^3 and 1023x1025x997, timed the same way in one process
+    (bin/sgemm_floor --quick; the full ladder is --sgemm-floor)."""
+    try:
+        f = sgemm_floor(quick=True)["sgemm_floor"]
+    except (OSError, SystemExit, ValueError, subprocess.TimeoutExpired) as e:
+        return {"error": str(e)}
+    probe = next(r for r in f["mfma"] if r["mfma_per_wave"] == 512)
+    sg = {f"{r['M']}x{r['N']}x{r['K']}": r for r in f["sgemm"]}
+    k, rg = sg["1024x1024x1024"], sg["1023x1025x997"]
+    return {"probe_us": probe["us"],
+            "probe_frac_of_peak": round(2 * 1024 ** 3 / probe["us"] / 1e6 / PEAK_FP32_MATRIX_TFLOPS, 4),
+            "sgemm_1024_us": k["us"], "sgemm_1024_frac_of_probe": round(probe["us"] / k["us"], 4),
+            "ragged_us": rg["us"], "ragged_frac_of_probe": round(probe["us"] / rg["us"], 4),
+            "checks": f["checks"]}
+
+
+def gemv_byname_lm_head():
+    """gemv_h launched by name from the qwen_kernels code object at the reference engine's grid
+    ((N+7)/8 blocks of 256, qwen_engine.c:265) on the lm_head [151936 x 896], weight copies rotated
+    across 600 MB: bin/gemv_test checks it against its CPU golden, then times it."""
+    exe = os.path.join(ROOT, "switch-l4t-gpu_amd", "bin", "gemv_test")
+    co = os.path.join(ROOT, "switch-l4t-gpu_amd", "build", "qwen_kernels.co")
+    try:
+        r = subprocess.run([exe, co, "151936", "896", "--h", "--normal", "--rotate", "600", "--json"],
+                           capture_output=True, text=True, timeout=180)
+        k = json.loads(r.stdout.strip().splitlines()[-1])["kernels"][0]
+    except (OSError, ValueError, IndexError, KeyError, subprocess.TimeoutExpired) as e:
+        return {"error": str(e)}
+    return {"kernel": "gemv_h launched by name", "shape": [151936, 896], "grid": k["grid"], "us": k["us"],
+            "gbps": k["gbps"], "frac_hbm": round(k["gbps"] / PEAK_HBM_GBPS, 4), "verdict": k["verdict"]}
+
+
 def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -684,12 +718,16 @@ def main():
         log(f"cpu gemv_h lm_head: {cpu_gv['value']} GB/s on {cpu_gv['cores']} threads, "
             f"{cpu_gv['single_thread']['value']} GB/s on one")
     del gv["W"], gv["x"], gvh["W"], gvh["x"]
-    sweep = gshapes = None
+    sweep = gshapes = floor = byname = None
     if not args.no_sweep:
         sweep = bench_sgemm_sweep(cpu=not args.no_cpu)
         log("sgemm sweep (in-graph): " + ", ".join(f"{r['M']}x{r['N']}x{r['K']} {r['tflops']:.1f} TF" for r in sweep))
         gshapes = bench_gemv_shapes(cpu=not args.no_cpu)
         log("gemv shapes (in-graph): " + ", ".join(f"{r['name']} {r['us_in_graph']:.2f} us" for r in gshapes))
+        floor = sgemm_floor_summary()
+        log(f"sgemm floor: {floor}")
+        byname = gemv_byname_lm_head()
+        log(f"gemv_h by name at the reference grid: {byname}")
     dec = g2 = cpu_dec = None
     if not args.no_decode:
         dec = bench_decode(keep_blob=not args.no_cpu)
@@ -745,7 +783,9 @@ def main():
                                  "traffic": traffic.get("gemv_hh_lm_head")},
                     "weight_copies_rotated": gvh["copies"], "normwise_err": gvh["err"]},
         "sgemm_sweep": sweep,
+        "sgemm_floor": floor,
         "gemv_shapes": gshapes,
+        "gemv_byname": byname,
         "decode": None if dec is None else {
             "model": "Qwen2.5-0.5B architecture, random-init N(0,0.02) fp16 weights",
             "tok_s": round(dec["tok_s"], 2), "ms_per_token": round(dec["ms_per_tok"], 4),
