@@ -47,7 +47,7 @@ static const struct {
 /* Every kernel the launchers use: (module, symbol). */
 enum {
     K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_SMALL16, K_SGEMM_SMALL32,
-    K_SGEMM_KWAVE, K_SGEMM_KWAVE_EDGE, K_SGEMM_NAIVE, K_MEMBW,
+    K_SGEMM_KWAVE, K_SGEMM_KWAVE_EDGE, K_SGEMM_KWAVE_WIDE, K_SGEMM_KWAVE_EDGE_WIDE, K_SGEMM_NAIVE, K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK, K_GEMV_MULTI_X8_64,
     K_GEMV_MULTI_X8_256,
     K_GEMV_H, K_GEMV_HH, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
@@ -62,7 +62,7 @@ static const struct {
     {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
     {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_splitk"}, {MOD_SWITCH, "sgemm_small16"},
     {MOD_SWITCH, "sgemm_small32"}, {MOD_SWITCH, "sgemm_kwave"}, {MOD_SWITCH, "sgemm_kwave_edge"},
-    {MOD_SWITCH, "sgemm_naive"},
+    {MOD_SWITCH, "sgemm_kwave_wide"}, {MOD_SWITCH, "sgemm_kwave_edge_wide"}, {MOD_SWITCH, "sgemm_naive"},
     {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
@@ -584,7 +584,7 @@ static int sgemm_tile(const char *k, int *tn) {
     if (!strcmp(k, "sgemm_tiled4")) return *tn = 128, 128;
     if (!strcmp(k, "sgemm_opt")) return *tn = 256, 128;
     if (!strcmp(k, "sgemm_opt256")) return *tn = 256, 256;
-    if (!strcmp(k, "sgemm_kwave")) return *tn = 64, 64;
+    if (!strcmp(k, "sgemm_kwave") || !strcmp(k, "sgemm_kwave_wide")) return *tn = 64, 64;
     return *tn = 0, 0;
 }
 
@@ -593,7 +593,7 @@ static int geometry(const devstate *d, const char *kernel, int M, int N, int K, 
     const unsigned cus = d ? (unsigned)d->cus : 256u;
     g[0] = g[1] = g[2] = 1;
     b[0] = b[1] = b[2] = 1;
-    if (!strcmp(kernel, "sgemm_kwave_edge")) {
+    if (!strcmp(kernel, "sgemm_kwave_edge") || !strcmp(kernel, "sgemm_kwave_edge_wide")) {
         long long nt = kwave_edge_tiles(M, N);
         g[0] = (unsigned)(nt > 0 ? nt : 1);
         b[0] = 256;
@@ -681,11 +681,22 @@ int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, in
 /* sgemm_kwave's problems: M, N multiples of 64, K a multiple of 32 (the operands' 16-byte
  * alignment is the launcher's check). */
 static int kwave_shape(int M, int N, int K) { return M > 0 && N > 0 && K > 0 && M % 64 == 0 && N % 64 == 0 && K % 32 == 0; }
+/* The K-over-waves members load their operands through 32-bit buffer offsets while a 64-row A
+ * panel (64*K floats) and a 16-row B slice (16*N floats) stay under 2^31 bytes; larger operands
+ * go to the LDS-staged forms with 64-bit addresses (the *_wide kernels). */
+static int kwave_direct(int N, int K) { return (long long)K * 256 < (1LL << 31) && (long long)N * 64 < (1LL << 31); }
+static int kwave_launch(int edge, const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    if (kwave_direct(N, K))
+        return edge ? sgemm_common(K_SGEMM_KWAVE_EDGE, "sgemm_kwave_edge", A, B, C, M, N, K, stream)
+                    : sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
+    return edge ? sgemm_common(K_SGEMM_KWAVE_EDGE_WIDE, "sgemm_kwave_edge_wide", A, B, C, M, N, K, stream)
+                : sgemm_common(K_SGEMM_KWAVE_WIDE, "sgemm_kwave_wide", A, B, C, M, N, K, stream);
+}
 int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
     if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
     if (M == 0 || N == 0) return SGPU_OK;
     if (!kwave_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B) & 15)) return SGPU_ERR_INVALID_ARG;
-    return sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
+    return kwave_launch(0, A, B, C, M, N, K, stream);
 }
 /* sgemm_kwave_edge's problems: M, N at least 64 (a partial last row or column of tiles is the
  * 64 rows or columns ending at the last one), K at least 1, float-aligned operands. */
@@ -696,7 +707,7 @@ int sgpu_sgemm_kwave_edge(const float *A, const float *B, float *C, int M, int N
     if (M == 0 || N == 0) return SGPU_OK;
     if (!kwave_edge_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 3))
         return SGPU_ERR_INVALID_ARG;
-    return sgemm_common(K_SGEMM_KWAVE_EDGE, "sgemm_kwave_edge", A, B, C, M, N, K, stream);
+    return kwave_launch(1, A, B, C, M, N, K, stream);
 }
 /* The optimised entry picks the member with the least work on its busiest CU: tiles are one
  * block each, dealt over the CUs, so a launch lasts about ceil(tiles / CUs) tile times, and a
@@ -925,10 +936,9 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     unsigned *cnt;
     if (p == PLAN_SPLITK && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
         return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
-    if (p == PLAN_KWAVE && !(((uintptr_t)A | (uintptr_t)B) & 15))
-        return sgemm_common(K_SGEMM_KWAVE, "sgemm_kwave", A, B, C, M, N, K, stream);
+    if (p == PLAN_KWAVE && !(((uintptr_t)A | (uintptr_t)B) & 15)) return kwave_launch(0, A, B, C, M, N, K, stream);
     if ((p == PLAN_KWAVE || p == PLAN_KWAVE_EDGE) && !(((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 3))
-        return sgemm_common(K_SGEMM_KWAVE_EDGE, "sgemm_kwave_edge", A, B, C, M, N, K, stream);   /* rows of any float alignment */
+        return kwave_launch(1, A, B, C, M, N, K, stream);   /* rows of any float alignment */
     const int m = p >= 0 ? p : sgemm_pick(M, N, d->cus);
     return sgemm_common(g_sgemm_members[m].kid, g_sgemm_members[m].name, A, B, C, M, N, K, stream);
 }

@@ -9,7 +9,10 @@
 //   (A, B, C, M, N, K, int S, float* ws, unsigned* cnt), the 64x64 tile with K split S ways,
 // sgemm_small16 / sgemm_small32 (same arguments as the reference members), one 16x16 /
 // 32x32 tile per block with the operands read straight into MFMA registers, no LDS staging,
-// and sgemm_kwave (same arguments), the 64x64 tile with K split over the block's waves.
+// sgemm_kwave (same arguments), the 64x64 tile with K split over the block's waves and its
+// operands loaded straight into MFMA registers, its edge form sgemm_kwave_edge (any M, N >= 64,
+// any K), and their LDS-staged forms for operands past 2^31-byte windows, sgemm_kwave_wide and
+// sgemm_kwave_edge_wide.
 //
 // C = A*B, fp32, row-major (A: MxK stride K, B: KxN stride N, C: MxN stride N), overwrite
 // (alpha 1, beta 0).  Unlike the reference kernels, every shape is accepted: interior tiles
@@ -885,6 +888,250 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
     __syncthreads();                                              // the staging is reused by the next tile
 }
 
+// The same K-over-waves tile with each wave's MFMA operands loaded straight from memory into
+// registers in the 32x32x2 operand layout: no LDS staging, no wave syncs in the k loop
+// (sgemm_kwave, sgemm_kwave_edge).  A 64-row A panel and a 16-row B slice must each span less
+// than 2^31 bytes (kd_fits: every buffer offset is a non-negative int); sgemm_kwave_tile above,
+// with 64-bit addresses, takes larger operands (the *_wide kernels).
+//   Slices are KD_SD = 16 deep.  In a slice starting at k0, lane (l32, h) holds A rows
+//   mt+l32 and mt+32+l32 at k0+8h .. k0+8h+7 (two 16-byte loads per row) and, for MFMA step
+//   t = 0..7, row k0+8h+t of B at columns nt+2*l32 and nt+2*l32+1 (one 8-byte load): column
+//   block j of the tile is columns nt+2c+j (c = 0..31), so one load feeds both column blocks and
+//   a lane stores C two adjacent columns at a time.  MFMA step t sums k = k0+8h+t over the two
+//   lane halves for all four 32x32 blocks.
+//   Two register sets alternate between slices, and each register is reloaded with the slice
+//   after next right after the MFMAs that read it have issued, so a slice's loads are in flight
+//   for about two slices of MFMAs (the same structure with a whole set loaded one slice ahead
+//   stalls on the load latency).  Loads go through buffer resources rebased to each slice, with
+//   every offset in range, so nothing is masked in the loop.
+// EDGE: as sgemm_kwave_tile's EDGE (clamped edge tiles stored from their first new row and
+//   column, any K, rows of any float alignment), with the partial slice (k < K % 16) loaded
+//   element by element by the wave holding slice 0: A elements and B rows past K % 16 read as
+//   zero (clamped in-range addresses, then replaced), so a non-finite value never meets a
+//   padded zero.
+// TH (EDGE, N % 64 == 1, the last column of whole tiles): lane (l32, h) also loads column N-1
+//   of its eight B rows per slice and meets its A operands in 16 VALU FMAs per slice; the eight
+//   (wave, lane half) partials of each row are summed at the end.
+constexpr int KD_SD = 16;
+__host__ __device__ constexpr bool kd_fits(long long N, long long K) {
+    return K * 64 * 4 < 2147483648LL && N * KD_SD * 4 < 2147483648LL;
+}
+typedef float kd_f32x2 __attribute__((ext_vector_type(2)));
+typedef float kd_f32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+template <bool EDGE, bool TH>
+__device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, const float* __restrict__ B,
+                                                   float* __restrict__ C, int M, int N, int K, int m0, int n0,
+                                                   sgpu_f32x4* __restrict__ red) {
+    static_assert(EDGE || !TH, "the extra column is an edge case");
+    constexpr int NST = KD_SD / 2;                                // MFMA steps per slice
+    const int lane = sgpu_tid() & 63, wave = __builtin_amdgcn_readfirstlane(sgpu_tid() >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int nk = EDGE ? (K + KD_SD - 1) / KD_SD : K / KD_SD;
+    const int kpart = EDGE ? K % KD_SD : 0;                       // slice 0 is partial when != 0
+    const int kshift = kpart ? KD_SD - kpart : 0;
+    const int s0 = wave * nk / 4, s1 = (wave + 1) * nk / 4;      // this wave's slices
+    const int mt = EDGE ? min(m0, M - 64) : m0;
+    const int nt = EDGE ? min(n0, N - 64) : n0;
+    // byte offsets inside a slice's resources
+    const unsigned va0 = ((unsigned)l32 * K + NST * h) * 4u, va1 = ((unsigned)(32 + l32) * K + NST * h) * 4u;
+    const unsigned vb = ((unsigned)NST * h * N + 2 * l32) * 4u;
+    const unsigned vt = ((unsigned)NST * h * N + (N - 1 - nt)) * 4u;
+    sgpu_f32x4 a[2][2][2];                                        // [set][row block][quad]
+    kd_f32x2 b[2][NST];                                           // [set][step]: columns 2c, 2c+1
+    float tb[2][NST];                                             // TH: [set][step] column N-1
+    struct Rs {
+        __amdgpu_buffer_rsrc_t a, b;
+    };
+    // slice s >= 1 starts at k0 = 16 s - kshift; slice 0 (whole or partial) at k0 = 0.  With
+    // live false both ranges are empty: every load through them returns zero and touches nothing.
+    auto rsrc = [&](int s, bool live = true) __attribute__((always_inline)) -> Rs {
+        const long long k0 = s ? (long long)s * KD_SD - kshift : 0;
+        return {__builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)mt * K + k0), (short)0,
+                                                  live ? (int)((64LL * K - k0) * 4) : 0, 0x00020000),
+                __builtin_amdgcn_make_buffer_rsrc((void*)(B + (size_t)k0 * N + nt), (short)0,
+                                                  live ? (int)((long long)KD_SD * N * 4) : 0, 0x00020000)};
+    };
+    auto lda = [&](const Rs& r, unsigned off) __attribute__((always_inline)) {
+        return __builtin_bit_cast(sgpu_f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.a, (int)off, 0, 0));
+    };
+    auto ldb = [&](const Rs& r, int st) __attribute__((always_inline)) {
+        return __builtin_bit_cast(kd_f32x2, __builtin_amdgcn_raw_buffer_load_b64(r.b, (int)vb, st * N * 4, 0));
+    };
+    auto ldt = [&](const Rs& r, int st) __attribute__((always_inline)) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r.b, (int)vt, st * N * 4, 0));
+    };
+    // a whole slice s into set D (s >= 1 when K % 16 != 0; live false: zeros, nothing read)
+    auto load_whole = [&](int s, auto d_c, bool live = true) __attribute__((always_inline)) {
+        constexpr int D = decltype(d_c)::value;
+        const Rs r = rsrc(s, live);
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+            a[D][0][v] = lda(r, va0 + 16 * v);
+            a[D][1][v] = lda(r, va1 + 16 * v);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                b[D][4 * v + e] = ldb(r, 4 * v + e);
+                if constexpr (TH) tb[D][4 * v + e] = ldt(r, 4 * v + e);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // EDGE, K % 16 != 0: the partial slice 0 in registers of its own (pa, pb, pt).  An element at
+    // k >= K % 16 is given the offset 2^31, past the resource's range (under 2^31 bytes), so the
+    // hardware returns zero without touching memory: no loaded value is selected on, and the
+    // loads need not complete before the pipeline's loads are issued.
+    sgpu_f32x4 pa[2][2];
+    kd_f32x2 pb[NST];
+    float pt[NST];
+    auto load_part = [&](bool live) __attribute__((always_inline)) {
+        const Rs r = rsrc(0, live);
+        constexpr unsigned OUT = 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int v = 0; v < 2; v++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int k = NST * h + 4 * v + e;
+                    const unsigned off = k < kpart ? ((unsigned)(32 * i + l32) * K + k) * 4u : OUT;
+                    pa[i][v][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r.a, (int)off, 0, 0));
+                }
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            const int row = NST * h + st;
+            const unsigned ro = (unsigned)row * N * 4u;
+            pb[st] = __builtin_bit_cast(
+                kd_f32x2, __builtin_amdgcn_raw_buffer_load_b64(r.b, (int)(row < kpart ? ro + 8u * l32 : OUT), 0, 0));
+            if constexpr (TH)
+                pt[st] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               r.b, (int)(row < kpart ? ro + (unsigned)(N - 1 - nt) * 4u : OUT), 0, 0));
+        }
+    };
+    sgpu_f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    float tacc[2] = {0.0f, 0.0f};                                 // TH: rows l32, 32+l32 of column N-1
+    // MFMA step st on operands xa (two row blocks' quads), xb (column pair), xt (TH: column N-1)
+    auto step = [&](const sgpu_f32x4 (&xa)[2][2], const kd_f32x2& xb, float xt, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[i][st >> 2][st & 3], xb[j], acc[i][j], 0, 0, 0);
+        if constexpr (TH) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) tacc[i] = __builtin_fmaf(xa[i][st >> 2][st & 3], xt, tacc[i]);
+        }
+    };
+    // the MFMAs of the slice in set D, each register of the set reloaded with slice sn as soon
+    // as the MFMAs reading it have issued (RELOAD false: the last slice, nothing to load)
+    auto slice = [&](auto d_c, int sn, auto reload_c) __attribute__((always_inline)) {
+        constexpr int D = decltype(d_c)::value;
+        constexpr bool RELOAD = decltype(reload_c)::value;
+        Rs r;
+        if constexpr (RELOAD) r = rsrc(sn);
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            step(a[D], b[D][st], TH ? tb[D][st] : 0.0f, st);
+            if constexpr (RELOAD) {
+                if ((st & 3) == 3) {
+                    a[D][0][st >> 2] = lda(r, va0 + 16 * (st >> 2));
+                    a[D][1][st >> 2] = lda(r, va1 + 16 * (st >> 2));
+                }
+                b[D][st] = ldb(r, st);
+                if constexpr (TH) tb[D][st] = ldt(r, st);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using Z = std::integral_constant<int, 0>;
+    using O = std::integral_constant<int, 1>;
+    // Every wave issues the same loads before the loop, whatever it holds: the partial slice
+    // (EDGE; real only in the wave holding slice 0), then its first two whole slices (a wave with
+    // one re-reads it, a wave with none reads nothing: empty ranges return zeros).  Every path into
+    // the loop then has the same loads in flight in the same order, which keeps the compiler's
+    // wait counts in the loop exact (a load issued on one path only makes them all conservative).
+    // The wave holding a partial slice computes it before its whole slices sw...
+    const bool part = EDGE && kpart && s0 == 0 && s0 < s1;
+    const int sw = part ? 1 : s0;                                 // first whole slice
+    if constexpr (EDGE) load_part(part);
+    __builtin_amdgcn_sched_barrier(0);
+    load_whole(sw, Z{}, sw < s1);
+    load_whole(min(sw + 1, max(s1 - 1, sw)), O{}, sw < s1);
+    if (part) {
+#pragma unroll
+        for (int st = 0; st < NST; st++) step(pa, pb[st], TH ? pt[st] : 0.0f, st);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (sw < s1) {
+        // pairs of slices; the reloads of the last pair re-read slice s1-1 (in range, unused)
+        int s = sw;
+        for (; s + 2 <= s1; s += 2) {
+            slice(Z{}, min(s + 2, s1 - 1), std::true_type{});
+            slice(O{}, min(s + 3, s1 - 1), std::true_type{});
+        }
+        if (s < s1) slice(Z{}, 0, std::false_type{});
+    }
+    // Partial tiles: lane l's accumulator registers 4rq..4rq+3 of block (i, j) at
+    // red[((w*4 + 2i+j)*4 + rq)*64 + l] (red is used by nothing else: no barrier before it).
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++)
+                red[((wave * 4 + i * 2 + j) * 4 + rq) * 64 + lane] =
+                    sgpu_f32x4{acc[i][j][4 * rq], acc[i][j][4 * rq + 1], acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]};
+    float* tred = reinterpret_cast<float*>(red + 4 * 4 * 4 * 64);
+    if constexpr (TH) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) tred[(wave * 2 + h) * 64 + i * 32 + l32] = tacc[i];
+    }
+    __syncthreads();
+    if constexpr (TH) {
+        if (wave == 0) {
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; w++) v += tred[w * 64 + lane];
+            if (mt + lane >= m0) __builtin_nontemporal_store(v, C + (size_t)(mt + lane) * N + (N - 1));
+        }
+    }
+    // Wave w finishes row block w/2, accumulator quads 2(w%2) and 2(w%2)+1 of both column
+    // blocks, summing the four waves' partials in wave order.  D layout: lane l, register r ->
+    // row 8*(r/4) + 4*(l/32) + r%4 of the block; column block j, lane l -> column nt + 2*(l%32) + j.
+    const int bi = wave >> 1;
+    const bool whole = !EDGE || (mt == m0 && nt == n0);
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int rq = 2 * (wave & 1) + q;
+        sgpu_f32x4 v[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            sgpu_f32x4 p[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) p[w] = red[((w * 4 + bi * 2 + j) * 4 + rq) * 64 + lane];
+            v[j] = ((p[0] + p[1]) + p[2]) + p[3];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int gm = mt + bi * 32 + 8 * rq + 4 * h + e, gn = nt + 2 * l32;
+            float* dst = C + (size_t)gm * N + gn;
+            if (whole) {
+                __builtin_nontemporal_store(kd_f32x2_a4{v[0][e], v[1][e]}, reinterpret_cast<kd_f32x2_a4*>(dst));
+            } else if (gm >= m0) {
+                if (gn >= n0) __builtin_nontemporal_store(v[0][e], dst);
+                if (gn + 1 >= n0) __builtin_nontemporal_store(v[1][e], dst + 1);
+            }
+        }
+    }
+    __syncthreads();                                              // red is reused by the next tile
+}
+
 }  // namespace
 
 extern "C" {
@@ -944,12 +1191,57 @@ sgemm_small32(const float* __restrict__ A, const float* __restrict__ B, float* _
     sgemm_small<32, 4>(A, B, C, M, N, K);
 }
 
-// sgemm_kwave: the 64x64 tile with K split over the block's four waves, for problems with M,
-// N multiples of 64, K a multiple of 32 and 16-byte aligned A and B (any other problem, or a
-// block size other than 256, returns without writing C).  Grid-stride over tiles, one block
-// per tile remapped XCD-compact as the other members; 144 KB of LDS, one block per CU.
+// sgemm_kwave: the 64x64 tile with K split over the block's four waves, operands loaded straight
+// into the matrix-core registers, for problems with M, N multiples of 64, K a multiple of 32,
+// 16-byte aligned A and B, a 64-row A panel (64*K floats) and a 16-row B slice (16*N floats)
+// each under 2^31 bytes (any other problem, or a block size other than 256, returns without
+// writing C; sgemm_kwave_wide takes the larger operands).  Grid-stride over tiles, one block per
+// tile remapped XCD-compact as the other members; 64 KB of LDS for the partial-tile sum.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 sgemm_kwave(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) sgpu_f32x4 red[4 * 4 * 4 * 64];
+    if (!sgpu_block256() || M <= 0 || N <= 0 || K <= 0 || M % 64 || N % 64 || K % KW_BK ||
+        ((((uintptr_t)A) | ((uintptr_t)B)) & 15) || !kd_fits(N, K))
+        return;
+    const int ntm = M / 64, ntn = N / 64, ntiles = ntm * ntn;
+    const int nb = sgpu_nblocks();
+    const bool remap = nb == ntiles && ntiles % kXcds == 0;
+    for (int t = sgpu_bid(); t < ntiles; t += nb) {
+        int tm, tn;
+        sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+        sgemm_kdirect_tile<false, false>(A, B, C, M, N, K, tm * 64, tn * 64, red);
+    }
+}
+
+// sgemm_kwave_edge: sgemm_kwave for any M >= 64, N >= 64 and K >= 1, rows of any float
+// alignment, under the same 2^31-byte bounds (sgemm_kwave_edge_wide beyond them).  A partial
+// last row or column of tiles is computed as the 64 rows (columns) ending at the last one and
+// stored from its first new row (column) on; with K % 16 != 0 the first k-slice is the partial
+// one (k < K % 16, zeros past it).  N % 64 == 1 (one column past the last whole tile) is
+// computed by the last column of whole tiles alongside their MFMAs (TH) rather than by a column
+// of 64-wide tiles; every other N rounds the tile columns up.  Tiles: ceil(M/64) times N/64
+// (N % 64 == 1) or ceil(N/64); grid-stride as sgemm_kwave; 66 KB of LDS.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgemm_kwave_edge(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) sgpu_f32x4 red[4 * 4 * 4 * 64 + 8 * 64 / 4];
+    if (!sgpu_block256() || M < 64 || N < 64 || K < 1 || !kd_fits(N, K)) return;
+    const bool th = N % 64 == 1;
+    const int ntm = (M + 63) / 64, ntn = th ? N / 64 : (N + 63) / 64, ntiles = ntm * ntn;
+    const int nb = sgpu_nblocks();
+    const bool remap = nb == ntiles && ntiles % kXcds == 0;
+    for (int t = sgpu_bid(); t < ntiles; t += nb) {
+        int tm, tn;
+        sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+        if (th && tn == ntn - 1) sgemm_kdirect_tile<true, true>(A, B, C, M, N, K, tm * 64, tn * 64, red);
+        else sgemm_kdirect_tile<true, false>(A, B, C, M, N, K, tm * 64, tn * 64, red);
+    }
+}
+
+// sgemm_kwave_wide / sgemm_kwave_edge_wide: the same members for operands past those bounds,
+// staged through LDS with 64-bit addresses (sgemm_kwave_tile: 32-deep slices, K % 32 for the
+// exact member); 144 / 145 KB of LDS, one block per CU.  Any other problem as above.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgemm_kwave_wide(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
     __shared__ __attribute__((aligned(16))) KwaveLds L[4];
     static_assert(sizeof(L) >= 4 * 4 * 4 * 64 * sizeof(sgpu_f32x4), "the partial tiles fit the staging");
     if (!sgpu_block256() || M <= 0 || N <= 0 || K <= 0 || M % 64 || N % 64 || K % KW_BK ||
@@ -965,16 +1257,9 @@ sgemm_kwave(const float* __restrict__ A, const float* __restrict__ B, float* __r
                                        reinterpret_cast<sgpu_f32x4*>(&L[0]));
     }
 }
-
-// sgemm_kwave_edge: sgemm_kwave for any M >= 64, N >= 64 and K >= 1, rows of any float
-// alignment.  A partial last row or column of tiles is computed as the 64 rows (columns)
-// ending at the last one and stored from its first new row (column) on; with K % 32 != 0 the
-// first k-slice is the partial one (k < K % 32, zeros past it).  N % 64 == 1 (one column past the last whole tile) is computed
-// by the last column of whole tiles alongside their MFMAs (TH) rather than by a column of
-// 64-wide tiles; every other N rounds the tile columns up.  Tiles: ceil(M/64) times N/64
-// (N % 64 == 1) or ceil(N/64); grid-stride as sgemm_kwave; 145 KB of LDS, one block per CU.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
-sgemm_kwave_edge(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+sgemm_kwave_edge_wide(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
+                      int K) {
     __shared__ __attribute__((aligned(16))) KwaveLdsEdge L[4];
     static_assert(sizeof(L) >= 4 * 4 * 4 * 64 * sizeof(sgpu_f32x4) + 8 * 64 * sizeof(float),
                   "the partial tiles and the extra column's partials fit the staging");
@@ -986,12 +1271,11 @@ sgemm_kwave_edge(const float* __restrict__ A, const float* __restrict__ B, float
     for (int t = sgpu_bid(); t < ntiles; t += nb) {
         int tm, tn;
         sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+        sgpu_f32x4* red = reinterpret_cast<sgpu_f32x4*>(&L[0]);
         if (th && tn == ntn - 1)
-            sgemm_kwave_tile<true, true>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6],
-                                         reinterpret_cast<sgpu_f32x4*>(&L[0]));
+            sgemm_kwave_tile<true, true>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6], red);
         else
-            sgemm_kwave_tile<true, false>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6],
-                                          reinterpret_cast<sgpu_f32x4*>(&L[0]));
+            sgemm_kwave_tile<true, false>(A, B, C, M, N, K, tm * 64, tn * 64, L[sgpu_tid() >> 6], red);
     }
 }
 

@@ -169,11 +169,14 @@ def test_opt_launches_its_plan(gpu, M, N, K):
 # Shapes whose edge tiles take the clamped-address path: an A tile (BM rows of K floats) or a
 # B slice (BK rows of N floats) of 2^31 bytes or more.  Entries in {-1, 0, 1}: every partial
 # sum is an exact fp32 integer (|sum| <= K < 2^24).
-# The edge member's loads use 64-bit addresses throughout: A and B of 2^31 bytes or more through
-# a K tail, and the extra column (N % 64 == 1) at 2^23 + 1 columns.
+# The K-over-waves members: buffer offsets up to just under 2^31 bytes (a 64-row A panel of
+# 64 * (2^23 - 32) floats), the LDS-staged forms with 64-bit addresses past that (A of 2^31 bytes
+# and more, with and without a K tail), and the extra column (N % 64 == 1) at 2^23 + 1 columns.
 @pytest.mark.parametrize("fn,M,N,K", [("sgpu_sgemm_tiled", 3, 5, (1 << 23) + 7),
                                       ("sgpu_sgemm_opt256", 3, 5, (1 << 21) + 3),
                                       ("sgpu_sgemm_tiled", 2, (1 << 24) + 5, 3),
+                                      ("sgpu_sgemm_kwave", 64, 64, (1 << 23) - 32),
+                                      ("sgpu_sgemm_kwave", 64, 64, 1 << 23),
                                       ("sgpu_sgemm_kwave_edge", 64, 64, (1 << 23) + 7),
                                       ("sgpu_sgemm_kwave_edge", 64, (1 << 23) + 1, 65)])
 def test_large_operand_windows_integer_exact(gpu, fn, M, N, K):
@@ -404,10 +407,12 @@ def test_small_integer_exact(gpu, M, N, K, tile):
         assert np.array_equal(dC.to_host(), want)
 
 
-# sgemm_kwave splits each tile's 32-deep slices over the block's four waves: one slice (three
-# waves idle), three (one idle), uneven quarters, and up to 32 slices per wave.
+# sgemm_kwave splits each tile's 16-deep slices over the block's four waves: two slices (two
+# waves idle), six (uneven), one or two per wave (no pipelined pair, one pair), odd counts per
+# wave (the pipeline's tail slice), and up to 64 slices per wave.
 KWAVE_CASES = [(64, 64, 32), (64, 64, 96), (64, 128, 160), (128, 192, 1024), (256, 320, 544),
-               (512, 1024, 2048), (64, 64, 4096), (1024, 1024, 1024)]
+               (512, 1024, 2048), (64, 64, 4096), (1024, 1024, 1024), (64, 64, 64), (128, 64, 128),
+               (64, 128, 192), (192, 64, 224), (64, 64, 352)]
 
 
 @pytest.mark.parametrize("M,N,K", KWAVE_CASES)
@@ -489,11 +494,14 @@ def test_opt_unaligned_kwave_shape_takes_the_edge_member(gpu):
 
 # sgemm_kwave_edge: M, N >= 64 with partial last rows and columns of tiles (computed as the 64
 # ending at the last one), N % 64 == 1 (the column computed by the last column of whole tiles:
-# one such column, many), K tails of 1..31 and K < 4 (element-wise A loads), one slice (three
-# waves idle), uneven quarters, up to 130 slices per wave, and rows of any float alignment.
+# one such column, many), K tails of 1..15 (the partial first slice: up to 8 deep, one lane half
+# padded; 9..15, both halves partly real) and K < 16 (the partial slice alone), a wave holding
+# only the partial slice, one slice (three waves idle), uneven quarters, up to 260 slices per
+# wave, and rows of any float alignment.
 EDGE_CASES = [(64, 64, 1), (64, 65, 37), (130, 64, 33), (127, 129, 131), (64, 64, 5), (200, 191, 3),
               (64, 127, 100), (100, 100, 2), (65, 4097, 64), (300, 1025, 2047), (64, 65, 4103),
-              (1023, 1025, 997), (1024, 1024, 1000), (1023, 1000, 997), (8192, 128, 1000)]
+              (1023, 1025, 997), (1024, 1024, 1000), (1023, 1000, 997), (8192, 128, 1000),
+              (64, 64, 16), (64, 64, 17), (65, 66, 25), (128, 130, 47), (64, 129, 24), (64, 65, 25)]
 
 
 @pytest.mark.parametrize("a_off,b_off", [(0, 0), (1, 3)])
