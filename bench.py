@@ -3,8 +3,8 @@
 Metric (headline): SGEMM TFLOPS at 4096^3 fp32 + batch-1 GEMV GB/s (fraction of HBM peak)
 + decode tok/s.  `value` is the SGEMM figure: a step is one C = A*B, M = N = K = 4096, fp32
 row-major, A and B from the reference generator (srand(42), gpu_workload.c:81-82), computed
-by sgpu_sgemm_opt through libswitchgpu.so (the 256x256-tile member sgemm_opt256 at this
-shape).  One verified launch, then W untimed warm-up steps immediately followed by exactly K
+by sgpu_sgemm_opt through libswitchgpu.so (the member its plan picks at this shape, named
+in the line's config: the K-over-waves member sgemm_kwave).  One verified launch, then W untimed warm-up steps immediately followed by exactly K
 timed steps between device synchronisations.  Inputs are resident in HBM before timing starts.
 
 Secondary figures measured in the same run (same JSON line):
@@ -581,8 +581,8 @@ def cpu_baseline(n, target_s=1.5):
 def pmc_probe():
     """One launch each of: add2 over 64 Mi floats (a plain elementwise kernel whose HBM
     traffic is known: 512 MiB read, 256 MiB written -- the counter calibration), the lm_head
-    gemv_h and gemv_hh, and ten back-to-back launches each of sgpu_sgemm_opt at 4096^3
-    (sgemm_opt256), 1024^3 (sgemm_kwave) and 1023x1025x997 (sgemm_kwave_edge); per-dispatch
+    gemv_h and gemv_hh, and ten back-to-back launches each of sgpu_sgemm_opt at 4096^3 and
+    1024^3 (sgemm_kwave) and 1023x1025x997 (sgemm_kwave_edge); per-dispatch
     counters are averaged.  Run under `rocprofv3 --pmc FETCH_SIZE`, again with WRITE_SIZE,
     and with the MFMA-busy counters; prints the algorithmic bytes of each launch as one JSON
     line."""
@@ -700,6 +700,8 @@ def main():
     log(f"device: {props.name.decode()} ({props.arch.decode()}), {props.compute_units} CUs, "
         f"{props.clock_khz / 1e3:.0f} MHz")
     n = 4096
+    S = ct.c_int(0)
+    member = sgpu.lib().sgpu_sgemm_opt_plan(n, n, n, props.compute_units, ct.byref(S)).decode()
     sg = bench_sgemm(n, args.steps, args.warmup)
     tflops = sg["flops"] * args.steps / sg["wall_s"] / 1e12
     achieved = sg["flops"] / (sg["kernel_ms"] * 1e-3) / 1e12
@@ -759,12 +761,12 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": "SGEMM C=A*B M=N=K=4096 fp32 row-major, A,B from srand(42) "
-                               "(rand()%2000-1000)/1000, alpha=1 beta=0, sgpu_sgemm_opt (launches the 256x256-tile "
-                               "member sgemm_opt256 at this shape)",
+                               "(rand()%2000-1000)/1000, alpha=1 beta=0, sgpu_sgemm_opt (launches the member "
+                               f"{member} at this shape)",
                    "M": n, "N": n, "K": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MATRIX_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MATRIX_TFLOPS, 4),
-                     "traffic": traffic.get("sgemm_opt256_4096")},
+                     "kernel": member, "traffic": traffic.get(f"{member}_4096")},
         "cpu_baseline": cpu,
         "steady_state": {"kernel_ms": round(sg["steady_ms"], 4), "launches": sg["steady_launches"],
                          "tflops": round(sg["flops"] / (sg["steady_ms"] * 1e-3) / 1e12, 3),

@@ -881,29 +881,34 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
         if (t16 <= cus && K <= 4096 && (K <= 2048 || t16 * 4 <= cus || M <= 16 || N <= 16)) return PLAN_SMALL16;
         if (t32 <= cus && K <= 1024) return PLAN_SMALL32;
     }
-    /* Whole 64x64 tiles filling 3/4 to all of the CUs in one round, K a multiple of 32 and
-     * at least 1024: the 64x64 tile with K split over its four waves (no block-wide slice
-     * barrier in the k loop).  Recorded graphs, srand inputs, us: 1024^3 20.0 vs 20.8 for the
-     * 64x64 member; 1024x1024x2048 35.8 vs 38.2; 1024x1024x4096 66.6 vs 74.0 for the split
-     * pick (S = 2); 1024x1024x8192 128.6 vs 140.1 (S = 2); 768x1024x1024 19.9 vs 20.7
-     * (S = 4).  With fewer tiles the K splits across blocks win (512x1024x1024 15.4 at S = 2
-     * vs 19.7; 768x768x2048 28.0 at S = 5 vs 35.4), and at K = 512 the two 64x64 forms tie
-     * (1024x1024x512 12.2 vs 12.2). */
-    if (kwave_shape(M, N, K) && K >= 1024) {
-        const long long tiles = (long long)(M / 64) * (N / 64);
-        if (tiles <= cus && 4 * tiles >= 3LL * cus) return PLAN_KWAVE;
+    /* M and N of 64 or more, K of 256 or more: the 64x64 tile with K split over its four waves
+     * and the operands loaded straight into the matrix-core registers, on whole tiles
+     * (sgemm_kwave: M, N multiples of 64, K of 32) or with clamped edge tiles and a zero-padded
+     * first k-slice (sgemm_kwave_edge), whatever the tile count.  Its k loop runs at about 97%
+     * of the MFMA issue rate, so it beats the larger tiles and the K splits across blocks from
+     * one tile to many rounds of tiles.  Recorded graphs, zero inputs, us, against this
+     * function's earlier pick: 4096^3 914 vs 941 (sgemm_opt256); 2048^3 120 vs 126
+     * (sgemm_tiled4); 3072^3 392 vs 444 (sgemm_tiled); 4097^3 1031 vs 1162; 1024^3 17.9 vs 19.8;
+     * 1024x1024x512 10.9 vs 11.8; 1024x1024x256 7.4 vs 7.6; 768x768x2048 32.6 vs 37.1 (split,
+     * S = 5); 512x1024x1024 17.6 vs 20.0 (S = 2); 256x256x8192 117.5 vs 137.7 (S = 16);
+     * 64x64x8192 114.6 vs 136.2 (S = 16); 1023x1025x997 19.9 vs 21.6; 2048x1024x1000 33.8 vs
+     * 40.9; 1000x1000x256 8.6 vs 9.0.  The exception: many rounds of short k loops where the
+     * 256x256 member fills the CUs, whose larger tiles amortise the per-tile fill and
+     * partial-tile sum (4096x4096x1024 243 vs 250; 8192x8192x1024 970 vs 989; at K 2048 it is
+     * a tie, 8192x8192x2048 1883 vs 1872).  Below K 256 the 64x64 member keeps the shapes whose
+     * 64x64 tiles fit one round (1024x1024x128 5.5 vs 5.7; 1000x1000x192 7.6 vs 7.8). */
+    if (M >= 64 && N >= 64 && K >= 256) {
+        const int exact = kwave_shape(M, N, K);
+        const long long tiles = exact ? (long long)(M / 64) * (N / 64) : kwave_edge_tiles(M, N);
+        if (!(K < 2048 && tiles > 12LL * cus && g_sgemm_members[sgemm_pick(M, N, cus)].kid == K_SGEMM_OPT256))
+            return exact ? PLAN_KWAVE : PLAN_KWAVE_EDGE;
     }
-    /* Any other problem whose edge-member tiles (M and N rounded up to 64, or N rounded down
-     * when N % 64 == 1) fill 3/4 to all of the CUs in one round: the same structure with
-     * clamped edge tiles and a zero-padded first k-slice, from K 384, or from K 128 when the
-     * 64x64 member would need a second round (N % 64 == 1 past the CUs).  Recorded graphs,
-     * srand inputs, us, against the best of the 64x64 member and S = 2..6 splits:
-     * 1023x1025x997 22.0 vs 31.1 (S = 4); 1024x1024x1000 21.0 vs 26.6; 1023x1025x128 7.1 vs
-     * 8.2; 1023x1025x96 7.0 vs 7.0; 1023x1025x64 6.9 vs 5.8; 1000x1000x384 11.5 vs 12.2;
-     * 1000x1000x320 11.2 vs 10.8; 1000x1000x256 9.3 vs 9.3; 1000x1000x192 9.1 vs 7.8. */
-    if (kwave_edge_shape(M, N, K) && !kwave_shape(M, N, K) && K >= 128) {
+    /* K from 128 to 255 on edge tiles that fill 3/4 to all of the CUs in one round while the
+     * 64x64 member would need a second (N % 64 == 1 rides on the last column of whole tiles):
+     * 1023x1025x128 7.0 vs 7.0, against 5.6 vs 6.0 for the 64x64 member at K 64. */
+    if (kwave_edge_shape(M, N, K) && K >= 128) {
         const long long tiles = kwave_edge_tiles(M, N), tiles64 = (long long)cdiv(M, 64) * cdiv(N, 64);
-        if (tiles <= cus && 4 * tiles >= 3LL * cus && (K >= 384 || tiles64 > cus)) return PLAN_KWAVE_EDGE;
+        if (tiles <= cus && 4 * tiles >= 3LL * cus && tiles64 > cus) return PLAN_KWAVE_EDGE;
     }
     if (K > 0 && (*S = splitk_pick(M, N, K, cus)) > 1) return PLAN_SPLITK;
     *S = 1;

@@ -17,46 +17,52 @@ sys.path.insert(0, os.path.join(ROOT, "switch-l4t-gpu_amd"))
 import sgpu  # noqa: E402
 
 PINNED_256 = [
-    # large problems: the member whose busiest CU has the least work
-    (4096, 4096, 4096, "sgemm_opt256", 1),
-    (8192, 8192, 8192, "sgemm_opt256", 1),
-    (2048, 2048, 2048, "sgemm_tiled4", 1),
-    (3072, 3072, 3072, "sgemm_tiled", 1),
-    (4097, 4097, 4097, "sgemm_tiled", 1),
-    # one round of 64x64 tiles, K a multiple of 32: whole tiles filling 3/4 of the CUs or more
-    # with K >= 1024 take the K-over-waves member; fewer tiles split K across blocks
+    # M, N >= 64 and K >= 256: the K-over-waves members (operands straight into the matrix
+    # cores) at any tile count, whole tiles (K a multiple of 32) or clamped edge tiles
+    (4096, 4096, 4096, "sgemm_kwave", 1),
+    (8192, 8192, 8192, "sgemm_kwave", 1),
+    (2048, 2048, 2048, "sgemm_kwave", 1),
+    (3072, 3072, 3072, "sgemm_kwave", 1),
+    (6144, 6144, 1024, "sgemm_kwave", 1),
     (1024, 1024, 1024, "sgemm_kwave", 1),
     (1024, 1024, 4096, "sgemm_kwave", 1),
     (1024, 768, 1024, "sgemm_kwave", 1),
-    (1024, 1024, 992, "sgemm_tiled", 1),
-    (1024, 1024, 512, "sgemm_tiled", 1),
-    (768, 768, 2048, "sgemm_splitk", 5),
-    (512, 1024, 1024, "sgemm_splitk", 2),
-    (1088, 1024, 1024, "sgemm_splitk", 4),
-    # edge tiles (M or N off 64, K off 32) filling 3/4 of the CUs or more in one round: the
-    # K-over-waves edge member from K 384, or from K 128 when the 64x64 member needs a second
-    # round (N % 64 == 1 rides on the last column of whole tiles)
+    (1024, 1024, 992, "sgemm_kwave", 1),
+    (1024, 1024, 512, "sgemm_kwave", 1),
+    (1024, 1024, 256, "sgemm_kwave", 1),
+    (768, 768, 2048, "sgemm_kwave", 1),
+    (512, 1024, 1024, "sgemm_kwave", 1),
+    (1088, 1024, 1024, "sgemm_kwave", 1),
+    (64, 64, 8192, "sgemm_kwave", 1),
+    (256, 256, 4096, "sgemm_kwave", 1),
+    (4097, 4097, 4097, "sgemm_kwave_edge", 1),
     (1023, 1025, 997, "sgemm_kwave_edge", 1),
     (1000, 1000, 1000, "sgemm_kwave_edge", 1),
     (1024, 1024, 1000, "sgemm_kwave_edge", 1),
     (8192, 128, 1000, "sgemm_kwave_edge", 1),
     (1000, 1000, 384, "sgemm_kwave_edge", 1),
+    (640, 640, 1000, "sgemm_kwave_edge", 1),
+    (1087, 1085, 2000, "sgemm_kwave_edge", 1),
+    (1408, 1408, 997, "sgemm_kwave_edge", 1),
+    (2048, 1024, 1000, "sgemm_kwave_edge", 1),
+    # many rounds of short k loops where the 256x256 member fills the CUs
+    (4096, 4096, 1024, "sgemm_opt256", 1),
+    (8192, 8192, 1024, "sgemm_opt256", 1),
+    # K under 256: the 64x64 member, or the edge member from K 128 when N % 64 == 1 would give
+    # the 64x64 member a second round
+    (1024, 1024, 128, "sgemm_tiled", 1),
+    (1000, 1000, 192, "sgemm_tiled", 1),
     (1023, 1025, 128, "sgemm_kwave_edge", 1),
     (1023, 1025, 64, "sgemm_tiled", 1),
-    # K tails
-    (640, 640, 1000, "sgemm_splitk", 5),
-    (1087, 1085, 2000, "sgemm_splitk", 7),
-    (1408, 1408, 997, "sgemm_tiled", 1),
-    (2048, 1024, 1000, "sgemm_tiled", 1),
-    # few tiles: tall K splits up to 16 ways, one row or column of tiles
-    (64, 64, 8192, "sgemm_splitk", 16),
+    # M or N under 64: K splits up to 16 ways, one row or column of tiles
     (32, 32, 16384, "sgemm_splitk", 16),
-    (256, 256, 4096, "sgemm_splitk", 8),
     (8192, 1, 2048, "sgemm_splitk", 2),
     (1, 8192, 4096, "sgemm_splitk", 4),
     # the small members
     (256, 256, 256, "sgemm_small16", 1),
+    (256, 256, 2048, "sgemm_small16", 1),
     (512, 512, 512, "sgemm_small32", 1),
+    (512, 512, 1024, "sgemm_small32", 1),
     (1, 4096, 4096, "sgemm_small16", 1),
     (16, 4096, 4096, "sgemm_small16", 1),
     (100, 70, 3000, "sgemm_small16", 1),
@@ -102,14 +108,16 @@ def test_plan_invariants(cus):
                     elif name == "sgemm_small32":
                         assert cdiv(M, 32) * cdiv(N, 32) <= cus and K <= 1024
                     elif name == "sgemm_kwave":
-                        assert M % 64 == 0 and N % 64 == 0 and K % 32 == 0 and K >= 1024
-                        assert tiles <= cus and 4 * tiles >= 3 * cus
+                        assert M % 64 == 0 and N % 64 == 0 and K % 32 == 0 and K >= 256
                     elif name == "sgemm_kwave_edge":
                         assert M >= 64 and N >= 64 and K >= 128
                         assert M % 64 or N % 64 or K % 32
                         edge_tiles = cdiv(M, 64) * (N // 64 if N % 64 == 1 else cdiv(N, 64))
-                        assert edge_tiles <= cus and 4 * edge_tiles >= 3 * cus
-                        assert K >= 384 or tiles > cus
+                        if K < 256:
+                            assert edge_tiles <= cus and 4 * edge_tiles >= 3 * cus and tiles > cus
+                    elif M >= 64 and N >= 64 and K >= 256:
+                        # only the 256x256 member over many rounds of short k loops
+                        assert name == "sgemm_opt256" and K < 2048 and tiles > 12 * cus
                     else:
                         assert name in members
 
