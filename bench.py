@@ -241,18 +241,21 @@ def bench_sgemm_sweep(reps=100, warm=50, graphs=True, warm_s=0.1, cpu=False):
         st = sgpu.Stream()
         sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
         st.synchronize()
-        per_graph = 10
+        # 50 launches a graph (the graph launch's own cost spread thin), the median of five
+        # event-timed replays
+        per_graph, replays = 50, 5
         with sgpu.Graph(st) as g:
             for _ in range(per_graph):
                 sgpu.call("sgpu_sgemm_opt", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
         warm_for(g.launch, st.synchronize, max(1, warm // per_graph), warm_s)
-        for _ in range(2):
+        g.launch()
+        times = []
+        for _ in range(replays):
+            ev.record_start(st.h)
             g.launch()
-        ev.record_start(st.h)
-        for _ in range(max(1, reps // per_graph)):
-            g.launch()
-        ev.record_stop(st.h)
-        us_g = ev.elapsed_ms() * 1e3 / (max(1, reps // per_graph) * per_graph)
+            ev.record_stop(st.h)
+            times.append(ev.elapsed_ms() * 1e3 / per_graph)
+        us_g = float(np.median(times))
         g.close()
         st.close()
         tf = 2.0 * M * N * K / (us_g * 1e-6) / 1e12

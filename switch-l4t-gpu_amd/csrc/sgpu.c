@@ -881,27 +881,18 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
         if (t16 <= cus && K <= 4096 && (K <= 2048 || t16 * 4 <= cus || M <= 16 || N <= 16)) return PLAN_SMALL16;
         if (t32 <= cus && K <= 1024) return PLAN_SMALL32;
     }
-    /* M and N of 64 or more, K of 256 or more: the 64x64 tile with K split over its four waves
-     * and the operands loaded straight into the matrix-core registers, on whole tiles
-     * (sgemm_kwave: M, N multiples of 64, K of 32) or with clamped edge tiles and a zero-padded
-     * first k-slice (sgemm_kwave_edge), whatever the tile count.  Its k loop runs at about 97%
-     * of the MFMA issue rate, so it beats the larger tiles and the K splits across blocks from
-     * one tile to many rounds of tiles.  Recorded graphs, zero inputs, us, against this
-     * function's earlier pick: 4096^3 914 vs 941 (sgemm_opt256); 2048^3 120 vs 126
-     * (sgemm_tiled4); 3072^3 392 vs 444 (sgemm_tiled); 4097^3 1031 vs 1162; 1024^3 17.9 vs 19.8;
-     * 1024x1024x512 10.9 vs 11.8; 1024x1024x256 7.4 vs 7.6; 768x768x2048 32.6 vs 37.1 (split,
-     * S = 5); 512x1024x1024 17.6 vs 20.0 (S = 2); 256x256x8192 117.5 vs 137.7 (S = 16);
-     * 64x64x8192 114.6 vs 136.2 (S = 16); 1023x1025x997 19.9 vs 21.6; 2048x1024x1000 33.8 vs
-     * 40.9; 1000x1000x256 8.6 vs 9.0.  The exception: many rounds of short k loops where the
-     * 256x256 member fills the CUs, whose larger tiles amortise the per-tile fill and
-     * partial-tile sum (4096x4096x1024 243 vs 250; 8192x8192x1024 970 vs 989; at K 2048 it is
-     * a tie, 8192x8192x2048 1883 vs 1872).  Below K 256 the 64x64 member keeps the shapes whose
-     * 64x64 tiles fit one round (1024x1024x128 5.5 vs 5.7; 1000x1000x192 7.6 vs 7.8). */
+    /* One round of 64x64 tiles filling 3/4 to all of the CUs, K of 256 or more: the 64x64 tile
+     * with K split over its four waves and the operands loaded straight into the matrix-core
+     * registers, on whole tiles (sgemm_kwave: M, N multiples of 64, K of 32) or with clamped
+     * edge tiles and a zero-padded first k-slice (sgemm_kwave_edge).  Recorded graphs, random
+     * inputs in [-1, 1), us, against the 64x64 member: 1024^3 18.1 vs 20.5; 1024x1024x512
+     * 10.9 vs 11.9; 1024x1024x256 7.4 vs 7.7; 1023x1025x997 20.2 vs 40.3 (S = 4 split: 31.1);
+     * 1000^3 19.4 vs 27.3; 1000x1000x256 8.5 vs 9.1.  With fewer tiles the K splits across
+     * blocks win (512x1024x1024 15.3 at S = 2 vs 17.7; 768x768x2048 31.0 at S = 8 vs 32.6). */
     if (M >= 64 && N >= 64 && K >= 256) {
         const int exact = kwave_shape(M, N, K);
         const long long tiles = exact ? (long long)(M / 64) * (N / 64) : kwave_edge_tiles(M, N);
-        if (!(K < 2048 && tiles > 12LL * cus && g_sgemm_members[sgemm_pick(M, N, cus)].kid == K_SGEMM_OPT256))
-            return exact ? PLAN_KWAVE : PLAN_KWAVE_EDGE;
+        if (tiles <= cus && 4 * tiles >= 3LL * cus) return exact ? PLAN_KWAVE : PLAN_KWAVE_EDGE;
     }
     /* K from 128 to 255 on edge tiles that fill 3/4 to all of the CUs in one round while the
      * 64x64 member would need a second (N % 64 == 1 rides on the last column of whole tiles):
@@ -912,7 +903,16 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
     }
     if (K > 0 && (*S = splitk_pick(M, N, K, cus)) > 1) return PLAN_SPLITK;
     *S = 1;
-    return sgemm_pick(M, N, cus);
+    /* Where the busiest-CU model picks the 64x64 member over several rounds, the K-over-waves
+     * members run the same tiles faster (random inputs, us: 3072^3 422 vs 452; 2048x1024x1024
+     * 33.8 vs 37.2; 4097^3 1107 vs 1222; 2047x2049x2047 140 vs 179).  The larger tiles keep
+     * their shapes: they move half the bytes per flop or less, and with random operands the
+     * 64x64 tiles' extra traffic costs clock (4096^3 945 us on sgemm_opt256 vs 989; 2048^3 127
+     * on sgemm_tiled4 vs 130; 8192x1024x1024 131 vs 133). */
+    const int pick = sgemm_pick(M, N, cus);
+    if (g_sgemm_members[pick].kid == K_SGEMM_TILED && M >= 64 && N >= 64 && K >= 256)
+        return kwave_shape(M, N, K) ? PLAN_KWAVE : PLAN_KWAVE_EDGE;
+    return pick;
 }
 const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits) {
     if (M < 1 || N < 1 || K < 0 || cus < 1) return NULL;

@@ -17,52 +17,54 @@ sys.path.insert(0, os.path.join(ROOT, "switch-l4t-gpu_amd"))
 import sgpu  # noqa: E402
 
 PINNED_256 = [
-    # M, N >= 64 and K >= 256: the K-over-waves members (operands straight into the matrix
-    # cores) at any tile count, whole tiles (K a multiple of 32) or clamped edge tiles
-    (4096, 4096, 4096, "sgemm_kwave", 1),
-    (8192, 8192, 8192, "sgemm_kwave", 1),
-    (2048, 2048, 2048, "sgemm_kwave", 1),
+    # large problems: the member whose busiest CU has the least work; where that is the 64x64
+    # member (several rounds of 64x64 tiles, K >= 256) the K-over-waves members run its tiles
+    (4096, 4096, 4096, "sgemm_opt256", 1),
+    (8192, 8192, 8192, "sgemm_opt256", 1),
+    (4096, 4096, 1024, "sgemm_opt256", 1),
+    (2048, 2048, 2048, "sgemm_tiled4", 1),
+    (6144, 6144, 1024, "sgemm_tiled4", 1),
     (3072, 3072, 3072, "sgemm_kwave", 1),
-    (6144, 6144, 1024, "sgemm_kwave", 1),
+    (2048, 1024, 1024, "sgemm_kwave", 1),
+    (4097, 4097, 4097, "sgemm_kwave_edge", 1),
+    (2047, 2049, 2047, "sgemm_kwave_edge", 1),
+    (1408, 1408, 997, "sgemm_kwave_edge", 1),
+    (2048, 1024, 1000, "sgemm_kwave_edge", 1),
+    # one round of 64x64 tiles filling 3/4 of the CUs or more, K >= 256: the K-over-waves
+    # members (whole tiles, or clamped edge tiles and a partial first k-slice)
     (1024, 1024, 1024, "sgemm_kwave", 1),
     (1024, 1024, 4096, "sgemm_kwave", 1),
     (1024, 768, 1024, "sgemm_kwave", 1),
     (1024, 1024, 992, "sgemm_kwave", 1),
     (1024, 1024, 512, "sgemm_kwave", 1),
     (1024, 1024, 256, "sgemm_kwave", 1),
-    (768, 768, 2048, "sgemm_kwave", 1),
-    (512, 1024, 1024, "sgemm_kwave", 1),
-    (1088, 1024, 1024, "sgemm_kwave", 1),
-    (64, 64, 8192, "sgemm_kwave", 1),
-    (256, 256, 4096, "sgemm_kwave", 1),
-    (4097, 4097, 4097, "sgemm_kwave_edge", 1),
     (1023, 1025, 997, "sgemm_kwave_edge", 1),
     (1000, 1000, 1000, "sgemm_kwave_edge", 1),
     (1024, 1024, 1000, "sgemm_kwave_edge", 1),
     (8192, 128, 1000, "sgemm_kwave_edge", 1),
     (1000, 1000, 384, "sgemm_kwave_edge", 1),
-    (640, 640, 1000, "sgemm_kwave_edge", 1),
-    (1087, 1085, 2000, "sgemm_kwave_edge", 1),
-    (1408, 1408, 997, "sgemm_kwave_edge", 1),
-    (2048, 1024, 1000, "sgemm_kwave_edge", 1),
-    # many rounds of short k loops where the 256x256 member fills the CUs
-    (4096, 4096, 1024, "sgemm_opt256", 1),
-    (8192, 8192, 1024, "sgemm_opt256", 1),
+    (1000, 1000, 256, "sgemm_kwave_edge", 1),
     # K under 256: the 64x64 member, or the edge member from K 128 when N % 64 == 1 would give
     # the 64x64 member a second round
     (1024, 1024, 128, "sgemm_tiled", 1),
     (1000, 1000, 192, "sgemm_tiled", 1),
     (1023, 1025, 128, "sgemm_kwave_edge", 1),
     (1023, 1025, 64, "sgemm_tiled", 1),
-    # M or N under 64: K splits up to 16 ways, one row or column of tiles
+    # fewer tiles: K splits across blocks
+    (768, 768, 2048, "sgemm_splitk", 5),
+    (512, 1024, 1024, "sgemm_splitk", 2),
+    (1088, 1024, 1024, "sgemm_splitk", 4),
+    (640, 640, 1000, "sgemm_splitk", 5),
+    (1087, 1085, 2000, "sgemm_splitk", 7),
+    # few tiles: tall K splits up to 16 ways, one row or column of tiles
+    (64, 64, 8192, "sgemm_splitk", 16),
     (32, 32, 16384, "sgemm_splitk", 16),
+    (256, 256, 4096, "sgemm_splitk", 8),
     (8192, 1, 2048, "sgemm_splitk", 2),
     (1, 8192, 4096, "sgemm_splitk", 4),
     # the small members
     (256, 256, 256, "sgemm_small16", 1),
-    (256, 256, 2048, "sgemm_small16", 1),
     (512, 512, 512, "sgemm_small32", 1),
-    (512, 512, 1024, "sgemm_small32", 1),
     (1, 4096, 4096, "sgemm_small16", 1),
     (16, 4096, 4096, "sgemm_small16", 1),
     (100, 70, 3000, "sgemm_small16", 1),
@@ -115,11 +117,10 @@ def test_plan_invariants(cus):
                         edge_tiles = cdiv(M, 64) * (N // 64 if N % 64 == 1 else cdiv(N, 64))
                         if K < 256:
                             assert edge_tiles <= cus and 4 * edge_tiles >= 3 * cus and tiles > cus
-                    elif M >= 64 and N >= 64 and K >= 256:
-                        # only the 256x256 member over many rounds of short k loops
-                        assert name == "sgemm_opt256" and K < 2048 and tiles > 12 * cus
                     else:
                         assert name in members
+                        if name == "sgemm_tiled" and M >= 64 and N >= 64:
+                            assert K < 256                        # else the K-over-waves members run its tiles
 
 
 def test_plan_rejects():
