@@ -494,14 +494,16 @@ def test_opt_unaligned_kwave_shape_takes_the_edge_member(gpu):
 
 # sgemm_kwave_edge: M, N >= 64 with partial last rows and columns of tiles (computed as the 64
 # ending at the last one), N % 64 == 1 (the column computed by the last column of whole tiles:
-# one such column, many), K tails of 1..15 (the partial first slice: up to 8 deep, one lane half
+# one such column, many; with 16 or more tile columns it is spread over all of them, 4, 2 or
+# 1 rows a tile, some tiles with none), K tails of 1..15 (the partial first slice: up to 8 deep, one lane half
 # padded; 9..15, both halves partly real) and K < 16 (the partial slice alone), a wave holding
 # only the partial slice, one slice (three waves idle), uneven quarters, up to 260 slices per
 # wave, and rows of any float alignment.
 EDGE_CASES = [(64, 64, 1), (64, 65, 37), (130, 64, 33), (127, 129, 131), (64, 64, 5), (200, 191, 3),
               (64, 127, 100), (100, 100, 2), (65, 4097, 64), (300, 1025, 2047), (64, 65, 4103),
               (1023, 1025, 997), (1024, 1024, 1000), (1023, 1000, 997), (8192, 128, 1000),
-              (64, 64, 16), (64, 64, 17), (65, 66, 25), (128, 130, 47), (64, 129, 24), (64, 65, 25)]
+              (64, 64, 16), (64, 64, 17), (65, 66, 25), (128, 130, 47), (64, 129, 24), (64, 65, 25),
+              (130, 1281, 100), (70, 2561, 33)]
 
 
 @pytest.mark.parametrize("a_off,b_off", [(0, 0), (1, 3)])
