@@ -153,16 +153,19 @@ const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits);
  * (A, B, C, M, N, K) symbol arguments, for hosts that launch members by name. */
 int sgpu_sgemm_opt256(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 /* The sgemm_kwave member: 64x64 tiles of C, each computed by a block of four waves that
- * split K four ways, every wave accumulating the whole tile from its own LDS staging, the
- * four partial tiles summed in wave order.  M and N multiples of 64, K a multiple of 32, A
- * and B 16-byte aligned (SGPU_ERR_INVALID_ARG otherwise).  No counterpart in the reference:
- * an added member of the family with the (A, B, C, M, N, K) symbol arguments. */
+ * split K four ways, every wave accumulating the whole tile with its MFMA operands loaded
+ * straight from memory into registers, the four partial tiles summed in wave order.  M and
+ * N multiples of 64, K a multiple of 32, A and B 16-byte aligned (SGPU_ERR_INVALID_ARG
+ * otherwise).  Operands whose 64-row A panel or 16-row B slice reach 2^31 bytes run on the
+ * LDS-staged sgemm_kwave_wide instead (same results).  No counterpart in the reference: an
+ * added member of the family with the (A, B, C, M, N, K) symbol arguments. */
 int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 /* The sgemm_kwave_edge member: sgemm_kwave's structure for any M >= 64, N >= 64, K >= 1 and
  * float-aligned A, B, C (SGPU_ERR_INVALID_ARG otherwise; M or N == 0 is a no-op).  A partial
  * last row or column of tiles is computed as the 64 rows or columns ending at the last one
- * and stored from its first new row or column on; with K % 32 != 0 the first 32-deep k-slice
- * is the partial one (k < K % 32), read with zeros past it.
+ * and stored from its first new row or column on; with K % 16 != 0 the first 16-deep k-slice
+ * is the partial one (k < K % 16), read with zeros past it.  Operands past the 2^31-byte
+ * windows run on the LDS-staged sgemm_kwave_edge_wide (32-deep slices).
  * With N % 64 == 1 the last column is computed by the last column of whole tiles alongside
  * their MFMAs, so ceil(M/64) * (N/64) blocks; otherwise ceil(M/64) * ceil(N/64).  No
  * counterpart in the reference: an added member of the family with the (A, B, C, M, N, K)
