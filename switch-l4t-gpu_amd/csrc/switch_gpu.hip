@@ -910,8 +910,9 @@ __device__ __forceinline__ void sgemm_kwave_tile(const float* __restrict__ A, co
 //   zero (clamped in-range addresses, then replaced), so a non-finite value never meets a
 //   padded zero.
 // TH (EDGE, N % 64 == 1, the last column of whole tiles): lane (l32, h) also loads column N-1
-//   of its eight B rows per slice and meets its A operands in 16 VALU FMAs per slice; the eight
-//   (wave, lane half) partials of each row are summed at the end.
+//   of its eight B rows per slice and meets its A operands in 16 VALU FMAs per slice, issued
+//   together before the slice's MFMAs; the eight (wave, lane half) partials of each row are
+//   summed at the end.
 constexpr int KD_SD = 16;
 __host__ __device__ constexpr bool kd_fits(long long N, long long K) {
     return K * 64 * 4 < 2147483648LL && N * KD_SD * 4 < 2147483648LL;
@@ -1015,18 +1016,24 @@ __device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, 
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-    float tacc[2] = {0.0f, 0.0f};                                 // TH: rows l32, 32+l32 of column N-1
-    // MFMA step st on operands xa (two row blocks' quads), xb (column pair), xt (TH: column N-1)
-    auto step = [&](const sgpu_f32x4 (&xa)[2][2], const kd_f32x2& xb, float xt, int st) __attribute__((always_inline)) {
+    // TH: rows l32 and 32+l32 of column N-1, in two chains (even and odd MFMA steps) summed at
+    // the end
+    float tacc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    // TH: a slice's 16 column FMAs, issued together ahead of its MFMAs (0.2-0.3 µs a launch
+    // faster than one pair after each MFMA step)
+    auto column = [&](const sgpu_f32x4 (&xa)[2][2], const float (&xt)[NST]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < NST; st++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) tacc[st & 1][i] = __builtin_fmaf(xa[i][st >> 2][st & 3], xt[st], tacc[st & 1][i]);
+    };
+    // MFMA step st on operands xa (two row blocks' quads) and xb (column pair)
+    auto step = [&](const sgpu_f32x4 (&xa)[2][2], const kd_f32x2& xb, int st) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[i][st >> 2][st & 3], xb[j], acc[i][j], 0, 0, 0);
-        if constexpr (TH) {
-#pragma unroll
-            for (int i = 0; i < 2; i++) tacc[i] = __builtin_fmaf(xa[i][st >> 2][st & 3], xt, tacc[i]);
-        }
     };
     // the MFMAs of the slice in set D, each register of the set reloaded with slice sn as soon
     // as the MFMAs reading it have issued (RELOAD false: the last slice, nothing to load)
@@ -1035,9 +1042,11 @@ __device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, 
         constexpr bool RELOAD = decltype(reload_c)::value;
         Rs r;
         if constexpr (RELOAD) r = rsrc(sn);
+        if constexpr (TH) column(a[D], tb[D]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int st = 0; st < NST; st++) {
-            step(a[D], b[D][st], TH ? tb[D][st] : 0.0f, st);
+            step(a[D], b[D][st], st);
             if constexpr (RELOAD) {
                 if ((st & 3) == 3) {
                     a[D][0][st >> 2] = lda(r, va0 + 16 * (st >> 2));
@@ -1065,7 +1074,8 @@ __device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, 
     load_whole(min(sw + 1, max(s1 - 1, sw)), O{}, sw < s1);
     if (part) {
 #pragma unroll
-        for (int st = 0; st < NST; st++) step(pa, pb[st], TH ? pt[st] : 0.0f, st);
+        for (int st = 0; st < NST; st++) step(pa, pb[st], st);
+        if constexpr (TH) column(pa, pt);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (sw < s1) {
@@ -1090,7 +1100,7 @@ __device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, 
     float* tred = reinterpret_cast<float*>(red + 4 * 4 * 4 * 64);
     if constexpr (TH) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) tred[(wave * 2 + h) * 64 + i * 32 + l32] = tacc[i];
+        for (int i = 0; i < 2; i++) tred[(wave * 2 + h) * 64 + i * 32 + l32] = tacc[0][i] + tacc[1][i];
     }
     __syncthreads();
     if constexpr (TH) {
