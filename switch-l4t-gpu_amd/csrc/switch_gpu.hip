@@ -1060,15 +1060,15 @@ __device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, 
     };
     using Z = std::integral_constant<int, 0>;
     using O = std::integral_constant<int, 1>;
-    // Every wave issues the same loads before the loop, whatever it holds: the partial slice
-    // (EDGE; real only in the wave holding slice 0), then its first two whole slices (a wave with
-    // one re-reads it, a wave with none reads nothing: empty ranges return zeros).  Every path into
-    // the loop then has the same loads in flight in the same order, which keeps the compiler's
-    // wait counts in the loop exact (a load issued on one path only makes them all conservative).
-    // The wave holding a partial slice computes it before its whole slices sw...
+    // Before the loop: the partial slice (EDGE, only in the wave holding slice 0), then every
+    // wave's first two whole slices, unconditionally (a wave with one re-reads it, a wave with
+    // none reads nothing: empty ranges return zeros).  Every path into the loop then has the same
+    // loads newest in flight in the same order, which keeps the compiler's wait counts in the
+    // loop exact (a load issued after them on one path only makes them all conservative).  The
+    // wave holding a partial slice computes it before its whole slices sw...
     const bool part = EDGE && kpart && s0 == 0 && s0 < s1;
     const int sw = part ? 1 : s0;                                 // first whole slice
-    if constexpr (EDGE) load_part(part);
+    if (part) load_part(true);
     __builtin_amdgcn_sched_barrier(0);
     load_whole(sw, Z{}, sw < s1);
     load_whole(min(sw + 1, max(s1 - 1, sw)), O{}, sw < s1);
