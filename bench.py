@@ -165,8 +165,11 @@ def bench_gemv_lm_head(reps=100, copies=4, warm=1000, x16=False):
     return dict(us=us, bytes=algo_bytes, gbps=algo_bytes / (us * 1e-6) / 1e9, err=err, copies=copies, W=W, x=x)
 
 
-SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
-                (1023, 1025, 997)]
+# In order of size.  A shape timed right after 4096^3 (about 0.6 s of the chip at full matrix
+# load) runs slower than the same shape timed before it: 1023x1025x997 took 20.7-21.3 us a launch
+# in a graph straight after 4096^3, 20.5 after a 0.5 s pause, and 20.2 before any large shape.
+SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1023, 1025, 997), (1024, 1024, 1024), (2048, 2048, 2048),
+                (4096, 4096, 4096)]
 GEMV_SHAPES = [("fp32", "gpt2 qkv", 2304, 768), ("fp32", "gpt2 attn-out", 768, 768), ("fp32", "gpt2 fc", 3072, 768),
                ("fp32", "gpt2 proj", 768, 3072), ("fp32", "gpt2 lm_head", 50257, 768),
                ("fp16", "qwen q", 896, 896), ("fp16", "qwen k/v", 128, 896), ("fp16", "qwen o", 896, 896),
