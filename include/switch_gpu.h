@@ -171,6 +171,14 @@ int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int
  * counterpart in the reference: an added member of the family with the (A, B, C, M, N, K)
  * symbol arguments. */
 int sgpu_sgemm_kwave_edge(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+/* The sgemm_kwave128 member: sgemm_kwave's structure on 128x128 tiles (each wave accumulates
+ * the whole tile over a quarter of K, 16-deep k-slices handed out in pairs).  M and N multiples
+ * of 128, K a multiple of 32, A and B 16-byte aligned, a 128-row A panel (128*K floats) and a
+ * 16-row B slice (16*N floats) each under 2^31 bytes (SGPU_ERR_INVALID_ARG otherwise; there
+ * is no wide form).  One block of 256 threads per tile, (M/128) * (N/128) blocks.  No
+ * counterpart in the reference: an added member of the family with the (A, B, C, M, N, K)
+ * symbol arguments. */
+int sgpu_sgemm_kwave128(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 /* The sgemm_splitk member: 64x64 tiles with K split S ways (S >= 1; reduced so that every
  * split holds at least one 32-deep slice), each (tile, split) a block.  Every split writes its
  * partial tile to a library-owned workspace of the launch's stream and the last split of a

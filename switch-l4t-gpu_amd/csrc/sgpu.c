@@ -47,7 +47,8 @@ static const struct {
 /* Every kernel the launchers use: (module, symbol). */
 enum {
     K_SGEMM_TILED, K_SGEMM_TILED4, K_SGEMM_OPT, K_SGEMM_OPT256, K_SGEMM_SPLITK, K_SGEMM_SMALL16, K_SGEMM_SMALL32,
-    K_SGEMM_KWAVE, K_SGEMM_KWAVE_EDGE, K_SGEMM_KWAVE_WIDE, K_SGEMM_KWAVE_EDGE_WIDE, K_SGEMM_NAIVE, K_MEMBW,
+    K_SGEMM_KWAVE, K_SGEMM_KWAVE_EDGE, K_SGEMM_KWAVE_WIDE, K_SGEMM_KWAVE_EDGE_WIDE, K_SGEMM_KWAVE128, K_SGEMM_NAIVE,
+    K_MEMBW,
     K_GEMV, K_GEMV4, K_GEMV_WARP, K_GEMV_WARP_B, K_GEMV_MULTI, K_GEMV_MULTI_SPLITK, K_GEMV_MULTI_X8_64,
     K_GEMV_MULTI_X8_256,
     K_GEMV_H, K_GEMV_HH, K_RMSNORM, K_ROPE, K_SWIGLU, K_ASCORES, K_ASOFTMAX, K_AMIX, K_ADD2,
@@ -62,7 +63,8 @@ static const struct {
     {MOD_SWITCH, "sgemm_tiled"}, {MOD_SWITCH, "sgemm_tiled4"}, {MOD_SWITCH, "sgemm_opt"},
     {MOD_SWITCH, "sgemm_opt256"}, {MOD_SWITCH, "sgemm_splitk"}, {MOD_SWITCH, "sgemm_small16"},
     {MOD_SWITCH, "sgemm_small32"}, {MOD_SWITCH, "sgemm_kwave"}, {MOD_SWITCH, "sgemm_kwave_edge"},
-    {MOD_SWITCH, "sgemm_kwave_wide"}, {MOD_SWITCH, "sgemm_kwave_edge_wide"}, {MOD_SWITCH, "sgemm_naive"},
+    {MOD_SWITCH, "sgemm_kwave_wide"}, {MOD_SWITCH, "sgemm_kwave_edge_wide"}, {MOD_SWITCH, "sgemm_kwave128"},
+    {MOD_SWITCH, "sgemm_naive"},
     {MOD_SWITCH, "membw_read4"},
     {MOD_GEMV, "gemv"}, {MOD_GEMV, "gemv4"}, {MOD_GEMV, "gemv_warp"},
     {MOD_GPT2, "gemv_warp_b"}, {MOD_GPT2, "gemv_multi"}, {MOD_GPT2, "gemv_multi_splitk"},
@@ -585,6 +587,7 @@ static int sgemm_tile(const char *k, int *tn) {
     if (!strcmp(k, "sgemm_opt")) return *tn = 256, 128;
     if (!strcmp(k, "sgemm_opt256")) return *tn = 256, 256;
     if (!strcmp(k, "sgemm_kwave") || !strcmp(k, "sgemm_kwave_wide")) return *tn = 64, 64;
+    if (!strcmp(k, "sgemm_kwave128")) return *tn = 128, 128;
     return *tn = 0, 0;
 }
 
@@ -697,6 +700,19 @@ int sgpu_sgemm_kwave(const float *A, const float *B, float *C, int M, int N, int
     if (M == 0 || N == 0) return SGPU_OK;
     if (!kwave_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B) & 15)) return SGPU_ERR_INVALID_ARG;
     return kwave_launch(0, A, B, C, M, N, K, stream);
+}
+/* sgemm_kwave128's problems: M, N multiples of 128, K a multiple of 32, a 128-row A panel and a
+ * 16-row B slice each under 2^31 bytes (32-bit buffer offsets; there is no wide form), and
+ * 16-byte aligned A and B (the launcher's check). */
+static int kwave128_shape(int M, int N, int K) {
+    return M > 0 && N > 0 && K > 0 && M % 128 == 0 && N % 128 == 0 && K % 32 == 0 &&
+           (long long)K * 512 < (1LL << 31) && (long long)N * 64 < (1LL << 31);
+}
+int sgpu_sgemm_kwave128(const float *A, const float *B, float *C, int M, int N, int K, void *stream) {
+    if (M < 0 || N < 0 || K < 0) return SGPU_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return SGPU_OK;
+    if (!kwave128_shape(M, N, K) || !A || !B || !C || (((uintptr_t)A | (uintptr_t)B) & 15)) return SGPU_ERR_INVALID_ARG;
+    return sgemm_common(K_SGEMM_KWAVE128, "sgemm_kwave128", A, B, C, M, N, K, stream);
 }
 /* sgemm_kwave_edge's problems: M, N at least 64 (a partial last row or column of tiles is the
  * 64 rows or columns ending at the last one), K at least 1, float-aligned operands. */
@@ -867,7 +883,7 @@ int sgpu_sgemm_small(const float *A, const float *B, float *C, int M, int N, int
 /* The launch sgpu_sgemm_opt makes for an M x N x K problem on `cus` CUs: PLAN_SMALL16 /
  * PLAN_SMALL32, PLAN_SPLITK with *S splits (the unsplit member is launched instead when the
  * stream has no workspace), or an index into g_sgemm_members. */
-enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3, PLAN_KWAVE = -4, PLAN_KWAVE_EDGE = -5 };
+enum { PLAN_SMALL16 = -1, PLAN_SMALL32 = -2, PLAN_SPLITK = -3, PLAN_KWAVE = -4, PLAN_KWAVE_EDGE = -5, PLAN_KWAVE128 = -6 };
 static int opt_plan(int M, int N, int K, int cus, int *S) {
     *S = 1;
     /* Problems whose 16x16 (32x32) tiles fit the CUs in one round go to the small members
@@ -910,6 +926,22 @@ static int opt_plan(int M, int N, int K, int cus, int *S) {
      * 64x64 tiles' extra traffic costs clock (4096^3 945 us on sgemm_opt256 vs 989; 2048^3 127
      * on sgemm_tiled4 vs 130; 8192x1024x1024 131 vs 133). */
     const int pick = sgemm_pick(M, N, cus);
+    /* The 128x128 K-over-waves member where its tiles fill whole rounds of the CUs (the last
+     * round at least 94% full) and K is deep enough to carry its per-round cost (about 6.6 us:
+     * the first slices' latency, the partial-tile sum through LDS, the C store): K >= 512
+     * against the 128x128 and 128x256 members, K >= 4096 against sgemm_opt256, which needs
+     * fewer rounds.  Recorded graphs, random inputs in [-1, 1), us, against the pick before it:
+     * 2048^3 121.7 vs 127.7 (sgemm_tiled4); 2048x2048x512 36.5 vs 37.3; 6144^3 3156 vs 3326;
+     * 2048x4096x2048 242.3 vs 252.7 (sgemm_opt); 2816^3 327 vs 345; 4096^3 935 vs 947
+     * (sgemm_opt256); 8192^3 7465 vs 7526; 4096x4096x8192 1836 vs 1893.  Where it loses:
+     * 4096x4096x2048 482 vs 478, 2048x8192x1024 255 vs 246 (both sgemm_opt256), 2048x2048x256
+     * 22.3 vs 22.1, and every shape with a partly empty last round (5120^3 2036 vs 1980 at 89%
+     * full, 3072^3 525 vs 437 at 75%). */
+    if (kwave128_shape(M, N, K)) {
+        const long long t128 = (long long)(M / 128) * (N / 128), r128 = (t128 + cus - 1) / cus;
+        const int deep = g_sgemm_members[pick].kid == K_SGEMM_OPT256 ? K >= 4096 : K >= 512;
+        if (50 * t128 >= 47 * r128 * cus && deep) return PLAN_KWAVE128;
+    }
     if (g_sgemm_members[pick].kid == K_SGEMM_TILED && M >= 64 && N >= 64 && K >= 256)
         return kwave_shape(M, N, K) ? PLAN_KWAVE : PLAN_KWAVE_EDGE;
     return pick;
@@ -924,6 +956,7 @@ const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits) {
     if (p == PLAN_SPLITK) return "sgemm_splitk";
     if (p == PLAN_KWAVE) return "sgemm_kwave";
     if (p == PLAN_KWAVE_EDGE) return "sgemm_kwave_edge";
+    if (p == PLAN_KWAVE128) return "sgemm_kwave128";
     return g_sgemm_members[p].name;
 }
 
@@ -941,6 +974,8 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
     unsigned *cnt;
     if (p == PLAN_SPLITK && sk_workspace(d, stream, &ws, &cnt) == SGPU_OK)    /* else: the unsplit member */
         return splitk_launch(d, A, B, C, M, N, K, S, ws, cnt, stream);
+    if (p == PLAN_KWAVE128 && !(((uintptr_t)A | (uintptr_t)B) & 15))
+        return sgemm_common(K_SGEMM_KWAVE128, "sgemm_kwave128", A, B, C, M, N, K, stream);
     if (p == PLAN_KWAVE && !(((uintptr_t)A | (uintptr_t)B) & 15)) return kwave_launch(0, A, B, C, M, N, K, stream);
     if ((p == PLAN_KWAVE || p == PLAN_KWAVE_EDGE) && !(((uintptr_t)A | (uintptr_t)B | (uintptr_t)C) & 3))
         return kwave_launch(1, A, B, C, M, N, K, stream);   /* rows of any float alignment */

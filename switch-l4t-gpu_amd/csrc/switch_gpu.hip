@@ -1142,6 +1142,146 @@ __device__ __forceinline__ void sgemm_kdirect_tile(const float* __restrict__ A, 
     __syncthreads();                                              // red is reused by the next tile
 }
 
+// The K-over-waves structure on a 128x128 tile (sgemm_kwave128): half the operand bytes per
+// flop of the 64x64 tile, 4x4 MFMA blocks per wave (256 accumulator registers), so one block
+// per CU.  Slices are 16 deep, handed to the waves in pairs (K % 32 == 0): every wave has an
+// even count and the loop has no odd tail, whose separate copy made the compiler spill.
+//   Lane (l32, h) holds A rows mt+32i+l32 (i = 0..3) at k0+8h .. k0+8h+7 (two 16-byte loads
+//   per row; the row block through the scalar offset) and, for MFMA step t, B's row k0+8h+t at
+//   columns nt+4*l32 .. nt+4*l32+3 (one 16-byte load): column block j of the tile is the
+//   columns nt+4c+j, and a lane stores C four adjacent columns at a time.
+//   Two register sets, each register reloaded with the slice after next right after the MFMAs
+//   that read it, as in sgemm_kdirect_tile.
+//   The four partial tiles are summed through LDS in two rounds of two row blocks (128 KB a
+//   round), in wave order.
+// A 128-row A panel (128*K floats) and a 16-row B slice must each be under 2^31 bytes.
+constexpr int K128_SD = 16;
+__host__ __device__ constexpr bool k128_fits(long long N, long long K) {
+    return K * 128 * 4 < 2147483648LL && N * K128_SD * 4 < 2147483648LL;
+}
+__device__ __forceinline__ void sgemm_k128_tile(const float* __restrict__ A, const float* __restrict__ B,
+                                                float* __restrict__ C, int N, int K, int mt, int nt,
+                                                sgpu_f32x4* __restrict__ red) {
+    constexpr int SD = K128_SD, NST = SD / 2;
+    const int lane = sgpu_tid() & 63, wave = __builtin_amdgcn_readfirstlane(sgpu_tid() >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    const int np = K / (2 * SD);                                   // slice pairs
+    const int s0 = 2 * (wave * np / 4), s1 = 2 * ((wave + 1) * np / 4);
+    const unsigned va = ((unsigned)l32 * K + NST * h) * 4u;
+    const unsigned rowstep = 32u * (unsigned)K * 4u;               // one row block of A
+    const unsigned vb = ((unsigned)NST * h * N + 4 * l32) * 4u;
+    sgpu_f32x4 a[2][4][2];                                        // [set][row block][quad]
+    sgpu_f32x4 b[2][NST];                                         // [set][step]: columns 4c..4c+3
+    struct Rs {
+        __amdgpu_buffer_rsrc_t a, b;
+    };
+    // slice s at k0 = 16 s; live false: empty ranges, every load returns zero
+    auto rsrc = [&](int s, bool live = true) __attribute__((always_inline)) -> Rs {
+        const long long k0 = (long long)s * SD;
+        return {__builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)mt * K + k0), (short)0,
+                                                  live ? (int)((128LL * K - k0) * 4) : 0, 0x00020000),
+                __builtin_amdgcn_make_buffer_rsrc((void*)(B + (size_t)k0 * N + nt), (short)0,
+                                                  live ? (int)((long long)SD * N * 4) : 0, 0x00020000)};
+    };
+    auto lda = [&](const Rs& r, int i, int v) __attribute__((always_inline)) {
+        return __builtin_bit_cast(sgpu_f32x4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(r.a, (int)(va + 16 * v), (int)(i * rowstep), 0));
+    };
+    auto ldb = [&](const Rs& r, int st) __attribute__((always_inline)) {
+        return __builtin_bit_cast(sgpu_f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.b, (int)vb, st * N * 4, 0));
+    };
+    auto load_whole = [&](int s, auto d_c, bool live = true) __attribute__((always_inline)) {
+        constexpr int D = decltype(d_c)::value;
+        const Rs r = rsrc(s, live);
+#pragma unroll
+        for (int v = 0; v < 2; v++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[D][i][v] = lda(r, i, v);
+#pragma unroll
+            for (int e = 0; e < 4; e++) b[D][4 * v + e] = ldb(r, 4 * v + e);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    sgpu_f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    auto step = [&](const sgpu_f32x4 (&xa)[4][2], const sgpu_f32x4& xb, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[i][st >> 2][st & 3], xb[j], acc[i][j], 0, 0, 0);
+    };
+    auto slice = [&](auto d_c, int sn) __attribute__((always_inline)) {
+        constexpr int D = decltype(d_c)::value;
+        const Rs r = rsrc(sn);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            step(a[D], b[D][st], st);
+            if ((st & 3) == 3) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) a[D][i][st >> 2] = lda(r, i, st >> 2);
+            }
+            b[D][st] = ldb(r, st);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using Z = std::integral_constant<int, 0>;
+    using O = std::integral_constant<int, 1>;
+    // both sets before the loop, unconditionally (a wave with no slices reads nothing), so every
+    // path into the loop has the same loads in flight and its wait counts stay exact; the last
+    // pair's reloads re-read slice s1-1 (in range, unused)
+    load_whole(s0, Z{}, s0 < s1);
+    load_whole(min(s0 + 1, max(s1 - 1, s0)), O{}, s0 < s1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int s = s0; s < s1; s += 2) {
+        slice(Z{}, min(s + 2, s1 - 1));
+        slice(O{}, min(s + 3, s1 - 1));
+    }
+    // Round r sums row blocks 2r and 2r+1: lane l's accumulator quad rq of block (2r+ii, j) goes
+    // to red[(w*32 + ii*16 + j*4 + rq)*64 + l]; wave w finishes row block 2r + (w >> 1), quads
+    // 2(w & 1) and 2(w & 1)+1 of all four column blocks.  D layout: lane l, register r -> row
+    // 8*(r/4) + 4*(l/32) + r%4 of the block; column block j, lane l -> column nt + 4*(l%32) + j.
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int rq = 0; rq < 4; rq++)
+                    red[(wave * 32 + ii * 16 + j * 4 + rq) * 64 + lane] =
+                        sgpu_f32x4{acc[2 * r + ii][j][4 * rq], acc[2 * r + ii][j][4 * rq + 1],
+                                   acc[2 * r + ii][j][4 * rq + 2], acc[2 * r + ii][j][4 * rq + 3]};
+        __syncthreads();
+        const int ii = wave >> 1;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int rq = 2 * (wave & 1) + q;
+            sgpu_f32x4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sgpu_f32x4 p[4];
+#pragma unroll
+                for (int w = 0; w < 4; w++) p[w] = red[(w * 32 + ii * 16 + j * 4 + rq) * 64 + lane];
+                v[j] = ((p[0] + p[1]) + p[2]) + p[3];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int gm = mt + 32 * (2 * r + ii) + 8 * rq + 4 * h + e;
+                __builtin_nontemporal_store(sgpu_f32x4{v[0][e], v[1][e], v[2][e], v[3][e]},
+                                            reinterpret_cast<sgpu_f32x4*>(C + (size_t)gm * N + nt + 4 * l32));
+            }
+        }
+        __syncthreads();                                          // red is rewritten next
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -1244,6 +1384,28 @@ sgemm_kwave_edge(const float* __restrict__ A, const float* __restrict__ B, float
         sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
         if (th && tn == ntn - 1) sgemm_kdirect_tile<true, true>(A, B, C, M, N, K, tm * 64, tn * 64, red);
         else sgemm_kdirect_tile<true, false>(A, B, C, M, N, K, tm * 64, tn * 64, red);
+    }
+}
+
+// sgemm_kwave128: 128x128 tiles, K split over the block's four waves, operands straight into
+// the matrix-core registers (sgemm_k128_tile), for M and N multiples of 128, K a multiple of 32,
+// 16-byte aligned A and B, a 128-row A panel and a 16-row B slice each under 2^31 bytes (any
+// other problem, or a block size other than 256, returns without writing C).  Grid-stride over
+// tiles, one block per tile remapped XCD-compact as the other members; 128 KB of LDS for the
+// partial-tile sum.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+sgemm_kwave128(const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) sgpu_f32x4 red[4 * 32 * 64];
+    if (!sgpu_block256() || M <= 0 || N <= 0 || K <= 0 || M % 128 || N % 128 || K % (2 * K128_SD) ||
+        ((((uintptr_t)A) | ((uintptr_t)B)) & 15) || !k128_fits(N, K))
+        return;
+    const int ntm = M / 128, ntn = N / 128, ntiles = ntm * ntn;
+    const int nb = sgpu_nblocks();
+    const bool remap = nb == ntiles && ntiles % kXcds == 0;
+    for (int t = sgpu_bid(); t < ntiles; t += nb) {
+        int tm, tn;
+        sgemm_tile_coords(t, ntm, ntn, remap, tm, tn);
+        sgemm_k128_tile(A, B, C, N, K, tm * 128, tn * 128, red);
     }
 }
 

@@ -77,6 +77,7 @@ _SIGS = {
     "sgpu_sgemm_opt256": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_kwave": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_kwave_edge": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "sgpu_sgemm_kwave128": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "sgpu_sgemm_splitk": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_sgemm_splitk_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "sgpu_sgemm_small": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),

@@ -14,7 +14,7 @@ REFERENCE_KERNELS = {
     "switch_gpu": {"sgemm_tiled", "sgemm_tiled4", "sgemm_opt", "sgemm_naive", "membw_read4",
                    "sgemm_opt256", "sgemm_splitk", "sgemm_small16",
                    "sgemm_small32", "sgemm_kwave", "sgemm_kwave_edge", "sgemm_kwave_wide",
-                   "sgemm_kwave_edge_wide"},          # the last eight are added members
+                   "sgemm_kwave_edge_wide", "sgemm_kwave128"},   # the last nine are added members
                                                       # (no reference counterpart)
     "gemv": {"gemv", "gemv4", "gemv_warp"},
     "gpt2_kernels": {"gemv_warp", "gemv_warp_b", "gemv_multi", "layernorm", "gelu", "add_bias", "add2",

@@ -252,7 +252,9 @@ def test_gemv_test_harness(gpu, co, args):
 # clamped edge tiles and, N % 64 == 1, the tiles that also compute column N-1).
 BYNAME_KWAVE = [("sgemm_kwave", 256, 320, 544, 5), ("sgemm_kwave", 128, 192, 1024, 1),
                 ("sgemm_kwave_edge", 1023, 1025, 997, 7), ("sgemm_kwave_edge", 200, 191, 33, 3),
-                ("sgemm_kwave_edge", 130, 65, 40, 1), ("sgemm_kwave_edge", 1000, 1000, 1000, 64)]
+                ("sgemm_kwave_edge", 130, 65, 40, 1), ("sgemm_kwave_edge", 1000, 1000, 1000, 64),
+                ("sgemm_kwave128", 384, 512, 544, 5), ("sgemm_kwave128", 256, 256, 1024, 1),
+                ("sgemm_kwave128", 2048, 2048, 256, 100)]
 
 
 @pytest.mark.parametrize("sym,M,N,K,grid", BYNAME_KWAVE)

@@ -170,15 +170,17 @@ def test_opt_launches_its_plan(gpu, M, N, K):
 # B slice (BK rows of N floats) of 2^31 bytes or more.  Entries in {-1, 0, 1}: every partial
 # sum is an exact fp32 integer (|sum| <= K < 2^24).
 # The K-over-waves members: buffer offsets up to just under 2^31 bytes (a 64-row A panel of
-# 64 * (2^23 - 32) floats), the LDS-staged forms with 64-bit addresses past that (A of 2^31 bytes
-# and more, with and without a K tail), and the extra column (N % 64 == 1) at 2^23 + 1 columns.
+# 64 * (2^23 - 32) floats, a 128-row one of 128 * (2^22 - 32)), the LDS-staged forms with 64-bit
+# addresses past that (A of 2^31 bytes and more, with and without a K tail), and the extra
+# column (N % 64 == 1) at 2^23 + 1 columns.
 @pytest.mark.parametrize("fn,M,N,K", [("sgpu_sgemm_tiled", 3, 5, (1 << 23) + 7),
                                       ("sgpu_sgemm_opt256", 3, 5, (1 << 21) + 3),
                                       ("sgpu_sgemm_tiled", 2, (1 << 24) + 5, 3),
                                       ("sgpu_sgemm_kwave", 64, 64, (1 << 23) - 32),
                                       ("sgpu_sgemm_kwave", 64, 64, 1 << 23),
                                       ("sgpu_sgemm_kwave_edge", 64, 64, (1 << 23) + 7),
-                                      ("sgpu_sgemm_kwave_edge", 64, (1 << 23) + 1, 65)])
+                                      ("sgpu_sgemm_kwave_edge", 64, (1 << 23) + 1, 65),
+                                      ("sgpu_sgemm_kwave128", 128, 128, (1 << 22) - 32)])
 def test_large_operand_windows_integer_exact(gpu, fn, M, N, K):
     say(f"sgemm {fn} large window {M}x{N}x{K}")
     rng = np.random.default_rng(K + N)
@@ -711,6 +713,79 @@ def test_kwave_nonfinite_inputs_propagate(gpu, M, N, K):
     gpu.synchronize()
     got = dC.to_host()
     assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])
+
+
+# sgemm_kwave128 hands each tile's 16-deep slices to the block's four waves in pairs: one pair
+# (three waves idle), two and three pairs (uneven), one pair each, many pairs each, one tile,
+# one round of tiles and a grid of several rounds (2304 x 2048: 288 tiles).
+KWAVE128_CASES = [(128, 128, 32), (128, 128, 64), (128, 256, 96), (256, 128, 128), (384, 256, 352),
+                  (128, 128, 4096), (1024, 1024, 1024), (2048, 2048, 256), (2304, 2048, 64)]
+
+
+@pytest.mark.parametrize("M,N,K", KWAVE128_CASES)
+def test_kwave128_integer_exact(gpu, M, N, K):
+    """sgemm_kwave128 gives the exact product on integer inputs, twice in a row."""
+    say(f"sgemm kwave128 integer {M}x{N}x{K}")
+    rng = np.random.default_rng(M * 11 + N * 5 + K)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    for _ in range(2):
+        dC.fill_bytes(0xFF)
+        gpu.call("sgpu_sgemm_kwave128", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+        gpu.synchronize()
+        assert np.array_equal(dC.to_host(), want)
+
+
+def test_kwave128_reference_inputs(gpu, og):
+    """Reference-generator inputs at 1024^3 within the normwise bar of the oracle."""
+    n = 1024
+    say(f"sgemm kwave128 n={n} reference inputs")
+    A, B = ref_inputs(n, n, n)
+    C = run_sgemm(gpu, "sgpu_sgemm_kwave128", A, B, n, n, n)
+    ref = ref_golden(n, n, n)
+    assert np.abs(C.astype(np.float64) - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    assert og.sgemm_verdict_bad(C, ref, n, n) == 0
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (384, 128, 1024)])
+def test_kwave128_nonfinite_inputs_propagate(gpu, M, N, K):
+    """The non-finite operands of the other members through sgemm_kwave128."""
+    say(f"sgemm kwave128 non-finite {M}x{N}x{K}")
+    A, B, want = nonfinite_operands(M, N, K, M + 5 * N + 3 * K)
+    dA, dB, dC = gpu.DeviceArray.from_host(A), gpu.DeviceArray.from_host(B), gpu.DeviceArray((M, N))
+    dC.fill_bytes(0xFF)
+    gpu.call("sgpu_sgemm_kwave128", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+    gpu.synchronize()
+    got = dC.to_host()
+    assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])
+
+
+def test_kwave128_rejects_other_shapes(gpu):
+    """Shapes sgemm_kwave128 does not take (including a 128-row A panel or a 16-row B slice of
+    2^31 bytes), and operands off 16-byte alignment, are refused before any launch; M or N = 0
+    is a no-op."""
+    dA, dB, dC = gpu.DeviceArray(128 * 4096 + 4), gpu.DeviceArray(4096 * 256 + 4), gpu.DeviceArray(128 * 256)
+    L = gpu.lib()
+    for M, N, K in ((64, 128, 64), (128, 192, 64), (128, 128, 48), (128, 128, 16), (128, 128, 0), (-128, 128, 64),
+                    (128, 128, 1 << 22), (128, 1 << 25, 32)):
+        assert L.sgpu_sgemm_kwave128(dA.ptr, dB.ptr, dC.ptr, M, N, K, None) == gpu.SGPU_ERR_INVALID_ARG, (M, N, K)
+    assert L.sgpu_sgemm_kwave128(dA.offset(1), dB.ptr, dC.ptr, 128, 128, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave128(dA.ptr, dB.offset(2), dC.ptr, 128, 128, 64, None) == gpu.SGPU_ERR_INVALID_ARG
+    assert L.sgpu_sgemm_kwave128(dA.ptr, dB.ptr, dC.ptr, 0, 128, 64, None) == 0
+
+
+def test_opt_unaligned_kwave128_shape_takes_the_size_rule_member(gpu):
+    """sgpu_sgemm_opt plans sgemm_kwave128 for 2048^3; with A off 16-byte alignment it launches
+    the member the size rule picks (sgemm_tiled4), whose C it then equals bit for bit."""
+    M = N = K = 2048
+    rng = np.random.default_rng(2048)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    C = run_sgemm(gpu, "sgpu_sgemm_opt", A, B, M, N, K, a_off=1)
+    D = run_sgemm(gpu, "sgpu_sgemm_tiled4", A, B, M, N, K, a_off=1)
+    assert np.array_equal(C, D)
 
 
 @pytest.mark.parametrize("tile", [16, 32])

@@ -17,13 +17,25 @@ sys.path.insert(0, os.path.join(ROOT, "switch-l4t-gpu_amd"))
 import sgpu  # noqa: E402
 
 PINNED_256 = [
+    # whole rounds of 128x128 tiles (the last at least 94% full) with K >= 512 (K >= 4096 where
+    # the busiest-CU model picks sgemm_opt256): the 128x128 K-over-waves member
+    (4096, 4096, 4096, "sgemm_kwave128", 1),
+    (8192, 8192, 8192, "sgemm_kwave128", 1),
+    (2048, 2048, 2048, "sgemm_kwave128", 1),
+    (2048, 2048, 512, "sgemm_kwave128", 1),
+    (6144, 6144, 1024, "sgemm_kwave128", 1),
+    (2048, 4096, 2048, "sgemm_kwave128", 1),
+    (2816, 2816, 2816, "sgemm_kwave128", 1),
+    (4096, 4096, 8192, "sgemm_kwave128", 1),
     # large problems: the member whose busiest CU has the least work; where that is the 64x64
     # member (several rounds of 64x64 tiles, K >= 256) the K-over-waves members run its tiles
-    (4096, 4096, 4096, "sgemm_opt256", 1),
-    (8192, 8192, 8192, "sgemm_opt256", 1),
     (4096, 4096, 1024, "sgemm_opt256", 1),
-    (2048, 2048, 2048, "sgemm_tiled4", 1),
-    (6144, 6144, 1024, "sgemm_tiled4", 1),
+    (4096, 4096, 2048, "sgemm_opt256", 1),
+    (2048, 8192, 1024, "sgemm_opt256", 1),
+    (2048, 2048, 256, "sgemm_tiled4", 1),
+    (5120, 5120, 5120, "sgemm_kwave", 1),
+    (4096, 4096, 4064, "sgemm_opt256", 1),
+    (4096, 4096, 4080, "sgemm_opt256", 1),
     (3072, 3072, 3072, "sgemm_kwave", 1),
     (2048, 1024, 1024, "sgemm_kwave", 1),
     (4097, 4097, 4097, "sgemm_kwave_edge", 1),
@@ -88,7 +100,8 @@ def cdiv(a, b):
 
 @pytest.mark.parametrize("cus", [1, 80, 104, 256, 304])
 def test_plan_invariants(cus):
-    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled", "sgemm_kwave", "sgemm_kwave_edge"}
+    members = {"sgemm_opt256", "sgemm_opt", "sgemm_tiled4", "sgemm_tiled", "sgemm_kwave", "sgemm_kwave_edge",
+               "sgemm_kwave128"}
     for M in (1, 17, 64, 300, 1000, 1023, 2048):
         for N in (1, 64, 511, 1000, 1025, 4096):
             for K in (0, 1, 31, 64, 128, 320, 997, 2048, 8192):
@@ -111,6 +124,10 @@ def test_plan_invariants(cus):
                         assert cdiv(M, 32) * cdiv(N, 32) <= cus and K <= 1024
                     elif name == "sgemm_kwave":
                         assert M % 64 == 0 and N % 64 == 0 and K % 32 == 0 and K >= 256
+                    elif name == "sgemm_kwave128":
+                        t128 = (M // 128) * (N // 128)
+                        assert M % 128 == 0 and N % 128 == 0 and K % 32 == 0 and K >= 512
+                        assert 50 * t128 >= 47 * cdiv(t128, cus) * cus
                     elif name == "sgemm_kwave_edge":
                         assert M >= 64 and N >= 64 and K >= 128
                         assert M % 64 or N % 64 or K % 32
