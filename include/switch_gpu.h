@@ -134,7 +134,11 @@ int sgpu_kernel_geometry(const char *kernel, int M, int N, int K, unsigned grid[
  * multiple of 32 and at least 1024, go to sgemm_kwave (to sgemm_kwave_edge when A or B is
  * off 16-byte alignment), and other problems whose sgemm_kwave_edge tiles fill 3/4 to all
  * of the CUs in one round, with K >= 384 (K >= 128 when the 64x64 tiles would not fit the
- * CUs in one round), go to sgemm_kwave_edge. */
+ * CUs in one round), go to sgemm_kwave_edge.  Of the problems left for the size rule, those
+ * with M, N multiples of 128 and K of 32 whose 128x128 tiles fill whole rounds of the CUs
+ * (the last at least 94% full), with K >= 512 (K >= 4096 where the size rule picks
+ * sgemm_opt256), go to sgemm_kwave128 (to the size rule's member when A or B is off
+ * 16-byte alignment). */
 int sgpu_sgemm_tiled(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_tiled4(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
 int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
@@ -144,8 +148,9 @@ int sgpu_sgemm_opt(const float *A, const float *B, float *C, int M, int N, int K
  * is launched (M or N < 1) or an argument is invalid.  sgpu_sgemm_opt launches the unsplit
  * member instead of "sgemm_splitk" on a stream being recorded that has no workspace yet;
  * the plan assumes 16-byte aligned A and B: with A or B off 16 bytes, "sgemm_kwave" becomes
- * "sgemm_kwave_edge", and with an operand off 4 bytes "sgemm_kwave" or "sgemm_kwave_edge"
- * becomes the 64x64-or-larger member the size rule picks.
+ * "sgemm_kwave_edge" and "sgemm_kwave128" the member the size rule picks, and with an operand
+ * off 4 bytes "sgemm_kwave" or "sgemm_kwave_edge" becomes the 64x64-or-larger member the size
+ * rule picks.
  * No counterpart in the reference (its sgemm_opt is one kernel). */
 const char *sgpu_sgemm_opt_plan(int M, int N, int K, int cus, int *splits);
 /* The sgemm_opt256 member alone (any shape; masked loads on edge tiles).  No
