@@ -86,6 +86,10 @@ def test_geometry_contract(sg):
     assert tuple(b) == (256, 1, 1) and g[0] == 16 * 16          # one 256x256 tile per block
     assert L.sgpu_kernel_geometry(b"sgemm_tiled4", 4096, 4096, 4096, g, b) == 0
     assert tuple(b) == (256, 1, 1) and g[0] == 32 * 32          # one 128x128 tile per block
+    assert L.sgpu_kernel_geometry(b"sgemm_kwave128", 4096, 4096, 4096, g, b) == 0
+    assert tuple(b) == (256, 1, 1) and g[0] == 32 * 32          # one 128x128 tile per block
+    assert L.sgpu_kernel_geometry(b"sgemm_kwave", 1024, 1024, 1024, g, b) == 0
+    assert tuple(b) == (256, 1, 1) and g[0] == 16 * 16          # one 64x64 tile per block
     assert L.sgpu_kernel_geometry(b"sgemm_tiled", 1023, 1025, 997, g, b) == 0
     assert g[0] == 16 * 17                                       # ceil(1023/64) * ceil(1025/64)
     assert L.sgpu_kernel_geometry(b"sgemm_naive", 100, 50, 7, g, b) == 0

@@ -762,6 +762,33 @@ def test_kwave128_nonfinite_inputs_propagate(gpu, M, N, K):
     assert np.array_equal(got, want, equal_nan=True), (np.argwhere(~((got == want) | (np.isnan(got) & np.isnan(want))))[:5])
 
 
+def test_kwave128_graph_replay(gpu):
+    """sgemm_kwave128 recorded once in a graph and replayed with new inputs copied in between:
+    every replay equals the direct launch bit for bit (it uses no workspace and no fills)."""
+    M, N, K = 256, 384, 1024
+    say(f"sgemm kwave128 graph replay {M}x{N}x{K}")
+    dA, dB, dC, dD = gpu.DeviceArray((M, K)), gpu.DeviceArray((K, N)), gpu.DeviceArray((M, N)), gpu.DeviceArray((M, N))
+    st = gpu.Stream()
+    with gpu.Graph(st) as g:
+        gpu.call("sgpu_sgemm_kwave128", dA.ptr, dB.ptr, dC.ptr, M, N, K, st.h)
+    for rep in range(4):
+        rng = np.random.default_rng(700 + rep)
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        B = rng.standard_normal((K, N)).astype(np.float32)
+        gpu.call("sgpu_memcpy_htod", dA.ptr, A.ctypes.data, A.nbytes)
+        gpu.call("sgpu_memcpy_htod", dB.ptr, B.ctypes.data, B.nbytes)
+        gpu.call("sgpu_sgemm_kwave128", dA.ptr, dB.ptr, dD.ptr, M, N, K, st.h)
+        st.synchronize()
+        dC.fill_bytes(0xFF)
+        g.launch()
+        st.synchronize()
+        assert np.array_equal(dC.to_host().view(np.uint32), dD.to_host().view(np.uint32)), rep
+        ref = A.astype(np.float64) @ B.astype(np.float64)
+        assert np.abs(dC.to_host() - ref).max() / np.abs(ref).max() <= NORMWISE_TOL
+    g.close()
+    st.close()
+
+
 def test_kwave128_rejects_other_shapes(gpu):
     """Shapes sgemm_kwave128 does not take (including a 128-row A panel or a 16-row B slice of
     2^31 bytes), and operands off 16-byte alignment, are refused before any launch; M or N = 0
