@@ -146,3 +146,16 @@ def test_plan_rejects():
     assert plan(4, 4, -1, 256) == (None, -1)
     assert plan(4, 4, 4, 0) == (None, -1)
     assert sgpu.lib().sgpu_sgemm_opt_plan(64, 64, 64, 256, None) is not None
+
+
+def test_bench_traffic_record_covers_the_4096_member():
+    """bench.py reports the HBM traffic of the member sgpu_sgemm_opt launches at 4096^3 from
+    profiles/traffic.json under "<member>_4096"; a plan change that moves 4096^3 to another
+    member needs that member's PMC record, or the bench line's roofline.traffic goes null."""
+    import json
+
+    name, _ = plan(4096, 4096, 4096, 256)
+    rec = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))
+    assert f"{name}_4096" in rec
+    assert rec[f"{name}_4096"] >= 3 * 4 * 4096 * 4096          # at least A, B and C once
+    assert "gemv_h_lm_head" in rec and "gemv_hh_lm_head" in rec
